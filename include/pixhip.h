@@ -1,0 +1,182 @@
+/* pixhip: MI355X (gfx950) backend for Pixelina's quantized linear layer.
+ *
+ * A C ABI (plain pointers and sizes) over hand-written HIP kernels:
+ *   - activation block quantizers (Q8_0, Q8_K),
+ *   - the Q5_K / Q6_K / Q8_0 integer GEMM on int8 MFMA (M > 1),
+ *   - the bandwidth-bound M = 1 matvec (decode).
+ * Each entry point names the reference interface it replaces (paths relative
+ * to the reference tree).  Every function returns PIXHIP_OK (0) or a negative
+ * PIXHIP_ERR_* code and never throws; pixhip_last_error() describes the last
+ * failure on the calling thread.  Work is enqueued in order on the session's
+ * stream; results are visible to the host after pixhip_synchronize(), as in
+ * the Vulkan backend (src/backend_vulkan.cpp:984-987).
+ *
+ * Type ids are GGML's, as in src/model_types.h:10-21: Q8_0 = 8, Q5_K = 13,
+ * Q6_K = 14.  Weights are row-major [rows][inner] GGUF blocks (row stride
+ * weight_bytes({inner}, type), src/model.cpp:87-121); activations fp32
+ * [columns][inner]; outputs fp32 [columns][rows] (src/kernels_quant.cpp:396).
+ */
+#ifndef PIXHIP_H
+#define PIXHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PIXHIP_OK 0
+#define PIXHIP_ERR_ARGUMENT (-1)    /* bad pointer, size or shape (cpu_quant_matmul's `return false`, src/kernels_quant.cpp:373-377) */
+#define PIXHIP_ERR_UNSUPPORTED (-2) /* weight type other than Q8_0 / Q5_K / Q6_K */
+#define PIXHIP_ERR_MEMORY (-3)      /* device allocation failed or exceeds the budget (src/backend_vulkan.cpp:689, :718-720) */
+#define PIXHIP_ERR_DEVICE (-4)      /* HIP runtime failure: no device, launch or synchronisation error */
+#define PIXHIP_ERR_STATE (-5)       /* missing session */
+
+#define PIXHIP_TYPE_Q8_0 8
+#define PIXHIP_TYPE_Q5_K 13
+#define PIXHIP_TYPE_Q6_K 14
+
+#define PIXHIP_STAGE_QUANTIZE 1u    /* pixhip_matmul_stage: quantize the activations into session scratch */
+#define PIXHIP_STAGE_MULTIPLY 2u    /* pixhip_matmul_stage: multiply the last quantized activations */
+
+typedef struct pixhip_session pixhip_session;
+typedef struct pixhip_weight pixhip_weight;
+
+/* ---- session: VulkanSession / VulkanState (src/backend_vulkan.h:124-137) ---- */
+
+/* VulkanSession::initialize (src/backend_vulkan.cpp:1004-1011): selects HIP
+ * device `device`, creates a default-priority stream, the allocator and the
+ * weight cache. */
+int pixhip_session_create(int device, pixhip_session** out);
+
+/* VulkanSession::~VulkanSession (src/backend_vulkan.cpp:1013-1016):
+ * synchronises, then releases every allocation, cached weight and stream. */
+void pixhip_session_destroy(pixhip_session* session);
+
+/* No Vulkan counterpart (the Vulkan backend owns its queue): run the session
+ * on a caller-owned hipStream_t instead of its own (NULL restores its own). */
+int pixhip_session_set_stream(pixhip_session* session, void* stream);
+void* pixhip_session_stream(pixhip_session* session);
+
+/* VulkanSession::device_name (src/backend_vulkan.cpp:1018-1021). */
+int pixhip_device_name(pixhip_session* session, char* buffer, size_t length);
+
+/* VulkanSession::memory_limits (src/backend_vulkan.cpp:1029-1045): usable
+ * device bytes and the largest single allocation. */
+int pixhip_memory_limits(pixhip_session* session, uint64_t* bytes, uint64_t* range);
+
+/* VulkanSession::prepare_stage (src/backend_vulkan.cpp:1047-1057): flush the
+ * weight cache and size its budget so `activation_bytes + scratch_bytes`
+ * stay available.  The budget is also capped by pixhip_set_weight_budget. */
+int pixhip_prepare_stage(pixhip_session* session, uint64_t activation_bytes, uint64_t scratch_bytes);
+
+/* VulkanSession::packed_weight_budget (src/backend_vulkan.h:136). */
+int pixhip_set_weight_budget(pixhip_session* session, uint64_t bytes);
+
+/* ---- memory: vulkan_allocate / vulkan_free / vulkan_synchronize (src/backend_vulkan.h:83-85) ---- */
+
+/* vulkan_allocate (src/backend_vulkan.cpp:994-997 -> VulkanState::allocate
+ * :683-733): device memory with reuse of freed blocks up to twice the request;
+ * NULL on failure. */
+void* pixhip_allocate(pixhip_session* session, size_t bytes);
+
+/* vulkan_free (src/backend_vulkan.cpp:999-1002 -> VulkanState::release
+ * :525-531): returns the block to the session pool after queued work. */
+void pixhip_free(pixhip_session* session, void* pointer);
+
+/* vulkan_synchronize (src/backend_vulkan.cpp:984-987). */
+int pixhip_synchronize(pixhip_session* session);
+
+/* Host <-> device copies on the session stream (the Vulkan backend's
+ * host-coherent mappings make these implicit, src/backend_vulkan.h:87-122). */
+int pixhip_copy_to_device(pixhip_session* session, void* device_dst, const void* host_src, size_t bytes);
+int pixhip_copy_to_host(pixhip_session* session, void* host_dst, const void* device_src, size_t bytes);
+
+/* ---- weights: VulkanState::weight (src/backend_vulkan.cpp:742-758) ---- */
+
+/* Looks `key` up in the session's LRU weight cache (the reference keys it
+ * "file:name:offset:bytes"); on a miss copies `bytes` host bytes of GGUF
+ * blocks [rows][inner] of `type` to the device and converts them into the
+ * resident layouts the kernels read.  The handle stays valid until the entry
+ * is evicted (pixhip_prepare_stage, budget pressure) or the session ends. */
+int pixhip_weight_get(pixhip_session* session, const char* key, const void* host_bytes, uint64_t bytes, uint32_t type,
+                      uint64_t inner, uint64_t rows, pixhip_weight** out);
+
+/* Number of cached weights and their resident bytes. */
+int pixhip_weight_cache_info(pixhip_session* session, uint64_t* entries, uint64_t* bytes);
+
+/* ---- the op: vulkan_matmul / VulkanState::multiply ---- */
+
+/* vulkan_matmul (src/backend_vulkan.h:139, src/backend_vulkan.cpp:1083-1094):
+ * output[c][r] = sum_k W[r][k] * input[c][k] for c < columns, r < rows, with
+ * the numerics of cpu_quant_matmul (src/kernels_quant.cpp:369-412): the
+ * activations are quantized (Q8_0 for Q8_0 weights, Q8_K for K-quants) and
+ * every block dot is exact in integers.  columns == 1 runs the matvec,
+ * columns > 1 the MFMA GEMM (src/backend_vulkan.cpp:963-981).  `input` and
+ * `output` may be device pointers (from pixhip_allocate or any HIP
+ * allocation) or host pointers; host buffers are staged through the device
+ * and the call then completes before returning.  Every output element is
+ * written. */
+int pixhip_matmul(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t columns, float* output);
+
+/* VulkanState::multiply with the push words the convolution path uses
+ * (src/backend_vulkan.cpp:1085-1091, :1186-1191): bias[rows] added when not
+ * NULL (push[8]), output row stride `ldy` (push[6], 0 means rows) and element
+ * offset `y_offset` (push[7]).  Device pointers only. */
+int pixhip_matmul_ex(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t columns, float* output,
+                     const float* bias, size_t ldy, size_t y_offset);
+
+/* The two passes of pixhip_matmul_ex run separately (PIXHIP_STAGE_* flags),
+ * for callers that reuse one quantized activation with several weights of the
+ * same type and inner size, and to time the GEMM alone.  MULTIPLY without a
+ * preceding QUANTIZE of a compatible shape returns PIXHIP_ERR_STATE. */
+int pixhip_matmul_stage(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t columns, float* output,
+                        const float* bias, size_t ldy, size_t y_offset, unsigned stages);
+
+/* cpu_quant_matmul (src/kernels_quant.cpp:369-412) with the same argument
+ * meaning: host GGUF weight bytes (cached on the device keyed by their
+ * address, size, type and shape), input [columns][inner], output
+ * [columns][rows].  Same failures: unsupported type, a zero size,
+ * inner % block != 0 or inner > INT32_MAX give an error and touch nothing. */
+int pixhip_quant_matmul(pixhip_session* session, const unsigned char* weights, uint32_t type, const float* input, float* output,
+                        size_t rows, size_t columns, size_t inner);
+
+/* ---- activation quantizers ---- */
+
+/* quantize_row_q8_0_ref (src/kernels_quant.cpp:120-144) applied to `rows`
+ * rows of `inner` fp32 values: writes rows*inner/32 block_q8_0 (34 B) to
+ * `blocks`.  Device pointers. */
+int pixhip_quantize_q8_0(pixhip_session* session, const float* input, void* blocks, size_t rows, size_t inner);
+
+/* quantize_row_q8_K_ref (src/kernels_quant.cpp:80-118): rows*inner/256
+ * block_q8_K (292 B: fp32 d, int8 qs[256], int16 bsums[16]).  Device pointers. */
+int pixhip_quantize_q8_K(pixhip_session* session, const float* input, void* blocks, size_t rows, size_t inner);
+
+/* ---- integer parity gate ---- */
+
+/* Runs the GEMM kernel's integer path and writes, for every (column c, row r,
+ * block b), the exact integer block sums the fp32 epilogue consumes:
+ *   Q5_K  sums = sum_s scale_s * dot_s,  mins = sum_s min_s * (bsum_2s + bsum_2s+1)
+ *         (pix_dot_q5_K's sumi and its min term, src/kernels_quant.cpp:198-245)
+ *   Q6_K  sums = sum_e scale * (q - 32) * q8 (src/kernels_quant.cpp:283-331)
+ *   Q8_0  sums = sum over the block of q * q8 (src/kernels_quant.cpp:353-360)
+ * Layout [columns][rows][blocks] with blocks = inner/256 (K-quants) or
+ * ceil(inner/64)*2 (Q8_0, the last block of an odd count is padding).
+ * `mins` is only written for Q5_K.  Device pointers. */
+int pixhip_block_sums(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t columns, int32_t* sums,
+                      int32_t* mins);
+
+/* ---- timing (HIP events on the session stream) ---- */
+int pixhip_timer_start(pixhip_session* session);
+int pixhip_timer_stop(pixhip_session* session, float* milliseconds);
+
+/* ---- diagnostics ---- */
+const char* pixhip_last_error(void);
+int pixhip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PIXHIP_H */

@@ -1,0 +1,54 @@
+/* Oracle: a plain-C restatement of Pixelina's CPU quantized linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or the timed CPU baseline) -- never as the thing measured or shipped.  The
+ * product path lives in pixelina_amd/ and fails loudly without its HIP build.
+ *
+ * Every function follows the file:line of the reference it restates (paths are
+ * relative to the reference tree).  Parity status of each function is pinned by
+ * tests/test_oracle.py against golden vectors written by the compiled
+ * reference (tests/golden/) plus closed-form / brute-force checks.
+ *
+ * Block layouts are the reference's (src/kernels_quant.cpp:14-38,
+ * src/model_types.h:10-21):
+ *   Q8_0   34 B : fp16 d, int8 qs[32]
+ *   Q8_K  292 B : fp32 d, int8 qs[256], int16 bsums[16]
+ *   Q5_K  176 B : fp16 d, fp16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
+ *   Q6_K  210 B : u8 ql[128], u8 qh[64], int8 scales[16], fp16 d
+ */
+#ifndef PIX_ORACLE_H
+#define PIX_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define ORC_Q8_0 8
+#define ORC_Q5_K 13
+#define ORC_Q6_K 14
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+float orc_half_to_float(uint16_t h);
+uint16_t orc_float_to_half(float f);
+int orc_nearest_int_fused(float scale, float x);
+void orc_quantize_q8_0(const float* x, void* blocks, int64_t k);
+void orc_quantize_q8_K(const float* x, void* blocks, int64_t k);
+float orc_dot_q8_0(int n, const void* w, const void* a);
+float orc_dot_q5_K(int n, const void* w, const void* a);
+float orc_dot_q6_K(int n, const void* w, const void* a);
+int32_t orc_block_sums_q8_0(const void* w, const void* a);
+void orc_superblock_sums_q5_K(const void* w, const void* a, int32_t* scaled, int32_t* mins);
+int32_t orc_superblock_sum_q6_K(const void* w, const void* a);
+int orc_quant_matmul(const void* w, uint32_t type, const float* x, float* y,
+                     size_t rows, size_t columns, size_t inner, int threads);
+void orc_decode(const void* data, uint32_t type, size_t count, double* out);
+uint64_t orc_row_bytes(uint64_t inner, uint32_t type);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,89 @@
+/* Test infrastructure only: C-ABI harness around the reference's own CPU
+ * quantized kernels, compiled in place from the reference sources by
+ * oracle/Makefile into oracle/_ref/libpixref.so.
+ *
+ * The reference keeps its quantizers and dot products `static` inside
+ * src/kernels_quant.cpp, so this translation unit includes that file (from the
+ * reference tree, never a copy) to reach them.  Nothing here re-implements the
+ * reference: every function forwards to the reference symbol named beside it.
+ * Used by tests/golden/make_golden.py (to write fixtures), by the tests (as a
+ * second checker when the library is present) and by bench.py's CPU-baseline
+ * leg (cpu_baseline.kind = "reference").
+ */
+#include "kernels_quant.cpp"
+
+extern "C" {
+
+/* quantize_row_q8_0_ref, src/kernels_quant.cpp:120-144 */
+void ref_quantize_q8_0(const float* x, void* blocks, int64_t k)
+{
+    quantize_row_q8_0_ref(x,static_cast<block_q8_0*>(blocks),k);
+}
+
+/* quantize_row_q8_K_ref, src/kernels_quant.cpp:80-118 */
+void ref_quantize_q8_K(const float* x, void* blocks, int64_t k)
+{
+    quantize_row_q8_K_ref(x,static_cast<block_q8_K*>(blocks),k);
+}
+
+/* pix_dot_q8_0, src/kernels_quant.cpp:339-365 */
+float ref_dot_q8_0(int n, const void* w, const void* a)
+{
+    return pix_dot_q8_0(n,static_cast<const block_q8_0*>(w),static_cast<const block_q8_0*>(a));
+}
+
+/* pix_dot_q5_K, src/kernels_quant.cpp:163-254 */
+float ref_dot_q5_K(int n, const void* w, const void* a)
+{
+    return pix_dot_q5_K(n,static_cast<const block_q5_K*>(w),static_cast<const block_q8_K*>(a));
+}
+
+/* pix_dot_q6_K, src/kernels_quant.cpp:256-337 */
+float ref_dot_q6_K(int n, const void* w, const void* a)
+{
+    return pix_dot_q6_K(n,static_cast<const block_q6_K*>(w),static_cast<const block_q8_K*>(a));
+}
+
+/* nearest_int, src/kernels_quant.cpp:41-48 */
+int ref_nearest_int(float f)
+{
+    return nearest_int(f);
+}
+
+/* cpu_quant_matmul, src/kernels_quant.cpp:369-412 (1 = true) */
+int ref_quant_matmul(const unsigned char* w, uint32_t type, const float* x, float* y,
+                     size_t rows, size_t columns, size_t inner)
+{
+    return cpu_quant_matmul(w,type,x,y,rows,columns,inner)? 1 : 0;
+}
+
+/* cpu_set_threads / cpu_thread_count, src/tensor.cpp:92-101 */
+void ref_set_threads(size_t n)
+{
+    cpu_set_threads(n);
+}
+
+size_t ref_thread_count(void)
+{
+    return cpu_thread_count();
+}
+
+/* cpu_decode, src/backend_cpu.cpp:24-101 */
+void ref_decode(const unsigned char* data, uint32_t type, size_t count, float* out)
+{
+    cpu_decode(data,type,count,out);
+}
+
+/* half_float, src/backend_cpu.cpp:12-22 */
+float ref_half_float(uint16_t h)
+{
+    return half_float(h);
+}
+
+/* weight_bytes, src/model.cpp:87-121, for a one-row shape {inner} */
+uint64_t ref_row_bytes(uint64_t inner, uint32_t type)
+{
+    return weight_bytes({inner},type);
+}
+
+}

@@ -1,0 +1,90 @@
+"""ctypes binding of libpixhip.so (include/pixhip.h) for tests and the bench.
+
+Loading fails loudly when the HIP library has not been built: there is no
+CPU fallback anywhere on the product path.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libpixhip.so")
+
+OK = 0
+ERR_ARGUMENT = -1
+ERR_UNSUPPORTED = -2
+ERR_MEMORY = -3
+ERR_DEVICE = -4
+ERR_STATE = -5
+
+Q8_0 = 8
+Q5_K = 13
+Q6_K = 14
+
+STAGE_QUANTIZE = 1
+STAGE_MULTIPLY = 2
+
+# Exported C symbols and their ctypes signatures (restype, argtypes).
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
+_int = ctypes.c_int
+SIGNATURES = {
+    "pixhip_version": (_int, []),
+    "pixhip_last_error": (ctypes.c_char_p, []),
+    "pixhip_session_create": (_int, [_int, ctypes.POINTER(_vp)]),
+    "pixhip_session_destroy": (None, [_vp]),
+    "pixhip_session_set_stream": (_int, [_vp, _vp]),
+    "pixhip_session_stream": (_vp, [_vp]),
+    "pixhip_device_name": (_int, [_vp, ctypes.c_char_p, _sz]),
+    "pixhip_memory_limits": (_int, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "pixhip_prepare_stage": (_int, [_vp, _u64, _u64]),
+    "pixhip_set_weight_budget": (_int, [_vp, _u64]),
+    "pixhip_allocate": (_vp, [_vp, _sz]),
+    "pixhip_free": (None, [_vp, _vp]),
+    "pixhip_synchronize": (_int, [_vp]),
+    "pixhip_copy_to_device": (_int, [_vp, _vp, _vp, _sz]),
+    "pixhip_copy_to_host": (_int, [_vp, _vp, _vp, _sz]),
+    "pixhip_weight_get": (_int, [_vp, ctypes.c_char_p, _vp, _u64, _u32, _u64, _u64, ctypes.POINTER(_vp)]),
+    "pixhip_weight_cache_info": (_int, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "pixhip_matmul": (_int, [_vp, _vp, _vp, _sz, _vp]),
+    "pixhip_matmul_ex": (_int, [_vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz]),
+    "pixhip_matmul_stage": (_int, [_vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz, ctypes.c_uint]),
+    "pixhip_quant_matmul": (_int, [_vp, _vp, _u32, _vp, _vp, _sz, _sz, _sz]),
+    "pixhip_quantize_q8_0": (_int, [_vp, _vp, _vp, _sz, _sz]),
+    "pixhip_quantize_q8_K": (_int, [_vp, _vp, _vp, _sz, _sz]),
+    "pixhip_block_sums": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
+    "pixhip_timer_start": (_int, [_vp]),
+    "pixhip_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
+}
+
+_lib = None
+
+
+def load():
+    """Load libpixhip.so once; raise if it is missing (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIBRARY):
+        raise RuntimeError(f"{LIBRARY} is not built: run `python -m pixelina_amd.build` (HIP is required, there is no CPU path)")
+    lib = ctypes.CDLL(LIBRARY)
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+class PixhipError(RuntimeError):
+    def __init__(self, code, what):
+        msg = load().pixhip_last_error().decode(errors="replace")
+        super().__init__(f"{what} failed ({code}): {msg}")
+        self.code = code
+
+
+def check(code, what):
+    if code != OK:
+        raise PixhipError(code, what)
+    return code

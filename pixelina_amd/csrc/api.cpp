@@ -1,0 +1,760 @@
+// C ABI of the HIP backend (include/pixhip.h): session, pooled device
+// allocator, LRU weight cache with upload-time conversion, and the dispatch of
+// VulkanState::multiply (src/backend_vulkan.cpp:963-981): M == 1 -> matvec,
+// M > 1 -> activation quantize + MFMA GEMM.  Nothing here throws; every HIP
+// status is checked and turned into a PIXHIP_ERR_* code.
+#include "pixhip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <new>
+#include <string>
+#include <unordered_map>
+
+#include "pixhip_internal.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& message)
+{
+    g_error = message;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    return fail(PIXHIP_ERR_DEVICE,std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define PIX_HIP(expr, what)                               \
+    do {                                                  \
+        hipError_t e_ = (expr);                           \
+        if (e_ != hipSuccess) return hip_fail(e_,what);   \
+    } while (0)
+
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+constexpr size_t kTile = 128;        // GEMM tile rows (token and feature padding)
+constexpr size_t kAlign = 256;       // sub-allocation alignment
+constexpr double kHeapFraction = 0.85;  // VULKAN_HEAP_FRACTION, src/backend_vulkan.h:26
+constexpr size_t kMatvecMaxInner = 16384;  // matvec keeps x in LDS (64 units per lane x 4)
+
+bool supported_type(uint32_t t) { return t == PIX_Q8_0 || t == PIX_Q5_K || t == PIX_Q6_K; }
+size_t block_values(uint32_t t) { return t == PIX_Q8_0? PIX_QK8 : PIX_QK; }
+size_t block_bytes(uint32_t t) { return t == PIX_Q8_0? PIX_Q8_0_BYTES : (t == PIX_Q5_K? PIX_Q5_K_BYTES : PIX_Q6_K_BYTES); }
+
+// Carves one device allocation into aligned sub-buffers.
+struct Carver {
+    size_t offset = 0;
+    size_t take(size_t bytes)
+    {
+        size_t at = offset;
+        offset = round_up(offset + bytes,kAlign);
+        return at;
+    }
+};
+
+}  // namespace
+
+struct pixhip_weight {
+    std::string key;
+    uint32_t type = 0;
+    uint64_t inner = 0, rows = 0, gguf_bytes = 0;
+    void* raw = nullptr;        // GGUF bytes (Q5_K matvec input; source of the other forms)
+    void* planes = nullptr;     // Q5_K / Q6_K GEMM planes
+    void* planar = nullptr;     // Q8_0 planar (GEMM + matvec) or Q6_K planar (matvec)
+    pixhip::PlanesQ5K q5{};
+    pixhip::PlanesQ6K q6{};
+    pixhip::PlanarQ80 q80{};
+    pixhip::PlanarQ6K q6p{};
+    size_t resident = 0;
+    uint64_t used = 0;
+};
+
+struct pixhip_session {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    std::string name;
+    size_t total_memory = 0;
+    size_t heap_limit = 0;
+    // allocator (VulkanState::allocate / release / trim)
+    std::map<uintptr_t,size_t> live;
+    std::multimap<size_t,void*> pool;
+    size_t pooled_bytes = 0;
+    // weight cache (VulkanState::weight / evict)
+    std::unordered_map<std::string,pixhip_weight*> weights;
+    size_t cache_bytes = 0, cache_limit = 0, budget = SIZE_MAX;
+    uint64_t uses = 0;
+    // quantized-activation scratch
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    // staging for host or misaligned pointers
+    void* stage = nullptr;
+    size_t stage_bytes = 0;
+    // activations left by the last QUANTIZE stage
+    int act_kind = 0;  // 0 none, 1 Q8_K, 2 Q8_0
+    size_t act_columns = 0, act_inner = 0;
+    pixhip::Act8K a8k{};
+    pixhip::Act80 a80{};
+};
+
+namespace {
+
+int use_device(pixhip_session* s)
+{
+    if (!s) return fail(PIXHIP_ERR_STATE,"no session");
+    PIX_HIP(hipSetDevice(s->device),"hipSetDevice");
+    return PIXHIP_OK;
+}
+
+void release_weight(pixhip_session* s, pixhip_weight* w)
+{
+    if (w->raw) (void)hipFree(w->raw);
+    if (w->planes) (void)hipFree(w->planes);
+    if (w->planar) (void)hipFree(w->planar);
+    s->cache_bytes -= w->resident;
+    delete w;
+}
+
+// VulkanState::evict (src/backend_vulkan.cpp:671-681): least recently used first.
+bool evict_one(pixhip_session* s, const pixhip_weight* keep)
+{
+    auto victim = s->weights.end();
+    for (auto it = s->weights.begin(); it != s->weights.end(); ++it) {
+        if (it->second == keep) continue;
+        if (victim == s->weights.end() || it->second->used < victim->second->used) victim = it;
+    }
+    if (victim == s->weights.end()) return false;
+    (void)hipStreamSynchronize(s->stream);
+    pixhip_weight* w = victim->second;
+    s->weights.erase(victim);
+    release_weight(s,w);
+    return true;
+}
+
+void trim_pool(pixhip_session* s)
+{
+    for (auto& e : s->pool) (void)hipFree(e.second);
+    s->pool.clear();
+    s->pooled_bytes = 0;
+}
+
+// Device allocation for cache forms: evicts older weights, then trims the
+// pool, when the budget or the device refuses.
+int weight_alloc(pixhip_session* s, pixhip_weight* w, size_t bytes, void** out)
+{
+    while (s->cache_bytes + bytes > s->cache_limit && evict_one(s,w)) {}
+    if (s->cache_bytes + bytes > s->cache_limit)
+        return fail(PIXHIP_ERR_MEMORY,"weight exceeds the cache budget (" + std::to_string(s->cache_limit) + " bytes)");
+    hipError_t e = hipMalloc(out,bytes);
+    while (e != hipSuccess && (evict_one(s,w) || s->pooled_bytes)) {
+        (void)hipGetLastError();
+        if (s->pooled_bytes) trim_pool(s);
+        e = hipMalloc(out,bytes);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *out = nullptr;
+        return fail(PIXHIP_ERR_MEMORY,"hipMalloc of " + std::to_string(bytes) + " weight bytes failed");
+    }
+    w->resident += bytes;
+    s->cache_bytes += bytes;
+    return PIXHIP_OK;
+}
+
+int grow(pixhip_session* s, void** buffer, size_t* have, size_t need)
+{
+    if (*have >= need) return PIXHIP_OK;
+    PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
+    if (*buffer) (void)hipFree(*buffer);
+    *buffer = nullptr;
+    *have = 0;
+    hipError_t e = hipMalloc(buffer,need);
+    if (e != hipSuccess && s->pooled_bytes) {
+        (void)hipGetLastError();
+        trim_pool(s);
+        e = hipMalloc(buffer,need);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *buffer = nullptr;
+        return fail(PIXHIP_ERR_MEMORY,"hipMalloc of " + std::to_string(need) + " scratch bytes failed");
+    }
+    *have = need;
+    return PIXHIP_OK;
+}
+
+// GEMM forms, built on first use from the resident GGUF bytes.
+int ensure_gemm_form(pixhip_session* s, pixhip_weight* w)
+{
+    const size_t N = w->rows, K = w->inner, npad = round_up(N,kTile), nb = K / PIX_QK;
+    if (w->type == PIX_Q5_K && !w->planes) {
+        Carver c;
+        size_t hi = c.take(npad * K), lo = c.take(npad * K), d = c.take(N * nb * 4), dm = c.take(N * nb * 4),
+               mn = c.take(npad * (K / 16) * 2);
+        int rc = weight_alloc(s,w,c.offset,&w->planes);
+        if (rc) return rc;
+        uint8_t* base = static_cast<uint8_t*>(w->planes);
+        PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");
+        w->q5 = {reinterpret_cast<int8_t*>(base + hi),reinterpret_cast<int8_t*>(base + lo),reinterpret_cast<float*>(base + d),
+                 reinterpret_cast<float*>(base + dm),reinterpret_cast<_Float16*>(base + mn)};
+        PIX_HIP(pixhip::launch_repack_q5_K(static_cast<const uint8_t*>(w->raw),N,K,const_cast<int8_t*>(w->q5.hi),
+                                           const_cast<int8_t*>(w->q5.lo),const_cast<float*>(w->q5.d),const_cast<float*>(w->q5.dm),
+                                           const_cast<_Float16*>(w->q5.mn),s->stream),
+                "repack Q5_K");
+    }
+    if (w->type == PIX_Q6_K && !w->planes) {
+        Carver c;
+        size_t hi = c.take(npad * K), lo = c.take(npad * K), d = c.take(N * nb * 4);
+        int rc = weight_alloc(s,w,c.offset,&w->planes);
+        if (rc) return rc;
+        uint8_t* base = static_cast<uint8_t*>(w->planes);
+        PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");
+        w->q6 = {reinterpret_cast<int8_t*>(base + hi),reinterpret_cast<int8_t*>(base + lo),reinterpret_cast<float*>(base + d)};
+        PIX_HIP(pixhip::launch_repack_q6_K_planes(static_cast<const uint8_t*>(w->raw),N,K,const_cast<int8_t*>(w->q6.hi),
+                                                  const_cast<int8_t*>(w->q6.lo),const_cast<float*>(w->q6.d),s->stream),
+                "repack Q6_K planes");
+    }
+    return PIXHIP_OK;
+}
+
+int ensure_matvec_form(pixhip_session* s, pixhip_weight* w)
+{
+    if (w->type != PIX_Q6_K || w->planar) return PIXHIP_OK;
+    const size_t N = w->rows, K = w->inner, nb = K / PIX_QK;
+    Carver c;
+    size_t ql = c.take(N * K / 2), qh = c.take(N * K / 4), sc = c.take(N * K / 16), d = c.take(N * nb * 2);
+    int rc = weight_alloc(s,w,c.offset,&w->planar);
+    if (rc) return rc;
+    uint8_t* base = static_cast<uint8_t*>(w->planar);
+    w->q6p = {base + ql,base + qh,reinterpret_cast<int8_t*>(base + sc),reinterpret_cast<_Float16*>(base + d)};
+    PIX_HIP(pixhip::launch_repack_q6_K_planar(static_cast<const uint8_t*>(w->raw),N,K,const_cast<uint8_t*>(w->q6p.ql),
+                                              const_cast<uint8_t*>(w->q6p.qh),const_cast<int8_t*>(w->q6p.sc),
+                                              const_cast<_Float16*>(w->q6p.d),s->stream),
+            "repack Q6_K planar");
+    return PIXHIP_OK;
+}
+
+int build_q8_0(pixhip_session* s, pixhip_weight* w)
+{
+    const size_t N = w->rows, K = w->inner, npad = round_up(N,kTile), kp = round_up(K,64);
+    Carver c;
+    size_t qs = c.take(npad * kp), d = c.take(N * (kp / PIX_QK8) * 2), dT = c.take((kp / PIX_QK8) * npad * 4);
+    int rc = weight_alloc(s,w,c.offset,&w->planar);
+    if (rc) return rc;
+    uint8_t* base = static_cast<uint8_t*>(w->planar);
+    PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");
+    w->q80 = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<_Float16*>(base + d),reinterpret_cast<float*>(base + dT)};
+    PIX_HIP(pixhip::launch_repack_q8_0(static_cast<const uint8_t*>(w->raw),N,K,kp,npad,const_cast<int8_t*>(w->q80.qs),
+                                       const_cast<_Float16*>(w->q80.d),const_cast<float*>(w->q80.dT),s->stream),
+            "repack Q8_0");
+    return PIXHIP_OK;
+}
+
+int check_shape(uint32_t type, uint64_t inner, uint64_t rows)
+{
+    if (!supported_type(type)) return fail(PIXHIP_ERR_UNSUPPORTED,"unsupported weight type " + std::to_string(type));
+    if (!inner || !rows || inner % block_values(type) || inner > INT32_MAX || rows > INT32_MAX)
+        return fail(PIXHIP_ERR_ARGUMENT,"bad weight shape inner=" + std::to_string(inner) + " rows=" + std::to_string(rows));
+    return PIXHIP_OK;
+}
+
+// Resolve a caller pointer to one the kernels may dereference: our own
+// allocations and HIP device / managed memory pass through; host memory
+// (pageable or pinned) is staged through HBM once instead of being re-read
+// over PCIe by every tile.
+bool device_visible(pixhip_session* s, const void* p, const void** dev)
+{
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    auto it = s->live.upper_bound(a);
+    if (it != s->live.begin()) {
+        --it;
+        if (a < it->first + it->second) {
+            *dev = p;
+            return true;
+        }
+    }
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr,p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) {
+        *dev = attr.devicePointer? attr.devicePointer : p;
+        return true;
+    }
+    return false;
+}
+
+int quantize_stage(pixhip_session* s, const pixhip_weight* w, const float* x, size_t columns)
+{
+    const size_t K = w->inner, mpad = round_up(columns,kTile);
+    if (w->type == PIX_Q8_0) {
+        const size_t kp = round_up(K,64);
+        Carver c;
+        size_t qs = c.take(mpad * kp), d = c.take((kp / PIX_QK8) * mpad * 4);
+        int rc = grow(s,&s->scratch,&s->scratch_bytes,c.offset);
+        if (rc) return rc;
+        uint8_t* base = static_cast<uint8_t*>(s->scratch);
+        s->a80 = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<float*>(base + d),mpad};
+        PIX_HIP(pixhip::launch_quantize_q8_0(x,columns,K,kp,s->a80,nullptr,s->stream),"quantize Q8_0");
+        s->act_kind = 2;
+    } else {
+        Carver c;
+        size_t qs = c.take(mpad * K), d = c.take((K / PIX_QK) * mpad * 4), bs = c.take(mpad * (K / 16) * 2);
+        int rc = grow(s,&s->scratch,&s->scratch_bytes,c.offset);
+        if (rc) return rc;
+        uint8_t* base = static_cast<uint8_t*>(s->scratch);
+        s->a8k = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<float*>(base + d),reinterpret_cast<_Float16*>(base + bs),mpad};
+        PIX_HIP(pixhip::launch_quantize_q8_K(x,columns,K,s->a8k,nullptr,s->stream),"quantize Q8_K");
+        s->act_kind = 1;
+    }
+    s->act_columns = columns;
+    s->act_inner = K;
+    return PIXHIP_OK;
+}
+
+int multiply_stage(pixhip_session* s, pixhip_weight* w, size_t columns, const pixhip::Output& out)
+{
+    const int kind = w->type == PIX_Q8_0? 2 : 1;
+    if (s->act_kind != kind || s->act_columns != columns || s->act_inner != w->inner)
+        return fail(PIXHIP_ERR_STATE,"no quantized activations of this shape: run the QUANTIZE stage first");
+    int rc = ensure_gemm_form(s,w);
+    if (rc) return rc;
+    hipError_t e;
+    if (w->type == PIX_Q5_K) e = pixhip::launch_gemm_q5_K(s->a8k,w->q5,columns,w->rows,w->inner,out,s->stream);
+    else if (w->type == PIX_Q6_K) e = pixhip::launch_gemm_q6_K(s->a8k,w->q6,columns,w->rows,w->inner,out,s->stream);
+    else e = pixhip::launch_gemm_q8_0(s->a80,w->q80,columns,w->rows,w->inner,out,s->stream);
+    PIX_HIP(e,"GEMM launch");
+    return PIXHIP_OK;
+}
+
+bool matvec_ok(const pixhip_weight* w)
+{
+    return w->inner <= kMatvecMaxInner;
+}
+
+int matvec(pixhip_session* s, pixhip_weight* w, const float* x, const pixhip::Output& out)
+{
+    hipError_t e;
+    if (w->type == PIX_Q5_K) {
+        e = pixhip::launch_matvec_q5_K(static_cast<const uint8_t*>(w->raw),x,w->rows,w->inner,out,s->stream);
+    } else if (w->type == PIX_Q8_0) {
+        e = pixhip::launch_matvec_q8_0(w->q80,x,w->rows,w->inner,out,s->stream);
+    } else {
+        int rc = ensure_matvec_form(s,w);
+        if (rc) return rc;
+        e = pixhip::launch_matvec_q6_K(w->q6p,x,w->rows,w->inner,out,s->stream);
+    }
+    PIX_HIP(e,"matvec launch");
+    return PIXHIP_OK;
+}
+
+int run(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t columns, float* output, const float* bias,
+        size_t ldy, size_t y_offset, unsigned stages, bool allow_host)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    pixhip_weight* w = const_cast<pixhip_weight*>(wc);
+    if (!w) return fail(PIXHIP_ERR_ARGUMENT,"null weight handle");
+    if (!columns || (stages & PIXHIP_STAGE_MULTIPLY && !output) || (stages & PIXHIP_STAGE_QUANTIZE && !input))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or zero columns");
+    if (!stages || stages > (PIXHIP_STAGE_QUANTIZE | PIXHIP_STAGE_MULTIPLY)) return fail(PIXHIP_ERR_ARGUMENT,"bad stage flags");
+    if (!ldy) ldy = w->rows;
+    if (ldy < w->rows) return fail(PIXHIP_ERR_ARGUMENT,"output stride smaller than rows");
+    w->used = ++s->uses;
+    const size_t K = w->inner;
+    const size_t in_bytes = columns * K * sizeof(float);
+    const size_t out_elems = y_offset + (columns - 1) * ldy + w->rows;
+
+    // Resolve pointers; stage host or misaligned inputs and host outputs.
+    const void* xin = nullptr;
+    void* yout = nullptr;
+    bool stage_in = false, stage_out = false;
+    if (stages & PIXHIP_STAGE_QUANTIZE) {
+        if (!device_visible(s,input,&xin)) {
+            if (!allow_host) return fail(PIXHIP_ERR_ARGUMENT,"input is not device memory");
+            stage_in = true;
+        } else if (reinterpret_cast<uintptr_t>(xin) % 16) {
+            stage_in = true;
+        }
+    }
+    if (stages & PIXHIP_STAGE_MULTIPLY) {
+        const void* yv = nullptr;
+        if (!device_visible(s,output,&yv)) {
+            if (!allow_host) return fail(PIXHIP_ERR_ARGUMENT,"output is not device memory");
+            stage_out = true;
+        } else {
+            yout = const_cast<void*>(yv);
+        }
+    }
+    const size_t in_region = stage_in? round_up(in_bytes,kAlign) : 0;
+    if (stage_in || stage_out) {
+        rc = grow(s,&s->stage,&s->stage_bytes,in_region + (stage_out? out_elems * sizeof(float) : 0));
+        if (rc) return rc;
+    }
+    if (stage_in) {
+        uint8_t* dst = static_cast<uint8_t*>(s->stage);
+        if (xin) PIX_HIP(hipMemcpyAsync(dst,xin,in_bytes,hipMemcpyDeviceToDevice,s->stream),"stage input");
+        else PIX_HIP(hipMemcpyAsync(dst,input,in_bytes,hipMemcpyHostToDevice,s->stream),"stage input");
+        xin = dst;
+    }
+    if (stage_out) {
+        yout = static_cast<uint8_t*>(s->stage) + in_region;
+        if (ldy != w->rows || y_offset)  // preserve the untouched gaps of a strided host output
+            PIX_HIP(hipMemcpyAsync(yout,output,out_elems * sizeof(float),hipMemcpyHostToDevice,s->stream),"stage output");
+    }
+    const pixhip::Output out = {static_cast<float*>(yout),bias,ldy,y_offset};
+    const float* x = static_cast<const float*>(xin);
+
+    if (columns == 1 && stages == (PIXHIP_STAGE_QUANTIZE | PIXHIP_STAGE_MULTIPLY) && matvec_ok(w)) {
+        rc = matvec(s,w,x,out);
+    } else {
+        rc = PIXHIP_OK;
+        if (stages & PIXHIP_STAGE_QUANTIZE) rc = quantize_stage(s,w,x,columns);
+        if (!rc && (stages & PIXHIP_STAGE_MULTIPLY)) rc = multiply_stage(s,w,columns,out);
+    }
+    if (rc) return rc;
+    if (stage_out) {
+        PIX_HIP(hipMemcpyAsync(output,yout,out_elems * sizeof(float),hipMemcpyDeviceToHost,s->stream),"copy output");
+    }
+    if (stage_in || stage_out) PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
+    return PIXHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pixhip_version(void) { return 100; }
+
+const char* pixhip_last_error(void) { return g_error.c_str(); }
+
+int pixhip_session_create(int device, pixhip_session** out)
+{
+    if (!out) return fail(PIXHIP_ERR_ARGUMENT,"null output");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return fail(PIXHIP_ERR_DEVICE,"no HIP device available");
+    }
+    if (device < 0 || device >= count) return fail(PIXHIP_ERR_ARGUMENT,"device index out of range");
+    PIX_HIP(hipSetDevice(device),"hipSetDevice");
+    pixhip_session* s = new (std::nothrow) pixhip_session();
+    if (!s) return fail(PIXHIP_ERR_MEMORY,"host allocation failed");
+    s->device = device;
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop,device)) != hipSuccess || (e = hipStreamCreate(&s->own_stream)) != hipSuccess ||
+        (e = hipEventCreate(&s->t0)) != hipSuccess || (e = hipEventCreate(&s->t1)) != hipSuccess) {
+        int rc = hip_fail(e,"session setup");
+        pixhip_session_destroy(s);
+        return rc;
+    }
+    s->stream = s->own_stream;
+    s->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    s->total_memory = prop.totalGlobalMem;
+    s->heap_limit = (size_t)(kHeapFraction * (double)prop.totalGlobalMem);
+    s->cache_limit = s->heap_limit;
+    *out = s;
+    return PIXHIP_OK;
+}
+
+void pixhip_session_destroy(pixhip_session* s)
+{
+    if (!s) return;
+    (void)hipSetDevice(s->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    for (auto& e : s->weights) release_weight(s,e.second);
+    s->weights.clear();
+    trim_pool(s);
+    for (auto& e : s->live) (void)hipFree(reinterpret_cast<void*>(e.first));
+    if (s->scratch) (void)hipFree(s->scratch);
+    if (s->stage) (void)hipFree(s->stage);
+    if (s->t0) (void)hipEventDestroy(s->t0);
+    if (s->t1) (void)hipEventDestroy(s->t1);
+    if (s->own_stream) (void)hipStreamDestroy(s->own_stream);
+    delete s;
+}
+
+int pixhip_session_set_stream(pixhip_session* s, void* stream)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
+    s->stream = stream? static_cast<hipStream_t>(stream) : s->own_stream;
+    return PIXHIP_OK;
+}
+
+void* pixhip_session_stream(pixhip_session* s) { return s? static_cast<void*>(s->stream) : nullptr; }
+
+int pixhip_device_name(pixhip_session* s, char* buffer, size_t length)
+{
+    if (!s) return fail(PIXHIP_ERR_STATE,"no session");
+    if (!buffer || !length) return fail(PIXHIP_ERR_ARGUMENT,"empty buffer");
+    std::strncpy(buffer,s->name.c_str(),length - 1);
+    buffer[length - 1] = 0;
+    return PIXHIP_OK;
+}
+
+int pixhip_memory_limits(pixhip_session* s, uint64_t* bytes, uint64_t* range)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    size_t free_b = 0, total_b = 0;
+    PIX_HIP(hipMemGetInfo(&free_b,&total_b),"hipMemGetInfo");
+    if (bytes) *bytes = std::min<uint64_t>(s->heap_limit,free_b);
+    if (range) *range = total_b;
+    return PIXHIP_OK;
+}
+
+int pixhip_prepare_stage(pixhip_session* s, uint64_t activation_bytes, uint64_t scratch_bytes)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (activation_bytes > s->heap_limit || scratch_bytes > s->heap_limit - activation_bytes)
+        return fail(PIXHIP_ERR_MEMORY,"stage does not fit the device heap");
+    PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
+    for (auto& e : s->weights) release_weight(s,e.second);
+    s->weights.clear();
+    trim_pool(s);
+    size_t held = s->scratch_bytes + s->stage_bytes;
+    for (auto& e : s->live) held += e.second;
+    const uint64_t reserve = std::max<uint64_t>(held,activation_bytes + scratch_bytes);
+    if (reserve >= s->heap_limit) return fail(PIXHIP_ERR_MEMORY,"no room left for weights");
+    s->cache_limit = (size_t)std::min<uint64_t>(s->budget,s->heap_limit - reserve);
+    return s->cache_limit? PIXHIP_OK : fail(PIXHIP_ERR_MEMORY,"empty weight budget");
+}
+
+int pixhip_set_weight_budget(pixhip_session* s, uint64_t bytes)
+{
+    if (!s) return fail(PIXHIP_ERR_STATE,"no session");
+    s->budget = (size_t)std::min<uint64_t>(bytes,SIZE_MAX);
+    s->cache_limit = std::min(s->cache_limit,s->budget);
+    return PIXHIP_OK;
+}
+
+void* pixhip_allocate(pixhip_session* s, size_t bytes)
+{
+    if (use_device(s)) return nullptr;
+    bytes = round_up(bytes? bytes : 4,kAlign);
+    auto hit = s->pool.lower_bound(bytes);
+    if (hit != s->pool.end() && hit->first <= 2 * bytes) {
+        void* p = hit->second;
+        s->live.emplace(reinterpret_cast<uintptr_t>(p),hit->first);
+        s->pooled_bytes -= hit->first;
+        s->pool.erase(hit);
+        return p;
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p,bytes);
+    if (e != hipSuccess && s->pooled_bytes) {
+        (void)hipGetLastError();
+        (void)hipStreamSynchronize(s->stream);
+        trim_pool(s);
+        e = hipMalloc(&p,bytes);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        fail(PIXHIP_ERR_MEMORY,"hipMalloc of " + std::to_string(bytes) + " bytes failed");
+        return nullptr;
+    }
+    s->live.emplace(reinterpret_cast<uintptr_t>(p),bytes);
+    return p;
+}
+
+void pixhip_free(pixhip_session* s, void* p)
+{
+    if (!s || !p) return;
+    auto it = s->live.find(reinterpret_cast<uintptr_t>(p));
+    if (it == s->live.end()) return;
+    // Work already queued on the session stream finishes before anything that
+    // reuses the block is queued behind it.
+    s->pool.emplace(it->second,p);
+    s->pooled_bytes += it->second;
+    s->live.erase(it);
+}
+
+int pixhip_synchronize(pixhip_session* s)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
+    return PIXHIP_OK;
+}
+
+int pixhip_copy_to_device(pixhip_session* s, void* dst, const void* src, size_t bytes)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!bytes) return PIXHIP_OK;
+    if (!dst || !src) return fail(PIXHIP_ERR_ARGUMENT,"null pointer");
+    PIX_HIP(hipMemcpyAsync(dst,src,bytes,hipMemcpyHostToDevice,s->stream),"hipMemcpyAsync");
+    PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
+    return PIXHIP_OK;
+}
+
+int pixhip_copy_to_host(pixhip_session* s, void* dst, const void* src, size_t bytes)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!bytes) return PIXHIP_OK;
+    if (!dst || !src) return fail(PIXHIP_ERR_ARGUMENT,"null pointer");
+    PIX_HIP(hipMemcpyAsync(dst,src,bytes,hipMemcpyDeviceToHost,s->stream),"hipMemcpyAsync");
+    PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
+    return PIXHIP_OK;
+}
+
+int pixhip_weight_get(pixhip_session* s, const char* key, const void* host_bytes, uint64_t bytes, uint32_t type, uint64_t inner,
+                      uint64_t rows, pixhip_weight** out)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!key || !out) return fail(PIXHIP_ERR_ARGUMENT,"null key or output");
+    *out = nullptr;
+    if ((rc = check_shape(type,inner,rows))) return rc;
+    const uint64_t expect = rows * (inner / block_values(type)) * block_bytes(type);
+    auto it = s->weights.find(key);
+    if (it != s->weights.end()) {
+        pixhip_weight* w = it->second;
+        if (w->type != type || w->inner != inner || w->rows != rows) return fail(PIXHIP_ERR_ARGUMENT,"cached key with another shape");
+        w->used = ++s->uses;
+        *out = w;
+        return PIXHIP_OK;
+    }
+    if (!host_bytes || bytes < expect) return fail(PIXHIP_ERR_ARGUMENT,"weight bytes missing or shorter than rows*row_bytes");
+    pixhip_weight* w = new (std::nothrow) pixhip_weight();
+    if (!w) return fail(PIXHIP_ERR_MEMORY,"host allocation failed");
+    w->key = key;
+    w->type = type;
+    w->inner = inner;
+    w->rows = rows;
+    w->gguf_bytes = expect;
+    w->used = ++s->uses;
+    rc = weight_alloc(s,w,round_up(expect,kAlign),&w->raw);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(w->raw,host_bytes,expect,hipMemcpyHostToDevice,s->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) rc = hip_fail(e,"weight upload");
+    }
+    if (!rc && type == PIX_Q8_0) rc = build_q8_0(s,w);
+    if (rc) {
+        release_weight(s,w);
+        return rc;
+    }
+    s->weights.emplace(w->key,w);
+    *out = w;
+    return PIXHIP_OK;
+}
+
+int pixhip_weight_cache_info(pixhip_session* s, uint64_t* entries, uint64_t* bytes)
+{
+    if (!s) return fail(PIXHIP_ERR_STATE,"no session");
+    if (entries) *entries = s->weights.size();
+    if (bytes) *bytes = s->cache_bytes;
+    return PIXHIP_OK;
+}
+
+int pixhip_matmul(pixhip_session* s, const pixhip_weight* w, const float* input, size_t columns, float* output)
+{
+    return run(s,w,input,columns,output,nullptr,0,0,PIXHIP_STAGE_QUANTIZE | PIXHIP_STAGE_MULTIPLY,true);
+}
+
+int pixhip_matmul_ex(pixhip_session* s, const pixhip_weight* w, const float* input, size_t columns, float* output, const float* bias,
+                     size_t ldy, size_t y_offset)
+{
+    return run(s,w,input,columns,output,bias,ldy,y_offset,PIXHIP_STAGE_QUANTIZE | PIXHIP_STAGE_MULTIPLY,false);
+}
+
+int pixhip_matmul_stage(pixhip_session* s, const pixhip_weight* w, const float* input, size_t columns, float* output,
+                        const float* bias, size_t ldy, size_t y_offset, unsigned stages)
+{
+    return run(s,w,input,columns,output,bias,ldy,y_offset,stages,false);
+}
+
+int pixhip_quant_matmul(pixhip_session* s, const unsigned char* weights, uint32_t type, const float* input, float* output,
+                        size_t rows, size_t columns, size_t inner)
+{
+    if (!s) return fail(PIXHIP_ERR_STATE,"no session");
+    int rc = check_shape(type,inner,rows);
+    if (rc) return rc;
+    if (!columns || !weights || !input || !output) return fail(PIXHIP_ERR_ARGUMENT,"null pointer or zero columns");
+    const uint64_t bytes = rows * (inner / block_values(type)) * block_bytes(type);
+    const std::string key = "host:" + std::to_string(reinterpret_cast<uintptr_t>(weights)) + ":" + std::to_string(bytes) + ":" +
+                            std::to_string(type) + ":" + std::to_string(rows) + ":" + std::to_string(inner);
+    pixhip_weight* w = nullptr;
+    if ((rc = pixhip_weight_get(s,key.c_str(),weights,bytes,type,inner,rows,&w))) return rc;
+    return pixhip_matmul(s,w,input,columns,output);
+}
+
+int pixhip_quantize_q8_0(pixhip_session* s, const float* input, void* blocks, size_t rows, size_t inner)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!rows || !inner || inner % PIX_QK8) return fail(PIXHIP_ERR_ARGUMENT,"inner must be a positive multiple of 32");
+    if (!input || !blocks || reinterpret_cast<uintptr_t>(input) % 16 || reinterpret_cast<uintptr_t>(blocks) % 2)
+        return fail(PIXHIP_ERR_ARGUMENT,"input must be 16-byte aligned, blocks 2-byte aligned");
+    PIX_HIP(pixhip::launch_quantize_q8_0(input,rows,inner,round_up(inner,64),pixhip::Act80{nullptr,nullptr,0},blocks,s->stream),
+            "quantize Q8_0");
+    return PIXHIP_OK;
+}
+
+int pixhip_quantize_q8_K(pixhip_session* s, const float* input, void* blocks, size_t rows, size_t inner)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!rows || !inner || inner % PIX_QK) return fail(PIXHIP_ERR_ARGUMENT,"inner must be a positive multiple of 256");
+    if (!input || !blocks || reinterpret_cast<uintptr_t>(input) % 16 || reinterpret_cast<uintptr_t>(blocks) % 4)
+        return fail(PIXHIP_ERR_ARGUMENT,"input must be 16-byte aligned, blocks 4-byte aligned");
+    PIX_HIP(pixhip::launch_quantize_q8_K(input,rows,inner,pixhip::Act8K{nullptr,nullptr,nullptr,0},blocks,s->stream),
+            "quantize Q8_K");
+    return PIXHIP_OK;
+}
+
+int pixhip_block_sums(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t columns, int32_t* sums, int32_t* mins)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    pixhip_weight* w = const_cast<pixhip_weight*>(wc);
+    if (!w || !input || !sums || !columns || (w->type == PIX_Q5_K && !mins)) return fail(PIXHIP_ERR_ARGUMENT,"null pointer");
+    if (reinterpret_cast<uintptr_t>(input) % 16) return fail(PIXHIP_ERR_ARGUMENT,"input must be 16-byte aligned");
+    if ((rc = quantize_stage(s,w,input,columns))) return rc;
+    if ((rc = ensure_gemm_form(s,w))) return rc;
+    hipError_t e;
+    if (w->type == PIX_Q5_K) e = pixhip::launch_sums_q5_K(s->a8k,w->q5,columns,w->rows,w->inner,sums,mins,s->stream);
+    else if (w->type == PIX_Q6_K) e = pixhip::launch_sums_q6_K(s->a8k,w->q6,columns,w->rows,w->inner,sums,s->stream);
+    else e = pixhip::launch_sums_q8_0(s->a80,w->q80,columns,w->rows,w->inner,sums,s->stream);
+    PIX_HIP(e,"block sums launch");
+    return PIXHIP_OK;
+}
+
+int pixhip_timer_start(pixhip_session* s)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    PIX_HIP(hipEventRecord(s->t0,s->stream),"hipEventRecord");
+    return PIXHIP_OK;
+}
+
+int pixhip_timer_stop(pixhip_session* s, float* ms)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    PIX_HIP(hipEventRecord(s->t1,s->stream),"hipEventRecord");
+    PIX_HIP(hipEventSynchronize(s->t1),"hipEventSynchronize");
+    float v = 0;
+    PIX_HIP(hipEventElapsedTime(&v,s->t0,s->t1),"hipEventElapsedTime");
+    if (ms) *ms = v;
+    return PIXHIP_OK;
+}
+
+}  // extern "C"

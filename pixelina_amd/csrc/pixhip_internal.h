@@ -1,0 +1,122 @@
+// Internal declarations shared by the HIP kernel files and the C-ABI layer.
+//
+// Resident (HBM) data layouts used by the kernels.  The boundary accepts the
+// reference's GGUF block bytes (src/kernels_quant.cpp:14-38); the weight cache
+// converts them once, at upload, into the layouts below, which is legal because
+// the cache is internal to the backend (src/backend_vulkan.cpp:742-758).
+//
+//   activations, Q8_K ("act8k"), M rows of K values:
+//     qs   int8   [M][K]          quantized values
+//     d    fp32   [K/256][Mpad]   block scale, super-block-major
+//     bs   fp16   [M][K/16]       sums of 16 quantized values (exact, |s| <= 2032)
+//   activations, Q8_0 ("act80"), rows of Kp = K rounded up to 64 (a zero pad block):
+//     qs   int8   [M][Kp]
+//     d    fp32   [Kp/32][Mpad]   fp16-rounded block scale widened to fp32
+//   weights Q5_K for the GEMM ("planes"), N rows:
+//     hi   int8   [N][K]          (scale_s * q) >> 6
+//     lo   int8   [N][K]          (scale_s * q) & 63
+//     d    fp32   [N][K/256]      super-block scale d
+//     dm   fp32   [N][K/256]      super-block dmin
+//     mn   fp16   [N][K/16]       six-bit minimum of the 32-value sub-block, once per 16 values
+//   weights Q6_K for the GEMM: hi/lo of scale*(q-32) = 64*hi + lo, d fp32 [N][K/256]
+//   weights Q8_0 ("planar", GEMM and matvec), rows of Kp with a zero pad block:
+//     qs int8 [Npad][Kp], d fp16 [N][Kp/32], and for the GEMM the same scales
+//     widened and transposed, dT fp32 [Kp/32][Npad]
+//   weights Q5_K for the matvec: the GGUF bytes unchanged (176-B blocks are 16-B aligned)
+//   weights Q6_K for the matvec ("q6 planar"): ql u8 [N][K/2], qh u8 [N][K/4],
+//     sc int8 [N][K/16], d fp16 [N][K/256] -- same bytes as GGUF, re-sliced so every
+//     plane is 16-B aligned (210-B blocks are only 2-B aligned).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define PIX_Q8_0 8
+#define PIX_Q5_K 13
+#define PIX_Q6_K 14
+#define PIX_QK 256
+#define PIX_QK8 32
+#define PIX_Q8_0_BYTES 34
+#define PIX_Q8_K_BYTES 292
+#define PIX_Q5_K_BYTES 176
+#define PIX_Q6_K_BYTES 210
+
+namespace pixhip {
+
+struct Act8K {
+    int8_t* qs;       // [mpad][K]
+    float* d;         // [K/256][mpad]
+    _Float16* bs;     // [mpad][K/16]
+    size_t mpad;      // rows allocated (multiple of the GEMM tile)
+};
+
+struct Act80 {
+    int8_t* qs;       // [mpad][Kp]
+    float* d;         // [Kp/32][mpad]
+    size_t mpad;
+};
+
+struct PlanesQ5K {
+    const int8_t* hi;
+    const int8_t* lo;
+    const float* d;
+    const float* dm;
+    const _Float16* mn;
+};
+
+struct PlanesQ6K {
+    const int8_t* hi;
+    const int8_t* lo;
+    const float* d;
+};
+
+struct PlanarQ80 {
+    const int8_t* qs;     // [Npad][Kp]
+    const _Float16* d;    // [N][Kp/32]   (matvec)
+    const float* dT;      // [Kp/32][Npad] (GEMM)
+};
+
+struct PlanarQ6K {
+    const uint8_t* ql;
+    const uint8_t* qh;
+    const int8_t* sc;
+    const _Float16* d;
+};
+
+struct Output {
+    float* y;
+    const float* bias;
+    size_t ldy;
+    size_t offset;
+};
+
+// quantize.hip
+hipError_t launch_quantize_q8_K(const float* x, size_t rows, size_t inner, Act8K planar, void* blocks, hipStream_t s);
+hipError_t launch_quantize_q8_0(const float* x, size_t rows, size_t inner, size_t kpad, Act80 planar, void* blocks,
+                                hipStream_t s);
+
+// repack.hip
+hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, int8_t* hi, int8_t* lo, float* d, float* dm,
+                              _Float16* mn, hipStream_t s);
+hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inner, int8_t* hi, int8_t* lo, float* d, hipStream_t s);
+hipError_t launch_repack_q6_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* ql, uint8_t* qh, int8_t* sc,
+                                     _Float16* d, hipStream_t s);
+hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, size_t kpad, size_t rows_pad, int8_t* qs, _Float16* d,
+                              float* dT, hipStream_t s);
+
+// gemm.hip
+hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s);
+hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s);
+hipError_t launch_gemm_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s);
+hipError_t launch_sums_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, int32_t* scaled, int32_t* mins,
+                            hipStream_t s);
+hipError_t launch_sums_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s);
+hipError_t launch_sums_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s);
+
+// matvec.hip
+hipError_t launch_matvec_q5_K(const uint8_t* raw, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
+hipError_t launch_matvec_q8_0(const PlanarQ80& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
+hipError_t launch_matvec_q6_K(const PlanarQ6K& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
+
+}  // namespace pixhip

@@ -1,0 +1,105 @@
+// Activation block quantizers (the counterpart of quantize_row_q8_0_ref /
+// quantize_row_q8_K_ref, src/kernels_quant.cpp:80-144, and of the GPU pass
+// shaders/quantize.comp:13-41 that precedes MMQ).  Each launch writes the
+// planar layout the GEMM reads and, when asked, the reference's own block
+// layout (block_q8_0 / block_q8_K) for callers and for the integer parity gate.
+//
+// HBM-bound byte work: one wave per Q8_K block (64 lanes x float4 = 256
+// values), one 8-lane group per Q8_0 block; reads 4 B/value, writes ~1.1 B/value.
+#include "pixhip_device.h"
+#include "pixhip_internal.h"
+
+namespace pixhip {
+
+constexpr int kQuantWaves = 4;
+
+__global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_K_kernel(const float* __restrict__ x, size_t rows, size_t inner,
+                                                                         size_t mpad, int8_t* __restrict__ qs, float* __restrict__ dT,
+                                                                         _Float16* __restrict__ bs, uint8_t* __restrict__ blocks)
+{
+    const size_t nb = inner / PIX_QK;
+    const size_t total = rows * nb;
+    const int lane = threadIdx.x & 63;
+    const size_t block = (size_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+    if (block >= total) return;  // whole wave exits together
+    const size_t row = block / nb, b = block % nb;
+    const float* src = x + row * inner + b * PIX_QK;
+    float4 v = reinterpret_cast<const float4*>(src)[lane];
+    uint32_t packed;
+    float d;
+    int gsum;
+    quantize_q8_K_wave(v,lane,packed,d,gsum);
+    if (qs) {
+        reinterpret_cast<uint32_t*>(qs + row * inner + b * PIX_QK)[lane] = packed;
+        if (lane == 0) dT[b * mpad + row] = d;
+        if ((lane & 3) == 0) bs[row * (inner / 16) + b * 16 + (lane >> 2)] = (_Float16)(float)gsum;
+    }
+    if (blocks) {
+        uint8_t* blk = blocks + block * PIX_Q8_K_BYTES;
+        reinterpret_cast<uint32_t*>(blk + 4)[lane] = packed;
+        if (lane == 0) *reinterpret_cast<float*>(blk) = d;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(blk + 4 + PIX_QK)[lane >> 2] = (int16_t)gsum;
+    }
+}
+
+// Planar rows have stride kpad = inner rounded up to 64; the padding block
+// (when inner % 64 == 32) is written as zeros with a zero scale so it adds
+// exactly nothing to a dot product.
+__global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_0_kernel(const float* __restrict__ x, size_t rows, size_t inner,
+                                                                         size_t kpad, size_t mpad, int8_t* __restrict__ qs,
+                                                                         float* __restrict__ dT, uint8_t* __restrict__ blocks)
+{
+    const size_t nb = inner / PIX_QK8, nbp = kpad / PIX_QK8;
+    const size_t total = rows * nbp;
+    const int lane = threadIdx.x & 63;
+    const size_t wave_block = ((size_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6)) * 8;
+    if (wave_block >= total) return;
+    const size_t block = wave_block + (lane >> 3);
+    const bool valid = block < total;
+    // Lanes past the end mirror the last block so every lane joins the 8-lane
+    // shuffles; only valid lanes store.
+    const size_t blk = valid? block : total - 1;
+    const size_t row = blk / nbp, b = blk % nbp;
+    const bool real = b < nb;
+    float4 v = real? reinterpret_cast<const float4*>(x + row * inner + b * PIX_QK8)[lane & 7] : make_float4(0.f,0.f,0.f,0.f);
+    uint32_t packed;
+    float d32;
+    uint16_t dh;
+    quantize_q8_0_group(v,packed,d32,dh);
+    if (!valid) return;
+    if (qs) {
+        reinterpret_cast<uint32_t*>(qs + row * kpad + b * PIX_QK8)[lane & 7] = packed;
+        if ((lane & 7) == 0) dT[b * mpad + row] = half_bits_to_float(dh);
+    }
+    if (blocks && real) {
+        uint8_t* out = blocks + (row * nb + b) * PIX_Q8_0_BYTES;
+        uint16_t* q16 = reinterpret_cast<uint16_t*>(out + 2 + 4 * (lane & 7));
+        q16[0] = (uint16_t)(packed & 0xffffu);
+        q16[1] = (uint16_t)(packed >> 16);
+        if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(out) = dh;
+    }
+}
+
+hipError_t launch_quantize_q8_K(const float* x, size_t rows, size_t inner, Act8K planar, void* blocks, hipStream_t s)
+{
+    size_t total = rows * (inner / PIX_QK);
+    if (!total) return hipSuccess;
+    size_t grid = (total + kQuantWaves - 1) / kQuantWaves;
+    quantize_q8_K_kernel<<<dim3((unsigned)grid),dim3(64 * kQuantWaves),0,s>>>(x,rows,inner,planar.mpad,planar.qs,planar.d,planar.bs,
+                                                                               static_cast<uint8_t*>(blocks));
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8_0(const float* x, size_t rows, size_t inner, size_t kpad, Act80 planar, void* blocks,
+                                hipStream_t s)
+{
+    size_t total = rows * (kpad / PIX_QK8);
+    if (!total) return hipSuccess;
+    size_t waves = (total + 7) / 8;
+    size_t grid = (waves + kQuantWaves - 1) / kQuantWaves;
+    quantize_q8_0_kernel<<<dim3((unsigned)grid),dim3(64 * kQuantWaves),0,s>>>(x,rows,inner,kpad,planar.mpad,planar.qs,planar.d,
+                                                                               static_cast<uint8_t*>(blocks));
+    return hipGetLastError();
+}
+
+}  // namespace pixhip

@@ -1,0 +1,112 @@
+// Implementation of the C++ shim declared in backend_hip.h, over the C ABI.
+#include "backend_hip.h"
+
+#include <hip/hip_runtime.h>
+
+struct HipState {
+    pixhip_session* session = nullptr;
+    ~HipState()
+    {
+        if (session) pixhip_session_destroy(session);
+    }
+};
+
+// One session per inference thread, as the reference's thread_local
+// active_state (src/backend_vulkan.cpp:86).
+static thread_local std::shared_ptr<HipState> active_state;
+
+std::shared_ptr<HipState> hip_active_state()
+{
+    return active_state;
+}
+
+pixhip_session* hip_state_session(const std::shared_ptr<HipState> &state)
+{
+    return state? state->session : nullptr;
+}
+
+void* hip_allocate(const std::shared_ptr<HipState> &state, size_t bytes)
+{
+    if (!state) return nullptr;
+    if (!bytes) bytes = 4;
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p,bytes,hipHostMallocDefault);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+
+void hip_free(const std::shared_ptr<HipState> &state, void* pointer)
+{
+    if (!state || !pointer) return;
+    // Queued work may still read the buffer (release is deferred in the
+    // reference, src/backend_vulkan.cpp:525-531).
+    (void)pixhip_synchronize(state->session);
+    (void)hipHostFree(pointer);
+}
+
+bool hip_synchronize()
+{
+    return !active_state || pixhip_synchronize(active_state->session) == PIXHIP_OK;
+}
+
+bool HipSession::initialize(int device)
+{
+    if (active_state) return false;
+    auto fresh = std::make_shared<HipState>();
+    if (pixhip_session_create(device,&fresh->session) != PIXHIP_OK) return false;
+    state = fresh;
+    active_state = state;
+    return true;
+}
+
+HipSession::~HipSession()
+{
+    if (active_state == state) active_state.reset();
+}
+
+std::string HipSession::device_name() const
+{
+    char name[256] = {0};
+    if (!state || pixhip_device_name(state->session,name,sizeof(name)) != PIXHIP_OK) return std::string();
+    return name;
+}
+
+bool HipSession::memory_limits(uint64_t &bytes, uint64_t &range) const
+{
+    return state && pixhip_memory_limits(state->session,&bytes,&range) == PIXHIP_OK && bytes != 0;
+}
+
+bool HipSession::prepare_stage(uint64_t activation_bytes, uint64_t scratch_bytes)
+{
+    if (!state) return false;
+    if (pixhip_set_weight_budget(state->session,packed_weight_budget) != PIXHIP_OK) return false;
+    return pixhip_prepare_stage(state->session,activation_bytes,scratch_bytes) == PIXHIP_OK;
+}
+
+pixhip_weight* hip_weight(const std::string &key, const void* host_bytes, uint64_t bytes, uint32_t type, uint64_t inner,
+                          uint64_t rows)
+{
+    if (!active_state) return nullptr;
+    pixhip_weight* w = nullptr;
+    if (pixhip_weight_get(active_state->session,key.c_str(),host_bytes,bytes,type,inner,rows,&w) != PIXHIP_OK) return nullptr;
+    return w;
+}
+
+bool hip_matmul_weight(pixhip_weight* weight, const float* input, size_t columns, float* output)
+{
+    return active_state && pixhip_matmul(active_state->session,weight,input,columns,output) == PIXHIP_OK;
+}
+
+bool hip_available(std::string &description)
+{
+    HipSession session;
+    if (!session.initialize()) {
+        description = "HIP initialization failed.";
+        return false;
+    }
+    description = session.device_name();
+    return true;
+}

@@ -1,0 +1,111 @@
+/* C++17 counterpart of src/backend_vulkan.h for the quantized linear path.
+ *
+ * Mirrors the reference's backend interface so that the branch in cpu_matmul
+ * (src/backend_cpu.cpp:108-112) can route to HIP exactly as it routes to
+ * Vulkan:
+ *
+ *   if (hip_active_state()) return hip_matmul(file,weight,input,columns,output);
+ *
+ *   HipSession          <- VulkanSession     (src/backend_vulkan.h:124-137)
+ *   hip_active_state()  <- vulkan_active_state (thread_local, :82, .cpp:86)
+ *   hip_allocate/free   <- vulkan_allocate/free (:83-84)
+ *   hip_synchronize()   <- vulkan_synchronize (:85)
+ *   HipAllocator<T>     <- VulkanAllocator<T> (:88-122)
+ *   hip_matmul(...)     <- vulkan_matmul (:139)
+ *
+ * hip_matmul is a template over the model-file and weight types so this
+ * header compiles against the reference's own PixModelFile / PixWeight
+ * (src/model.h:33-56) without including them: it reads file.filename,
+ * file.data, weight.name, weight.shape ({inner, rows}, GGML order),
+ * weight.type, weight.offset and weight.bytes, and builds the same cache key
+ * as VulkanState::weight (src/backend_vulkan.cpp:744).  No exceptions are
+ * thrown (the reference builds with -fno-exceptions); failures return false.
+ */
+#ifndef PIXELINA_BACKEND_HIP_H
+#define PIXELINA_BACKEND_HIP_H
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <new>
+#include <string>
+#include <type_traits>
+#include <utility>
+
+#include "pixhip.h"
+
+struct HipState;  // owns one pixhip_session
+std::shared_ptr<HipState> hip_active_state();
+pixhip_session* hip_state_session(const std::shared_ptr<HipState> &state);
+void* hip_allocate(const std::shared_ptr<HipState> &state, size_t bytes);
+void hip_free(const std::shared_ptr<HipState> &state, void* pointer);
+bool hip_synchronize();
+
+// Activation buffers shared by host and device: the model code reads
+// activations on the host after hip_synchronize(), as it does with the Vulkan
+// backend's host-coherent mappings.  Allocates pinned host memory; the kernels
+// stage it through HBM once per call (pixhip_matmul).
+template <typename T> struct HipAllocator {
+    using value_type = T;
+    using propagate_on_container_move_assignment = std::true_type;
+    std::shared_ptr<HipState> state;  // owning device lifetime, or CPU allocation mode
+    HipAllocator() : state(hip_active_state()) {}
+    template <typename U> HipAllocator(const HipAllocator<U> &other) : state(other.state) {}
+    T* allocate(size_t count)
+    {
+        if (state) return static_cast<T*>(hip_allocate(state,count * sizeof(T)));
+        return static_cast<T*>(::operator new(count * sizeof(T)));
+    }
+    void deallocate(T* pointer, size_t)
+    {
+        if (state) hip_free(state,pointer);
+        else ::operator delete(pointer);
+    }
+    void construct(T* pointer)
+    {
+        // Output kernels overwrite every element; skip host clearing on the device path.
+        if (state) ::new (static_cast<void*>(pointer)) T;
+        else ::new (static_cast<void*>(pointer)) T();
+    }
+    template <typename... Args> void construct(T* pointer, Args&&... args)
+    {
+        ::new (static_cast<void*>(pointer)) T(std::forward<Args>(args)...);
+    }
+    template <typename U> bool operator==(const HipAllocator<U> &other) const { return state == other.state; }
+    template <typename U> bool operator!=(const HipAllocator<U> &other) const { return state != other.state; }
+};
+
+class HipSession {
+    std::shared_ptr<HipState> state;  // independent HIP context
+public:
+    HipSession() = default;
+    ~HipSession();
+    HipSession(const HipSession &) = delete;
+    HipSession &operator=(const HipSession &) = delete;
+
+    bool initialize(int device = 0);  // fails if a session is already active on this thread
+    std::string device_name() const;
+    bool memory_limits(uint64_t &bytes, uint64_t &range) const;
+    bool prepare_stage(uint64_t activation_bytes, uint64_t scratch_bytes);
+
+    uint64_t packed_weight_budget = UINT64_MAX;  // per-job cache admission after device planning
+};
+
+// The active session's cached weight for (filename, name, offset, bytes);
+// nullptr when no session is active or the upload fails.
+pixhip_weight* hip_weight(const std::string &key, const void* host_bytes, uint64_t bytes, uint32_t type, uint64_t inner,
+                          uint64_t rows);
+bool hip_matmul_weight(pixhip_weight* weight, const float* input, size_t columns, float* output);
+
+template <class File, class Weight>
+bool hip_matmul(const File &file, const Weight &weight, const float* input, size_t columns, float* output)
+{
+    if (weight.shape.size() != 2) return false;
+    const std::string key = file.filename + ":" + weight.name + ":" + std::to_string(weight.offset) + ":" + std::to_string(weight.bytes);
+    pixhip_weight* w = hip_weight(key,file.data + weight.offset,weight.bytes,weight.type,weight.shape[0],weight.shape[1]);
+    return w && hip_matmul_weight(w,input,columns,output);
+}
+
+bool hip_available(std::string &description);
+
+#endif /* PIXELINA_BACKEND_HIP_H */

@@ -1,0 +1,119 @@
+"""Thin Python handle over the C ABI (tests and bench drive the kernels
+through exactly the entry points a C/C++ caller would use)."""
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import check
+
+
+class DeviceBuffer:
+    """A pixhip_allocate'd device block owned by a Session."""
+
+    def __init__(self, session, nbytes):
+        self.session = session
+        self.nbytes = int(nbytes)
+        self.ptr = session.lib.pixhip_allocate(session.handle, self.nbytes)
+        if not self.ptr:
+            raise _lib.PixhipError(_lib.ERR_MEMORY, f"pixhip_allocate({self.nbytes})")
+
+    def upload(self, array, offset=0):
+        a = np.ascontiguousarray(array)
+        if offset + a.nbytes > self.nbytes:
+            raise ValueError("upload larger than the buffer")
+        check(self.session.lib.pixhip_copy_to_device(self.session.handle, self.ptr + offset, a.ctypes.data, a.nbytes),
+              "pixhip_copy_to_device")
+        return self
+
+    def download(self, dtype, count, offset=0):
+        out = np.empty(count, dtype=dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download larger than the buffer")
+        check(self.session.lib.pixhip_copy_to_host(self.session.handle, out.ctypes.data, self.ptr + offset, out.nbytes),
+              "pixhip_copy_to_host")
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.session.lib.pixhip_free(self.session.handle, self.ptr)
+            self.ptr = None
+
+
+class Session:
+    def __init__(self, device=0):
+        self.lib = _lib.load()
+        h = ctypes.c_void_p()
+        check(self.lib.pixhip_session_create(device, ctypes.byref(h)), "pixhip_session_create")
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            self.lib.pixhip_session_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # memory
+    def alloc(self, nbytes):
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, array):
+        a = np.ascontiguousarray(array)
+        return DeviceBuffer(self, max(a.nbytes, 4)).upload(a)
+
+    def synchronize(self):
+        check(self.lib.pixhip_synchronize(self.handle), "pixhip_synchronize")
+
+    def device_name(self):
+        buf = ctypes.create_string_buffer(256)
+        check(self.lib.pixhip_device_name(self.handle, buf, 256), "pixhip_device_name")
+        return buf.value.decode()
+
+    # weights
+    def weight(self, key, gguf_bytes, wtype, inner, rows):
+        b = np.ascontiguousarray(gguf_bytes, dtype=np.uint8)
+        h = ctypes.c_void_p()
+        check(self.lib.pixhip_weight_get(self.handle, key.encode(), b.ctypes.data, b.nbytes, wtype, inner, rows,
+                                         ctypes.byref(h)), "pixhip_weight_get")
+        return h.value
+
+    def cache_info(self):
+        n, b = ctypes.c_uint64(), ctypes.c_uint64()
+        check(self.lib.pixhip_weight_cache_info(self.handle, ctypes.byref(n), ctypes.byref(b)), "pixhip_weight_cache_info")
+        return n.value, b.value
+
+    # the op
+    def matmul(self, weight, x_ptr, columns, y_ptr):
+        return self.lib.pixhip_matmul(self.handle, weight, x_ptr, columns, y_ptr)
+
+    def matmul_ex(self, weight, x_ptr, columns, y_ptr, bias_ptr=None, ldy=0, y_offset=0):
+        return self.lib.pixhip_matmul_ex(self.handle, weight, x_ptr, columns, y_ptr, bias_ptr, ldy, y_offset)
+
+    def matmul_stage(self, weight, x_ptr, columns, y_ptr, stages, bias_ptr=None, ldy=0, y_offset=0):
+        return self.lib.pixhip_matmul_stage(self.handle, weight, x_ptr, columns, y_ptr, bias_ptr, ldy, y_offset, stages)
+
+    def quant_matmul(self, w_host_ptr, wtype, x_ptr, y_ptr, rows, columns, inner):
+        return self.lib.pixhip_quant_matmul(self.handle, w_host_ptr, wtype, x_ptr, y_ptr, rows, columns, inner)
+
+    def quantize_q8_0(self, x_ptr, blocks_ptr, rows, inner):
+        return self.lib.pixhip_quantize_q8_0(self.handle, x_ptr, blocks_ptr, rows, inner)
+
+    def quantize_q8_K(self, x_ptr, blocks_ptr, rows, inner):
+        return self.lib.pixhip_quantize_q8_K(self.handle, x_ptr, blocks_ptr, rows, inner)
+
+    def block_sums(self, weight, x_ptr, columns, sums_ptr, mins_ptr=None):
+        return self.lib.pixhip_block_sums(self.handle, weight, x_ptr, columns, sums_ptr, mins_ptr)
+
+    # timing
+    def timer_start(self):
+        check(self.lib.pixhip_timer_start(self.handle), "pixhip_timer_start")
+
+    def timer_stop(self):
+        ms = ctypes.c_float()
+        check(self.lib.pixhip_timer_stop(self.handle, ctypes.byref(ms)), "pixhip_timer_stop")
+        return ms.value

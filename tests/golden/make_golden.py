@@ -1,0 +1,147 @@
+"""Writes the golden fixtures under tests/golden/ from the reference's own CPU
+path, compiled in place from the reference sources (oracle/Makefile ->
+oracle/_ref/libpixref.so).  Run in the build container only:
+
+    make -C oracle ref && python tests/golden/make_golden.py
+
+Fixtures (numpy .npz, data only):
+  g1_quantize_q8_0.npz  quantize_row_q8_0_ref on crafted and random rows
+  g2_quantize_q8_K.npz  quantize_row_q8_K_ref, incl. rows whose rounding
+                        depends on the fused multiply-add of nearest_int
+  g3_dots.npz           pix_dot_q8_0 / q5_K / q6_K on random rows
+  g4_matmul.npz         cpu_quant_matmul on small shapes and a decode slice
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.dirname(HERE))
+
+from oracle_lib import Q5_K, Q6_K, Q8_0, dot, quant_matmul, quantize, reference  # noqa: E402
+from pixelina_amd import synth  # noqa: E402
+
+
+def crafted_q8_0():
+    rows = []
+    z = np.zeros(32, np.float32)
+    rows.append(z.copy())                                   # all zero -> d = 0, id = 0
+    r = z.copy(); r[7] = 1.0; rows.append(r)                 # single spike
+    r = z.copy(); r[0] = 127.0                              # d = 1, id = 1: exact .5 ties
+    r[1:12] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5, 63.5, -63.5, 3.5]; rows.append(r)
+    r = np.linspace(-1e-3, 1e-3, 32).astype(np.float32); rows.append(r)   # fp16-subnormal d
+    r = np.linspace(-1e-6, 2e-6, 32).astype(np.float32); rows.append(r)   # deeper subnormal d
+    r = np.linspace(-1e7, 9e6, 32).astype(np.float32); rows.append(r)     # d overflows fp16 -> inf
+    r = np.linspace(-3.0, 1.0, 32).astype(np.float32); rows.append(r)     # negative max
+    r = z.copy(); r[5] = np.nan; r[6] = 2.0; rows.append(r)              # NaN ignored by amax, quantizes to 0
+    r = z.copy(); r[3] = np.inf; r[4] = -5.0; rows.append(r)             # infinite amax
+    r = np.full(32, -7.25, np.float32); rows.append(r)                   # constant negative
+    return np.stack(rows)
+
+
+def crafted_q8_K():
+    rows = []
+    z = np.zeros(256, np.float32)
+    rows.append(z.copy())
+    r = z.copy(); r[100] = -3.0; rows.append(r)              # single negative spike
+    r = z.copy(); r[3] = -5.0; r[10] = 5.0; rows.append(r)   # |max| tie: first (negative) wins
+    r = z.copy(); r[3] = 5.0; r[10] = -5.0; rows.append(r)   # |max| tie: first (positive) wins
+    r = np.linspace(-127, 127, 256).astype(np.float32); rows.append(r)
+    r = np.linspace(-1e-30, 1e-30, 256).astype(np.float32); rows.append(r)  # tiny scale
+    r = z.copy(); r[0] = np.nan; r[1] = 1.0; rows.append(r)  # NaN never wins the arg-max
+    r = np.full(256, 2.5, np.float32); rows.append(r)        # constant positive
+    return np.stack(rows)
+
+
+def fused_tie_rows(count, seed=7):
+    """Random N(0,1) rows where nearest_int(iscale*x) differs between a fused
+    multiply-add and a rounded product (found by exact float64 arithmetic)."""
+    rng = np.random.default_rng(seed)
+    found = []
+    while len(found) < count:
+        x = rng.standard_normal((4096, 256)).astype(np.float32)
+        ax = np.abs(x)
+        mx = x[np.arange(x.shape[0]), np.argmax(ax, axis=1)]
+        iscale = (np.float32(-127.0) / mx).astype(np.float32)
+        p = iscale.astype(np.float64)[:, None] * x.astype(np.float64)   # exact product
+        fused = np.rint(p)
+        unfused = np.rint(p.astype(np.float32).astype(np.float64))
+        hit = np.nonzero((fused != unfused).any(axis=1))[0]
+        found.extend(x[h] for h in hit[: count - len(found)])
+    return np.stack(found)
+
+
+def main():
+    ref = reference()
+    if ref is None:
+        raise SystemExit("oracle/_ref/libpixref.so missing: run `make -C oracle ref` first")
+    rng = np.random.default_rng(20260101)
+
+    # G1
+    x1 = np.concatenate([crafted_q8_0(), (rng.standard_normal((24, 32)) * rng.choice([1e-2, 1, 30], (24, 1))).astype(np.float32)])
+    b1 = quantize(ref, "ref", x1, "q8_0")
+    np.savez_compressed(os.path.join(HERE, "g1_quantize_q8_0.npz"), x=x1, blocks=b1)
+
+    # G2
+    ties = fused_tie_rows(12)
+    x2 = np.concatenate([crafted_q8_K(), ties, rng.standard_normal((12, 256)).astype(np.float32) * 3])
+    b2 = quantize(ref, "ref", x2, "q8_K")
+    np.savez_compressed(os.path.join(HERE, "g2_quantize_q8_K.npz"), x=x2, blocks=b2, fused_rows=np.arange(8, 8 + len(ties)))
+
+    # G3: dots on random rows
+    g3 = {}
+    for wtype, name in ((Q8_0, "q8_0"), (Q5_K, "q5_K"), (Q6_K, "q6_K")):
+        for k in (256, 512, 3840):
+            n = 12
+            wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+            if wtype == Q8_0:
+                wb = quantize(ref, "ref", wf, "q8_0")
+            elif wtype == Q5_K:
+                wb = synth.pack_q5_K(wf)
+            else:
+                wb = synth.pack_q6_K(wf)
+            xf = rng.standard_normal((n, k)).astype(np.float32)
+            xf[:, rng.integers(0, k, 3)] *= 20.0
+            ab = quantize(ref, "ref", xf, "q8_0" if wtype == Q8_0 else "q8_K")
+            y = np.array([dot(ref, "ref", wtype, wb[i], ab[i], k) for i in range(n)], dtype=np.float32)
+            g3[f"{name}_{k}_w"] = wb
+            g3[f"{name}_{k}_x"] = xf
+            g3[f"{name}_{k}_a"] = ab
+            g3[f"{name}_{k}_y"] = y
+    np.savez_compressed(os.path.join(HERE, "g3_dots.npz"), **g3)
+
+    # G4: cpu_quant_matmul, small shapes + a decode-row slice of the 18944x3584 matvec
+    g4 = {}
+    cases = []
+    for wtype, name in ((Q8_0, "q8_0"), (Q5_K, "q5_K"), (Q6_K, "q6_K")):
+        for m in (1, 3):
+            for n in (5, 17):
+                for k in (256, 3840):
+                    cases.append((wtype, name, m, n, k))
+        cases.append((wtype, name, 1, 64, 3584))
+    for i, (wtype, name, m, n, k) in enumerate(cases):
+        wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        if wtype == Q8_0:
+            wb = quantize(ref, "ref", wf, "q8_0")
+        elif wtype == Q5_K:
+            wb = synth.pack_q5_K(wf)
+        else:
+            wb = synth.pack_q6_K(wf)
+        xf = rng.standard_normal((m, k)).astype(np.float32)
+        y = quant_matmul(ref, "ref", wb, wtype, xf, n)
+        g4[f"c{i}_w"] = wb
+        g4[f"c{i}_x"] = xf
+        g4[f"c{i}_y"] = y
+        g4[f"c{i}_shape"] = np.array([wtype, m, n, k], dtype=np.int64)
+    g4["count"] = np.array(len(cases))
+    np.savez_compressed(os.path.join(HERE, "g4_matmul.npz"), **g4)
+    for f in sorted(os.listdir(HERE)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(HERE, f)))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,143 @@
+"""ctypes handles on the checkers: the oracle's C restatement
+(oracle/liboracle.so) and, where it was built, the reference's own CPU path
+(oracle/_ref/libpixref.so).  Test infrastructure only."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+ORACLE_SO = os.path.join(ORACLE_DIR, "liboracle.so")
+REF_SO = os.path.join(ORACLE_DIR, "_ref", "libpixref.so")
+
+Q8_0, Q5_K, Q6_K = 8, 13, 14
+Q8_0_BYTES, Q8_K_BYTES = 34, 292
+
+_vp, _i64, _int, _sz, _u32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t, ctypes.c_uint32
+
+_oracle = None
+_ref = None
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            subprocess.run(["make", "-C", ORACLE_DIR, "oracle"], check=True, capture_output=True)
+        lib = ctypes.CDLL(ORACLE_SO)
+        sig = {
+            "orc_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
+            "orc_float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
+            "orc_nearest_int_fused": (_int, [ctypes.c_float, ctypes.c_float]),
+            "orc_quantize_q8_0": (None, [_vp, _vp, _i64]),
+            "orc_quantize_q8_K": (None, [_vp, _vp, _i64]),
+            "orc_dot_q8_0": (ctypes.c_float, [_int, _vp, _vp]),
+            "orc_dot_q5_K": (ctypes.c_float, [_int, _vp, _vp]),
+            "orc_dot_q6_K": (ctypes.c_float, [_int, _vp, _vp]),
+            "orc_block_sums_q8_0": (ctypes.c_int32, [_vp, _vp]),
+            "orc_superblock_sums_q5_K": (None, [_vp, _vp, _vp, _vp]),
+            "orc_superblock_sum_q6_K": (ctypes.c_int32, [_vp, _vp]),
+            "orc_quant_matmul": (_int, [_vp, _u32, _vp, _vp, _sz, _sz, _sz, _int]),
+            "orc_decode": (None, [_vp, _u32, _sz, _vp]),
+            "orc_row_bytes": (ctypes.c_uint64, [ctypes.c_uint64, _u32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        _oracle = lib
+    return _oracle
+
+
+def reference():
+    """The compiled reference (None when oracle/_ref was not built here)."""
+    global _ref
+    if _ref is None:
+        if not os.path.exists(REF_SO):
+            return None
+        lib = ctypes.CDLL(REF_SO)
+        sig = {
+            "ref_quantize_q8_0": (None, [_vp, _vp, _i64]),
+            "ref_quantize_q8_K": (None, [_vp, _vp, _i64]),
+            "ref_dot_q8_0": (ctypes.c_float, [_int, _vp, _vp]),
+            "ref_dot_q5_K": (ctypes.c_float, [_int, _vp, _vp]),
+            "ref_dot_q6_K": (ctypes.c_float, [_int, _vp, _vp]),
+            "ref_nearest_int": (_int, [ctypes.c_float]),
+            "ref_quant_matmul": (_int, [_vp, _u32, _vp, _vp, _sz, _sz, _sz]),
+            "ref_set_threads": (None, [_sz]),
+            "ref_thread_count": (_sz, []),
+            "ref_decode": (None, [_vp, _u32, _sz, _vp]),
+            "ref_half_float": (ctypes.c_float, [ctypes.c_uint16]),
+            "ref_row_bytes": (ctypes.c_uint64, [ctypes.c_uint64, _u32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        _ref = lib
+    return _ref
+
+
+def ptr(a):
+    return a.ctypes.data
+
+
+# ---- numpy conveniences over either library (prefix "orc" or "ref") ----
+
+def quantize(lib, prefix, x, kind):
+    """Rows of x (float32 [R, K]) -> reference block bytes uint8 [R, K/QK*B]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    if kind == "q8_0":
+        out = np.zeros((rows, k // 32 * Q8_0_BYTES), dtype=np.uint8)
+        fn = getattr(lib, f"{prefix}_quantize_q8_0")
+    else:
+        out = np.zeros((rows, k // 256 * Q8_K_BYTES), dtype=np.uint8)
+        fn = getattr(lib, f"{prefix}_quantize_q8_K")
+    for r in range(rows):
+        fn(ptr(x[r]), ptr(out[r]), k)
+    return out
+
+
+def dot(lib, prefix, wtype, wrow, arow, k):
+    name = {Q8_0: "dot_q8_0", Q5_K: "dot_q5_K", Q6_K: "dot_q6_K"}[wtype]
+    wrow = np.ascontiguousarray(wrow)
+    arow = np.ascontiguousarray(arow)
+    return getattr(lib, f"{prefix}_{name}")(k, ptr(wrow), ptr(arow))
+
+
+def quant_matmul(lib, prefix, w, wtype, x, rows, threads=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    cols, k = x.shape
+    y = np.full((cols, rows), np.nan, dtype=np.float32)
+    if prefix == "orc":
+        ok = lib.orc_quant_matmul(ptr(w), wtype, ptr(x), ptr(y), rows, cols, k, threads or (os.cpu_count() or 1))
+    else:
+        ok = lib.ref_quant_matmul(ptr(w), wtype, ptr(x), ptr(y), rows, cols, k)
+    if not ok:
+        raise ValueError("quant_matmul rejected its arguments")
+    return y
+
+
+def decode(lib, w, wtype, count):
+    out = np.zeros(count, dtype=np.float64)
+    lib.orc_decode(ptr(np.ascontiguousarray(w)), wtype, count, ptr(out))
+    return out
+
+
+def q8_0_blocks(blocks):
+    """Split Q8_0 block bytes [..., nb*34] -> (d fp16 bits [..., nb], qs int8 [..., nb, 32])."""
+    b = blocks.reshape(*blocks.shape[:-1], -1, Q8_0_BYTES)
+    d = b[..., 0:2].copy().view(np.uint16)[..., 0]
+    qs = b[..., 2:].view(np.int8)
+    return d, qs
+
+
+def q8_K_blocks(blocks):
+    """Split Q8_K block bytes -> (d float32 [..., nb], qs int8 [..., nb, 256], bsums int16 [..., nb, 16])."""
+    b = blocks.reshape(*blocks.shape[:-1], -1, Q8_K_BYTES)
+    d = b[..., 0:4].copy().view(np.float32)[..., 0]
+    qs = b[..., 4:260].view(np.int8)
+    bs = b[..., 260:292].copy().view(np.int16)
+    return d, qs, bs
