@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized linear path on one MI355X.
+
+Headline workload (`value`): the Q5_K GEMM at the Z-Image DiT FFN shape,
+X fp32 [M=4096, K=3840] ~ N(0,1) with 1% of the K channels x20, W [N=10240,
+K=3840] ~ N(0,0.02) packed to Q5_K, output fp32 [4096, 10240].  One step is
+one full pixhip_matmul call: quantize X to Q8_K, then the int8-MFMA GEMM.
+Inputs are resident in HBM before timing starts.
+
+Also reported in the same JSON line: the GEMM kernel alone (the roofline
+object, against the int8 MFMA peak), the quantize pass alone, the M=1 decode
+matvec (Q5_K and Q8_0, W [18944, 3584], 100 repeats rotating >= 1 GiB of weight
+copies so the 256 MB Infinity Cache cannot serve them), and the reference CPU
+path (cpu_quant_matmul) timed on this host on the same inputs.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+
+Progress goes to stderr; stdout carries exactly one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q5_K/Q8_0 GEMM TOPS (% i8 MFMA peak); M=1 matvec GB/s (% HBM peak)"
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+MALL_DEFEAT_BYTES = 1 << 30  # rotate >= 1 GiB of weights per matvec series
+
+GEMM_M, GEMM_K, GEMM_N = 4096, 3840, 10240
+MV_K, MV_N = 3584, 18944
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def row_rel(y, r):
+    y = np.asarray(y, np.float64)
+    r = np.asarray(r, np.float64)
+    return float((np.abs(y - r).max(axis=-1) / np.maximum(np.abs(r).max(axis=-1), 1e-30)).max())
+
+
+class CpuBaseline:
+    """The reference CPU path: oracle/_ref (the reference's own kernels_quant.cpp,
+    built from its sources) when present, else the oracle's C restatement."""
+
+    def __init__(self, threads):
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib
+
+        self.ol = oracle_lib
+        self.threads = threads
+        ref = oracle_lib.reference()
+        if ref is not None:
+            self.kind, self.lib, self.prefix = "reference", ref, "ref"
+            ref.ref_set_threads(threads)
+        else:
+            self.kind, self.lib, self.prefix = "port", oracle_lib.oracle(), "orc"
+
+    def matmul(self, wb, wtype, x, rows):
+        return self.ol.quant_matmul(self.lib, self.prefix, wb, wtype, x, rows, threads=self.threads)
+
+
+def gemm_workload(synth):
+    log("generating Q5_K GEMM inputs (M=4096 K=3840 N=10240)")
+    x = synth.normal(synth.SEED_ACTIVATIONS, (GEMM_M, GEMM_K))
+    ch = synth.outlier_channels(GEMM_K)
+    x[:, ch] *= 20.0
+    w = synth.normal(synth.SEED_WEIGHTS, (GEMM_N, GEMM_K), std=0.02)
+    wb = synth.pack_q5_K(w)
+    del w
+    return x, wb, ch
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--matvec-reps", type=int, default=100)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-matvec", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    from pixelina_amd import Q5_K, Q8_0, Session, _lib, synth
+
+    x, wb, ch = gemm_workload(synth)
+    ops = 2.0 * GEMM_M * GEMM_N * GEMM_K
+    out = {}
+    with Session(0) as sess:
+        device = sess.device_name()
+        log(f"device {device}")
+        w = sess.weight("bench:gemm:q5k", wb, Q5_K, GEMM_K, GEMM_N)
+        xb = sess.to_device(x)
+        yb = sess.alloc(GEMM_M * GEMM_N * 4)
+        both = _lib.STAGE_QUANTIZE | _lib.STAGE_MULTIPLY
+        log(f"warmup {args.warmup} steps")
+        sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, both, max(1, args.warmup))
+        log(f"timing {args.steps} steps (quantize + GEMM)")
+        ms_step = sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, both, args.steps) / args.steps
+        ms_gemm = sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, _lib.STAGE_MULTIPLY, args.steps) / args.steps
+        ms_quant = sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, _lib.STAGE_QUANTIZE, args.steps) / args.steps
+        _lib.check(sess.matmul(w, xb.ptr, GEMM_M, yb.ptr), "pixhip_matmul")
+        y_gpu = yb.download(np.float32, GEMM_M * GEMM_N).reshape(GEMM_M, GEMM_N)
+        log(f"step {ms_step * 1e3:.1f} us, GEMM {ms_gemm * 1e3:.1f} us, quantize {ms_quant * 1e3:.1f} us")
+        xb.free()
+        yb.free()
+
+        matvec = {}
+        if not args.no_matvec:
+            xv = synth.normal(synth.SEED_ACTIVATIONS, (1, MV_K))
+            wv = synth.normal(synth.SEED_WEIGHTS, (MV_N, MV_K), std=0.02)
+            # Q8_0 weights from the HIP quantizer (bit-exact quantize_row_q8_0_ref)
+            wdev = sess.to_device(wv)
+            qdev = sess.alloc(MV_N * MV_K // 32 * 34)
+            _lib.check(sess.quantize_q8_0(wdev.ptr, qdev.ptr, MV_N, MV_K), "quantize weights")
+            wq8 = qdev.download(np.uint8, MV_N * MV_K // 32 * 34).reshape(MV_N, -1)
+            wdev.free()
+            qdev.free()
+            wq5 = synth.pack_q5_K(wv)
+            del wv
+            xvb = sess.to_device(xv)
+            yvb = sess.alloc(MV_N * 4)
+            for name, wtype, wbytes in (("q5_K", Q5_K, wq5), ("q8_0", Q8_0, wq8)):
+                copies = int(np.ceil(MALL_DEFEAT_BYTES / wbytes.nbytes))
+                handles = [sess.weight(f"bench:mv:{name}:{i}", wbytes, wtype, MV_K, MV_N) for i in range(copies)]
+                sess.bench_matmul(handles, xvb.ptr, 1, yvb.ptr, both, copies)
+                ms = sess.bench_matmul(handles, xvb.ptr, 1, yvb.ptr, both, args.matvec_reps) / args.matvec_reps
+                _lib.check(sess.matmul(handles[0], xvb.ptr, 1, yvb.ptr), "matvec")
+                yv = yvb.download(np.float32, MV_N)
+                alg = wbytes.nbytes + 4 * MV_K + 4 * MV_N
+                gbs = alg / (ms * 1e-3) / 1e9
+                log(f"matvec {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s over {copies} weight copies")
+                matvec[name] = {"us": ms * 1e3, "gbs": gbs, "bytes": alg, "copies": copies, "rotated_bytes": copies * wbytes.nbytes,
+                                "y": yv, "w": wbytes, "type": wtype}
+            xvb.free()
+            yvb.free()
+        n_cached, cached_bytes = sess.cache_info()
+        log(f"weight cache: {n_cached} entries, {cached_bytes / 2**30:.2f} GiB")
+
+    tops_step = ops / (ms_step * 1e-3) / 1e12
+    tops_gemm = ops / (ms_gemm * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(tops_step, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: SplitMix64 + Box-Muller, seeds 1337 (X), 1338 (W), 1339 (outlier channels)",
+        "config": {"workload": "Q5_K GEMM M=4096 K=3840 N=10240 (Z-Image DiT FFN), quantize + GEMM per step",
+                   "M": GEMM_M, "K": GEMM_K, "N": GEMM_N, "weight_type": "Q5_K", "activation_type": "Q8_K",
+                   "outlier_channels": int(len(ch)), "device": device},
+        "roofline": {"kernel": "gemm_kernel<Q5_K>", "bound": "mfma", "achieved": round(tops_gemm, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TOP/s", "frac": round(tops_gemm / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "work_per_launch": f"2*M*N*K = {ops:.4e} int8 ops", "avg_launch_us": round(ms_gemm * 1e3, 2)},
+        "gemm_only": {"us": round(ms_gemm * 1e3, 2), "tops": round(tops_gemm, 2)},
+        "quantize": {"us": round(ms_quant * 1e3, 2), "gbs": round((GEMM_M * GEMM_K * 4 + GEMM_M * GEMM_K * 1.14) / (ms_quant * 1e-3) / 1e9, 1)},
+    }
+    if matvec:
+        line["matvec"] = {
+            k: {"workload": f"{k} matvec x[1,{MV_K}] W[{MV_N},{MV_K}], {args.matvec_reps} reps over {v['copies']} copies "
+                            f"({v['rotated_bytes'] / 2**30:.2f} GiB)",
+                "us": round(v["us"], 3), "value": round(v["gbs"], 1), "unit": "GB/s",
+                "roofline": {"bound": "hbm", "achieved": round(v["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": round(v["gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                             "work_per_launch": f"W + 4K + 4N = {v['bytes']} bytes"}}
+            for k, v in matvec.items()}
+
+    if not args.no_cpu:
+        threads = cpu_threads()
+        cpu = CpuBaseline(threads)
+        log(f"CPU baseline ({cpu.kind}, {threads} threads, {cpu_model()})")
+        if cpu.kind == "reference":
+            xs, sample = x, f"full workload M={GEMM_M} N={GEMM_N} K={GEMM_K}, median of 3 after a pool warm-up"
+            cpu.matmul(wb[:64], Q5_K, x[:16], 64)
+            times = []
+            for _ in range(3):
+                t = time.perf_counter()
+                y_cpu = cpu.matmul(wb, Q5_K, xs, GEMM_N)
+                times.append(time.perf_counter() - t)
+            t_cpu = float(np.median(times))
+        else:
+            rows = 256
+            xs, sample = x[:rows], f"first {rows} tokens of the workload (N={GEMM_N} K={GEMM_K}), one run"
+            t = time.perf_counter()
+            y_cpu = cpu.matmul(wb, Q5_K, xs, GEMM_N)
+            t_cpu = time.perf_counter() - t
+        cpu_tops = 2.0 * xs.shape[0] * GEMM_N * GEMM_K / t_cpu / 1e12
+        parity = row_rel(y_gpu[: xs.shape[0]], y_cpu)
+        log(f"CPU {t_cpu:.2f} s -> {cpu_tops * 1e3:.1f} GOPS; GPU vs CPU max row rel err {parity:.2e}")
+        line["cpu_baseline"] = {"value": round(cpu_tops, 5), "unit": "TOPS", "cores": threads, "kind": cpu.kind,
+                                "sample": sample, "seconds": round(t_cpu, 3), "cpu": cpu_model()}
+        line["parity"] = {"max_row_rel_err_vs_cpu": parity, "tolerance": 1e-4, "rows_checked": int(xs.shape[0])}
+        for k, v in matvec.items():
+            reps = args.matvec_reps
+            cpu.matmul(v["w"], v["type"], xv, MV_N)
+            ts = []
+            for _ in range(reps):
+                t = time.perf_counter()
+                yc = cpu.matmul(v["w"], v["type"], xv, MV_N)
+                ts.append(time.perf_counter() - t)
+            tc = float(np.median(ts))
+            err = row_rel(v["y"][None, :], yc)
+            line["matvec"][k]["cpu_baseline"] = {"value": round(v["bytes"] / tc / 1e9, 2), "unit": "GB/s", "cores": threads,
+                                                 "kind": cpu.kind, "sample": f"full matvec, median of {reps}",
+                                                 "us": round(tc * 1e6, 1)}
+            line["matvec"][k]["parity_max_row_rel_err"] = err
+            log(f"CPU matvec {k}: {tc * 1e6:.0f} us; GPU vs CPU rel err {err:.2e}")
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -171,6 +171,13 @@ int pixhip_block_sums(pixhip_session* session, const pixhip_weight* weight, cons
 int pixhip_timer_start(pixhip_session* session);
 int pixhip_timer_stop(pixhip_session* session, float* milliseconds);
 
+/* No reference counterpart (measurement support): enqueues `reps` calls of
+ * pixhip_matmul_stage(weights[i % count], ...) back to back from a C loop and
+ * reports the elapsed stream time between HIP events recorded before the first
+ * and after the last call.  Device pointers only. */
+int pixhip_bench_matmul(pixhip_session* session, const pixhip_weight* const* weights, size_t count, const float* input,
+                        size_t columns, float* output, unsigned stages, size_t reps, float* milliseconds);
+
 /* ---- diagnostics ---- */
 const char* pixhip_last_error(void);
 int pixhip_version(void);

@@ -56,6 +56,8 @@ SIGNATURES = {
     "pixhip_block_sums": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "pixhip_timer_start": (_int, [_vp]),
     "pixhip_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
+    "pixhip_bench_matmul": (_int, [_vp, ctypes.POINTER(_vp), _sz, _vp, _sz, _vp, ctypes.c_uint, _sz,
+                                   ctypes.POINTER(ctypes.c_float)]),
 }
 
 _lib = None

@@ -40,7 +40,8 @@ int hip_fail(hipError_t e, const char* what)
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
-constexpr size_t kTile = 128;        // GEMM tile rows (token and feature padding)
+constexpr size_t kTileN = PIX_GEMM_NTILE;  // GEMM feature-tile rows (weight padding)
+constexpr size_t kTileM = PIX_GEMM_MTILE;  // GEMM token-tile rows (activation padding)
 constexpr size_t kAlign = 256;       // sub-allocation alignment
 constexpr double kHeapFraction = 0.85;  // VULKAN_HEAP_FRACTION, src/backend_vulkan.h:26
 constexpr size_t kMatvecMaxInner = 16384;  // matvec keeps x in LDS (64 units per lane x 4)
@@ -195,31 +196,31 @@ int grow(pixhip_session* s, void** buffer, size_t* have, size_t need)
 // GEMM forms, built on first use from the resident GGUF bytes.
 int ensure_gemm_form(pixhip_session* s, pixhip_weight* w)
 {
-    const size_t N = w->rows, K = w->inner, npad = round_up(N,kTile), nb = K / PIX_QK;
+    const size_t N = w->rows, K = w->inner, npad = round_up(N,kTileN), nb = K / PIX_QK;
     if (w->type == PIX_Q5_K && !w->planes) {
         Carver c;
-        size_t hi = c.take(npad * K), lo = c.take(npad * K), d = c.take(N * nb * 4), dm = c.take(N * nb * 4),
-               mn = c.take(npad * (K / 16) * 2);
+        size_t hi = c.take(npad * K), lo = c.take(npad * K), d = c.take(nb * npad * 4), dm = c.take(nb * npad * 4),
+               mn = c.take(nb * npad * 8 * 2);
         int rc = weight_alloc(s,w,c.offset,&w->planes);
         if (rc) return rc;
         uint8_t* base = static_cast<uint8_t*>(w->planes);
         PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");
         w->q5 = {reinterpret_cast<int8_t*>(base + hi),reinterpret_cast<int8_t*>(base + lo),reinterpret_cast<float*>(base + d),
-                 reinterpret_cast<float*>(base + dm),reinterpret_cast<_Float16*>(base + mn)};
-        PIX_HIP(pixhip::launch_repack_q5_K(static_cast<const uint8_t*>(w->raw),N,K,const_cast<int8_t*>(w->q5.hi),
+                 reinterpret_cast<float*>(base + dm),reinterpret_cast<_Float16*>(base + mn),npad};
+        PIX_HIP(pixhip::launch_repack_q5_K(static_cast<const uint8_t*>(w->raw),N,K,npad,const_cast<int8_t*>(w->q5.hi),
                                            const_cast<int8_t*>(w->q5.lo),const_cast<float*>(w->q5.d),const_cast<float*>(w->q5.dm),
                                            const_cast<_Float16*>(w->q5.mn),s->stream),
                 "repack Q5_K");
     }
     if (w->type == PIX_Q6_K && !w->planes) {
         Carver c;
-        size_t hi = c.take(npad * K), lo = c.take(npad * K), d = c.take(N * nb * 4);
+        size_t hi = c.take(npad * K), lo = c.take(npad * K), d = c.take(nb * npad * 4);
         int rc = weight_alloc(s,w,c.offset,&w->planes);
         if (rc) return rc;
         uint8_t* base = static_cast<uint8_t*>(w->planes);
         PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");
-        w->q6 = {reinterpret_cast<int8_t*>(base + hi),reinterpret_cast<int8_t*>(base + lo),reinterpret_cast<float*>(base + d)};
-        PIX_HIP(pixhip::launch_repack_q6_K_planes(static_cast<const uint8_t*>(w->raw),N,K,const_cast<int8_t*>(w->q6.hi),
+        w->q6 = {reinterpret_cast<int8_t*>(base + hi),reinterpret_cast<int8_t*>(base + lo),reinterpret_cast<float*>(base + d),npad};
+        PIX_HIP(pixhip::launch_repack_q6_K_planes(static_cast<const uint8_t*>(w->raw),N,K,npad,const_cast<int8_t*>(w->q6.hi),
                                                   const_cast<int8_t*>(w->q6.lo),const_cast<float*>(w->q6.d),s->stream),
                 "repack Q6_K planes");
     }
@@ -245,7 +246,7 @@ int ensure_matvec_form(pixhip_session* s, pixhip_weight* w)
 
 int build_q8_0(pixhip_session* s, pixhip_weight* w)
 {
-    const size_t N = w->rows, K = w->inner, npad = round_up(N,kTile), kp = round_up(K,64);
+    const size_t N = w->rows, K = w->inner, npad = round_up(N,kTileN), kp = round_up(K,64);
     Carver c;
     size_t qs = c.take(npad * kp), d = c.take(N * (kp / PIX_QK8) * 2), dT = c.take((kp / PIX_QK8) * npad * 4);
     int rc = weight_alloc(s,w,c.offset,&w->planar);
@@ -296,7 +297,7 @@ bool device_visible(pixhip_session* s, const void* p, const void** dev)
 
 int quantize_stage(pixhip_session* s, const pixhip_weight* w, const float* x, size_t columns)
 {
-    const size_t K = w->inner, mpad = round_up(columns,kTile);
+    const size_t K = w->inner, mpad = round_up(columns,kTileM);
     if (w->type == PIX_Q8_0) {
         const size_t kp = round_up(K,64);
         Carver c;
@@ -749,6 +750,25 @@ int pixhip_timer_stop(pixhip_session* s, float* ms)
 {
     int rc = use_device(s);
     if (rc) return rc;
+    PIX_HIP(hipEventRecord(s->t1,s->stream),"hipEventRecord");
+    PIX_HIP(hipEventSynchronize(s->t1),"hipEventSynchronize");
+    float v = 0;
+    PIX_HIP(hipEventElapsedTime(&v,s->t0,s->t1),"hipEventElapsedTime");
+    if (ms) *ms = v;
+    return PIXHIP_OK;
+}
+
+int pixhip_bench_matmul(pixhip_session* s, const pixhip_weight* const* weights, size_t count, const float* input, size_t columns,
+                        float* output, unsigned stages, size_t reps, float* ms)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!weights || !count || !reps) return fail(PIXHIP_ERR_ARGUMENT,"empty benchmark");
+    PIX_HIP(hipEventRecord(s->t0,s->stream),"hipEventRecord");
+    for (size_t i = 0; i < reps; i++) {
+        rc = run(s,weights[i % count],input,columns,output,nullptr,0,0,stages,false);
+        if (rc) return rc;
+    }
     PIX_HIP(hipEventRecord(s->t1,s->stream),"hipEventRecord");
     PIX_HIP(hipEventSynchronize(s->t1),"hipEventSynchronize");
     float v = 0;

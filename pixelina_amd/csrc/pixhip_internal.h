@@ -8,17 +8,21 @@
 //   activations, Q8_K ("act8k"), M rows of K values:
 //     qs   int8   [M][K]          quantized values
 //     d    fp32   [K/256][Mpad]   block scale, super-block-major
-//     bs   fp16   [M][K/16]       sums of 16 quantized values (exact, |s| <= 2032)
+//     bs   fp16   [M][K/16]       sums of 16 quantized values (exact, |s| <= 2032),
+//                                 within each super-block in the order 0,2,..,14,1,3,..,15
+//                                 (even groups, then odd: the min-term MFMA operand order)
 //   activations, Q8_0 ("act80"), rows of Kp = K rounded up to 64 (a zero pad block):
 //     qs   int8   [M][Kp]
 //     d    fp32   [Kp/32][Mpad]   fp16-rounded block scale widened to fp32
-//   weights Q5_K for the GEMM ("planes"), N rows:
-//     hi   int8   [N][K]          (scale_s * q) >> 6
-//     lo   int8   [N][K]          (scale_s * q) & 63
-//     d    fp32   [N][K/256]      super-block scale d
-//     dm   fp32   [N][K/256]      super-block dmin
-//     mn   fp16   [N][K/16]       six-bit minimum of the 32-value sub-block, once per 16 values
-//   weights Q6_K for the GEMM: hi/lo of scale*(q-32) = 64*hi + lo, d fp32 [N][K/256]
+//   Activations are allocated with Mpad rows (multiple of PIX_GEMM_MTILE) and
+//   GEMM weight forms with Npad rows (multiple of PIX_GEMM_NTILE).
+//   weights Q5_K for the GEMM ("planes"), N rows padded to Npad:
+//     hi   int8   [Npad][K]         (scale_s * q) >> 6
+//     lo   int8   [Npad][K]         (scale_s * q) & 63
+//     d    fp32   [K/256][Npad]     super-block scale d
+//     dm   fp32   [K/256][Npad]     super-block dmin
+//     mn   fp16   [K/256][Npad][8]  the eight six-bit sub-block minima
+//   weights Q6_K for the GEMM: hi/lo of scale*(q-32) = 64*hi + lo, d fp32 [K/256][Npad]
 //   weights Q8_0 ("planar", GEMM and matvec), rows of Kp with a zero pad block:
 //     qs int8 [Npad][Kp], d fp16 [N][Kp/32], and for the GEMM the same scales
 //     widened and transposed, dT fp32 [Kp/32][Npad]
@@ -41,6 +45,8 @@
 #define PIX_Q8_K_BYTES 292
 #define PIX_Q5_K_BYTES 176
 #define PIX_Q6_K_BYTES 210
+#define PIX_GEMM_MTILE 256  // GEMM workgroup tile: tokens
+#define PIX_GEMM_NTILE 128  // GEMM workgroup tile: output features
 
 namespace pixhip {
 
@@ -63,12 +69,14 @@ struct PlanesQ5K {
     const float* d;
     const float* dm;
     const _Float16* mn;
+    size_t npad;
 };
 
 struct PlanesQ6K {
     const int8_t* hi;
     const int8_t* lo;
     const float* d;
+    size_t npad;
 };
 
 struct PlanarQ80 {
@@ -97,9 +105,10 @@ hipError_t launch_quantize_q8_0(const float* x, size_t rows, size_t inner, size_
                                 hipStream_t s);
 
 // repack.hip
-hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, int8_t* hi, int8_t* lo, float* d, float* dm,
-                              _Float16* mn, hipStream_t s);
-hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inner, int8_t* hi, int8_t* lo, float* d, hipStream_t s);
+hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
+                              float* dm, _Float16* mn, hipStream_t s);
+hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
+                                     hipStream_t s);
 hipError_t launch_repack_q6_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* ql, uint8_t* qh, int8_t* sc,
                                      _Float16* d, hipStream_t s);
 hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, size_t kpad, size_t rows_pad, int8_t* qs, _Float16* d,

@@ -32,7 +32,9 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_K_kernel(const f
     if (qs) {
         reinterpret_cast<uint32_t*>(qs + row * inner + b * PIX_QK)[lane] = packed;
         if (lane == 0) dT[b * mpad + row] = d;
-        if ((lane & 3) == 0) bs[row * (inner / 16) + b * 16 + (lane >> 2)] = (_Float16)(float)gsum;
+        // group t = lane/4 stored at (t&1)*8 + t/2: even groups first, then odd
+        const int t = lane >> 2;
+        if ((lane & 3) == 0) bs[row * (inner / 16) + b * 16 + (t & 1) * 8 + (t >> 1)] = (_Float16)(float)gsum;
     }
     if (blocks) {
         uint8_t* blk = blocks + block * PIX_Q8_K_BYTES;

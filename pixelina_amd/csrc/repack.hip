@@ -26,7 +26,7 @@ __device__ __forceinline__ uint32_t load_u32_bytes(const uint8_t* p)
 
 // One wave per Q5_K super-block; lane l converts values 4l..4l+3 (sub-block l/8).
 __global__ __launch_bounds__(256) void repack_q5_K_kernel(const uint8_t* __restrict__ raw, size_t rows, size_t inner,
-                                                          int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                          size_t npad, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                           float* __restrict__ d, float* __restrict__ dm,
                                                           _Float16* __restrict__ mn)
 {
@@ -55,14 +55,10 @@ __global__ __launch_bounds__(256) void repack_q5_K_kernel(const uint8_t* __restr
     *reinterpret_cast<uint32_t*>(hi + off) = pack_bytes(h[0],h[1],h[2],h[3]);
     *reinterpret_cast<uint32_t*>(lo + off) = pack_bytes(l[0],l[1],l[2],l[3]);
     if (lane == 0) {
-        d[row * nb + b] = half_bits_to_float((uint16_t)(head & 0xffffu));
-        dm[row * nb + b] = half_bits_to_float((uint16_t)(head >> 16));
+        d[b * npad + row] = half_bits_to_float((uint16_t)(head & 0xffffu));
+        dm[b * npad + row] = half_bits_to_float((uint16_t)(head >> 16));
     }
-    if (lane < 16) {
-        int sc2, mn2;
-        q5_scale_min(w0,w1,w2,lane >> 1,sc2,mn2);
-        mn[row * (inner / 16) + b * 16 + lane] = (_Float16)(float)mn2;
-    }
+    if ((lane & 7) == 0) mn[(b * npad + row) * 8 + s] = (_Float16)(float)min;
 }
 
 // Q6_K value d*scale_{e/16}*(q-32) (src/backend_cpu.cpp:80-96): p = scale*(q-32)
@@ -76,7 +72,7 @@ __device__ __forceinline__ int q6_raw_value(const uint8_t* src, int e)
 }
 
 __global__ __launch_bounds__(256) void repack_q6_K_planes_kernel(const uint8_t* __restrict__ raw, size_t rows, size_t inner,
-                                                                 int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                                 size_t npad, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                                  float* __restrict__ d)
 {
     const size_t nb = inner / PIX_QK;
@@ -97,7 +93,7 @@ __global__ __launch_bounds__(256) void repack_q6_K_planes_kernel(const uint8_t* 
     const size_t off = row * inner + b * PIX_QK + 4 * lane;
     *reinterpret_cast<uint32_t*>(hi + off) = pack_bytes(h[0],h[1],h[2],h[3]);
     *reinterpret_cast<uint32_t*>(lo + off) = pack_bytes(l[0],l[1],l[2],l[3]);
-    if (lane == 0) d[row * nb + b] = half_bits_to_float((uint16_t)(src[208] | (src[209] << 8)));
+    if (lane == 0) d[b * npad + row] = half_bits_to_float((uint16_t)(src[208] | (src[209] << 8)));
 }
 
 // Q6_K re-sliced into aligned planes of identical total size (matvec input).
@@ -144,20 +140,21 @@ __global__ __launch_bounds__(256) void repack_q8_0_kernel(const uint8_t* __restr
 
 static unsigned waves_grid(size_t blocks) { return (unsigned)((blocks + 3) / 4); }
 
-hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, int8_t* hi, int8_t* lo, float* d, float* dm,
-                              _Float16* mn, hipStream_t s)
+hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
+                              float* dm, _Float16* mn, hipStream_t s)
 {
     size_t blocks = rows * (inner / PIX_QK);
     if (!blocks) return hipSuccess;
-    repack_q5_K_kernel<<<waves_grid(blocks),256,0,s>>>(raw,rows,inner,hi,lo,d,dm,mn);
+    repack_q5_K_kernel<<<waves_grid(blocks),256,0,s>>>(raw,rows,inner,npad,hi,lo,d,dm,mn);
     return hipGetLastError();
 }
 
-hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inner, int8_t* hi, int8_t* lo, float* d, hipStream_t s)
+hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
+                                     hipStream_t s)
 {
     size_t blocks = rows * (inner / PIX_QK);
     if (!blocks) return hipSuccess;
-    repack_q6_K_planes_kernel<<<waves_grid(blocks),256,0,s>>>(raw,rows,inner,hi,lo,d);
+    repack_q6_K_planes_kernel<<<waves_grid(blocks),256,0,s>>>(raw,rows,inner,npad,hi,lo,d);
     return hipGetLastError();
 }
 

@@ -113,6 +113,13 @@ class Session:
     def timer_start(self):
         check(self.lib.pixhip_timer_start(self.handle), "pixhip_timer_start")
 
+    def bench_matmul(self, weights, x_ptr, columns, y_ptr, stages, reps):
+        arr = (ctypes.c_void_p * len(weights))(*weights)
+        ms = ctypes.c_float()
+        check(self.lib.pixhip_bench_matmul(self.handle, arr, len(weights), x_ptr, columns, y_ptr, stages, reps,
+                                           ctypes.byref(ms)), "pixhip_bench_matmul")
+        return ms.value
+
     def timer_stop(self):
         ms = ctypes.c_float()
         check(self.lib.pixhip_timer_stop(self.handle, ctypes.byref(ms)), "pixhip_timer_stop")
