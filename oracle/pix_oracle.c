@@ -18,7 +18,20 @@
  * Everything else is evaluated exactly as written (no other contraction).
  *
  * Build: gcc -std=c11 -O2 -ffp-contract=off (oracle/Makefile).
+ *
+ * ORC_MUTANT (default 0) plants one plausible mistake per value, for the
+ * tests that show the golden vectors catch it (tests/test_oracle_pins.py
+ * compiles such copies into a temporary directory; nothing else sets it):
+ *   1 nearest_int rounded after a separate multiply (no fused multiply-add)
+ *   2 hsum8 summed left to right
+ *   3 Q5_K min term accumulated without the fused multiply-add
+ *   4 Q8_0 quantizer dividing by the fp16-rounded scale
+ *   5 Q5_K six-bit unpack of sub-blocks 4..7 taking the wrong high bits
+ *   6 Q8_K quantizer keeping the last (not the first) largest |x|
  */
+#ifndef ORC_MUTANT
+#define ORC_MUTANT 0
+#endif
 #include "pix_oracle.h"
 
 #include <math.h>
@@ -76,7 +89,12 @@ uint16_t orc_float_to_half(float f)
  * bits(fma(scale, x, 1.5*2^23)) & 0x7fffff - 0x400000. */
 int orc_nearest_int_fused(float scale, float x)
 {
+#if ORC_MUTANT == 1
+    float p = scale * x;
+    float v = p + 12582912.0f;
+#else
     float v = fmaf(scale,x,12582912.0f);
+#endif
     int32_t i;
     memcpy(&i,&v,4);
     return (i & 0x007fffff) - 0x00400000;
@@ -102,6 +120,9 @@ void orc_quantize_q8_0(const float* x, void* blocks, int64_t k)
         }
         float d = amax / 127.0f;
         float id = (d != 0.0f)? 1.0f / d : 0.0f;
+#if ORC_MUTANT == 4
+        id = (d != 0.0f)? 1.0f / orc_half_to_float(orc_float_to_half(d)) : 0.0f;
+#endif
         wr16(y,orc_float_to_half(d));
         for (int j = 0; j < QK8_0; j++) {
             float x0 = x[j] * id;
@@ -119,7 +140,11 @@ void orc_quantize_q8_K(const float* x, void* blocks, int64_t k)
         float max = 0, amax = 0;
         for (int j = 0; j < QK_K; j++) {
             float ax = fabsf(x[j]);
+#if ORC_MUTANT == 6
+            if (ax >= amax && ax > 0.0f) {
+#else
             if (ax > amax) {
+#endif
                 amax = ax;
                 max = x[j];
             }
@@ -148,6 +173,9 @@ void orc_quantize_q8_K(const float* x, void* blocks, int64_t k)
  * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)). */
 static float hsum8(const float a[8])
 {
+#if ORC_MUTANT == 2
+    return ((((((a[0] + a[1]) + a[2]) + a[3]) + a[4]) + a[5]) + a[6]) + a[7];
+#endif
     float r0 = a[4] + a[0], r1 = a[5] + a[1], r2 = a[6] + a[2], r3 = a[7] + a[3];
     float s0 = r0 + r2, s1 = r1 + r3;
     return s0 + s1;
@@ -199,7 +227,11 @@ static void q5_scales(const uint8_t* sc, int scale[8], int min[8])
             scale[s] = sc[s] & 63;
             min[s] = sc[s + 4] & 63;
         } else {
+#if ORC_MUTANT == 5
+            scale[s] = (sc[s + 4] & 15) | ((sc[s - 4] >> 4 & 3) << 4);
+#else
             scale[s] = (sc[s + 4] & 15) | ((sc[s - 4] >> 6) << 4);
+#endif
             min[s] = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
         }
     }
@@ -233,7 +265,11 @@ float orc_dot_q5_K(int n, const void* wv, const void* av)
             int16_t pair = (int16_t)(int16_t)((int16_t)rd16(bs + 4 * s) + (int16_t)rd16(bs + 4 * s + 2));
             isum += min[s] * pair;
         }
+#if ORC_MUTANT == 3
+        summs = summs + dmin * (float)isum;
+#else
         summs = fmaf(dmin,(float)isum,summs);
+#endif
         int32_t sumi[8] = {0};
         for (int j = 0; j < 4; j++) {
             for (int half = 0; half < 2; half++) {

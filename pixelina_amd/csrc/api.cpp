@@ -462,7 +462,9 @@ int pixhip_session_create(int device, pixhip_session** out)
         return rc;
     }
     s->stream = s->own_stream;
-    s->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    // hipDeviceProp_t::name can be empty (no marketing name in the driver's
+    // table); fall back to the architecture name alone.
+    s->name = prop.name[0]? std::string(prop.name) + " (" + prop.gcnArchName + ")" : std::string(prop.gcnArchName);
     s->total_memory = prop.totalGlobalMem;
     s->heap_limit = (size_t)(kHeapFraction * (double)prop.totalGlobalMem);
     s->cache_limit = s->heap_limit;

@@ -21,32 +21,38 @@ _oracle = None
 _ref = None
 
 
+def load_oracle(path):
+    """ctypes handle on an oracle build at `path` (the default build, or a
+    copy compiled with ORC_MUTANT by the tests that plant mistakes)."""
+    lib = ctypes.CDLL(path)
+    sig = {
+        "orc_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
+        "orc_float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
+        "orc_nearest_int_fused": (_int, [ctypes.c_float, ctypes.c_float]),
+        "orc_quantize_q8_0": (None, [_vp, _vp, _i64]),
+        "orc_quantize_q8_K": (None, [_vp, _vp, _i64]),
+        "orc_dot_q8_0": (ctypes.c_float, [_int, _vp, _vp]),
+        "orc_dot_q5_K": (ctypes.c_float, [_int, _vp, _vp]),
+        "orc_dot_q6_K": (ctypes.c_float, [_int, _vp, _vp]),
+        "orc_block_sums_q8_0": (ctypes.c_int32, [_vp, _vp]),
+        "orc_superblock_sums_q5_K": (None, [_vp, _vp, _vp, _vp]),
+        "orc_superblock_sum_q6_K": (ctypes.c_int32, [_vp, _vp]),
+        "orc_quant_matmul": (_int, [_vp, _u32, _vp, _vp, _sz, _sz, _sz, _int]),
+        "orc_decode": (None, [_vp, _u32, _sz, _vp]),
+        "orc_row_bytes": (ctypes.c_uint64, [ctypes.c_uint64, _u32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    return lib
+
+
 def oracle():
     global _oracle
     if _oracle is None:
         if not os.path.exists(ORACLE_SO):
             subprocess.run(["make", "-C", ORACLE_DIR, "oracle"], check=True, capture_output=True)
-        lib = ctypes.CDLL(ORACLE_SO)
-        sig = {
-            "orc_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
-            "orc_float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
-            "orc_nearest_int_fused": (_int, [ctypes.c_float, ctypes.c_float]),
-            "orc_quantize_q8_0": (None, [_vp, _vp, _i64]),
-            "orc_quantize_q8_K": (None, [_vp, _vp, _i64]),
-            "orc_dot_q8_0": (ctypes.c_float, [_int, _vp, _vp]),
-            "orc_dot_q5_K": (ctypes.c_float, [_int, _vp, _vp]),
-            "orc_dot_q6_K": (ctypes.c_float, [_int, _vp, _vp]),
-            "orc_block_sums_q8_0": (ctypes.c_int32, [_vp, _vp]),
-            "orc_superblock_sums_q5_K": (None, [_vp, _vp, _vp, _vp]),
-            "orc_superblock_sum_q6_K": (ctypes.c_int32, [_vp, _vp]),
-            "orc_quant_matmul": (_int, [_vp, _u32, _vp, _vp, _sz, _sz, _sz, _int]),
-            "orc_decode": (None, [_vp, _u32, _sz, _vp]),
-            "orc_row_bytes": (ctypes.c_uint64, [ctypes.c_uint64, _u32]),
-        }
-        for name, (res, args) in sig.items():
-            fn = getattr(lib, name)
-            fn.restype, fn.argtypes = res, args
-        _oracle = lib
+        _oracle = load_oracle(ORACLE_SO)
     return _oracle
 
 

@@ -1,0 +1,285 @@
+"""Pins on the oracle that do not depend on the reference's vectors: closed
+forms (IEEE fp16 conversion, exact rounding, the two quantizers written out in
+numpy), brute-force integer sums from a second, independent numpy decoder of
+the block formats, the fp64 value of whole dot products, and planted mistakes
+(the oracle compiled with ORC_MUTANT) that the golden vectors must catch."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, dot, load_oracle, oracle, ptr, quant_matmul, quantize)
+from pixelina_amd import synth
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ---- fp16 and rounding ----
+
+def test_half_to_float_exhaustive():
+    lib = oracle()
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([lib.orc_half_to_float(int(v)) for v in h], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_float_to_half_round_to_nearest_even():
+    lib = oracle()
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        (rng.standard_normal(4000) * np.exp2(rng.integers(-30, 20, 4000))).astype(np.float32),
+        np.array([65504.0, 65519.99, 65520.0, 1e6, -1e6, 5.96e-8, 2.98e-8, 2.99e-8, 0.0, -0.0, np.inf, -np.inf],
+                 dtype=np.float32),
+        # exact ties between two fp16 neighbours (even and odd mantissas)
+        (np.float32(1.0) + np.float32(2.0 ** -11) * np.arange(1, 40, 2)).astype(np.float32),
+    ])
+    got = np.array([lib.orc_float_to_half(float(v)) for v in x], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    assert np.isnan(np.uint16(lib.orc_float_to_half(float("nan"))).view(np.float16))
+
+
+def test_fused_nearest_int_is_exact_round_half_even():
+    lib = oracle()
+    rng = np.random.default_rng(6)
+    s = (rng.standard_normal(3000) * 50).astype(np.float32)
+    x = (rng.standard_normal(3000) * 3).astype(np.float32)
+    want = np.rint(s.astype(np.float64) * x.astype(np.float64)).astype(np.int64)
+    got = np.array([lib.orc_nearest_int_fused(float(a), float(b)) for a, b in zip(s, x)], dtype=np.int64)
+    assert np.array_equal(got, want)
+    # exact halves round to even
+    for a, b, r in [(1.0, 2.5, 2), (1.0, 3.5, 4), (-1.0, 2.5, -2), (0.5, 5.0, 2)]:
+        assert lib.orc_nearest_int_fused(a, b) == r
+
+
+# ---- the quantizers, written out ----
+
+def q8_K_closed_form(x):
+    """quantize_row_q8_K_ref (src/kernels_quant.cpp:80-118) in numpy, rows of 256."""
+    out = []
+    for blk in x.reshape(-1, 256):
+        ax = np.abs(blk)
+        j = int(np.argmax(ax))  # first index of the largest |x|
+        b = np.zeros(292, np.uint8)
+        if ax[j] == 0:
+            out.append(b)
+            continue
+        iscale = np.float32(-127.0) / blk[j]
+        q = np.minimum(127, np.rint(np.float64(iscale) * blk.astype(np.float64))).astype(np.int64)
+        b[0:4] = np.array([np.float32(1.0) / iscale], np.float32).view(np.uint8)
+        b[4:260] = q.astype(np.int8).view(np.uint8)
+        b[260:292] = q.reshape(16, 16).sum(1).astype(np.int16).view(np.uint8)
+        out.append(b)
+    return np.concatenate(out)
+
+
+def q8_0_closed_form(x):
+    """quantize_row_q8_0_ref (src/kernels_quant.cpp:120-144) in numpy, rows of 32."""
+    out = []
+    for blk in x.reshape(-1, 32):
+        amax = np.float32(np.max(np.abs(blk)))
+        d = amax / np.float32(127.0)
+        idv = np.float32(1.0) / d if d != 0 else np.float32(0.0)
+        v = (blk * idv).astype(np.float32).astype(np.float64)
+        q = np.trunc(v + np.copysign(0.5, v)).astype(np.int64)  # roundf: half away from zero
+        b = np.zeros(34, np.uint8)
+        b[0:2] = np.array([d], np.float32).astype(np.float16).view(np.uint8)
+        b[2:] = (q & 0xFF).astype(np.uint8)
+        out.append(b)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("scale", [1e-4, 1.0, 300.0])
+def test_quantizers_equal_closed_forms(scale):
+    rng = np.random.default_rng(int(scale * 10) + 1)
+    x = (rng.standard_normal((8, 512)) * scale).astype(np.float32)
+    x[1, 7] = -x[1, 7] * 9  # a dominant negative entry
+    x[2, :] = 0.0
+    x[3, 20], x[3, 300] = 4 * scale, -4 * scale  # |max| ties across blocks and signs
+    lib = oracle()
+    for r in range(len(x)):
+        assert np.array_equal(quantize(lib, "orc", x[r:r + 1], "q8_K")[0], q8_K_closed_form(x[r])), r
+        assert np.array_equal(quantize(lib, "orc", x[r:r + 1], "q8_0")[0], q8_0_closed_form(x[r])), r
+
+
+# ---- a second decoder of the block formats (numpy) ----
+
+def f16(b, off):
+    return b[..., off:off + 2].copy().view(np.float16)[..., 0].astype(np.float64)
+
+
+def q5_K_ints(blocks):
+    """-> d, dmin [nb], scale, min [nb, 8], q [nb, 256] for 176-byte blocks."""
+    b = blocks.reshape(-1, 176)
+    sc = b[:, 4:16].astype(np.int64)
+    scale = np.zeros((len(b), 8), np.int64)
+    mn = np.zeros((len(b), 8), np.int64)
+    for s in range(8):
+        if s < 4:
+            scale[:, s] = sc[:, s] & 63
+            mn[:, s] = sc[:, s + 4] & 63
+        else:
+            scale[:, s] = (sc[:, s + 4] & 15) | ((sc[:, s - 4] >> 6) << 4)
+            mn[:, s] = (sc[:, s + 4] >> 4) | ((sc[:, s] >> 6) << 4)
+    qh = b[:, 16:48].astype(np.int64)
+    qs = b[:, 48:176].astype(np.int64)
+    q = np.zeros((len(b), 256), np.int64)
+    for s in range(8):
+        low = (qs[:, (s // 2) * 32:(s // 2) * 32 + 32] >> (4 * (s % 2))) & 15
+        q[:, 32 * s:32 * s + 32] = low | (((qh >> s) & 1) << 4)
+    return f16(b, 0), f16(b, 2), scale, mn, q
+
+
+def q6_K_ints(blocks):
+    """-> d [nb], scale [nb, 16] (int8), q - 32 [nb, 256] for 210-byte blocks."""
+    b = blocks.reshape(-1, 210)
+    ql = b[:, 0:128].astype(np.int64)
+    qh = b[:, 128:192].astype(np.int64)
+    sc = b[:, 192:208].view(np.int8).astype(np.int64)
+    q = np.zeros((len(b), 256), np.int64)
+    for e in range(256):
+        h, r = divmod(e, 128)
+        g, i = divmod(r, 32)
+        low = ql[:, 64 * h + i + 32 * (g % 2)]
+        low = (low & 15) if g < 2 else (low >> 4)
+        q[:, e] = low | (((qh[:, 32 * h + i] >> (2 * g)) & 3) << 4)
+    return f16(b, 208), sc, q - 32
+
+
+def q8_K_ints(blocks):
+    b = blocks.reshape(-1, 292)
+    return (b[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64), b[:, 4:260].view(np.int8).astype(np.int64),
+            b[:, 260:292].copy().view(np.int16).astype(np.int64))
+
+
+def weights(rng, rows, k):
+    return (rng.standard_normal((rows, k)) * 0.02).astype(np.float32)
+
+
+def test_second_decoder_agrees_with_oracle_decode():
+    rng = np.random.default_rng(21)
+    w = weights(rng, 3, 512)
+    lib = oracle()
+    for wtype, blocks in ((Q5_K, synth.pack_q5_K(w)), (Q6_K, synth.pack_q6_K(w))):
+        out = np.zeros(3 * 512)
+        lib.orc_decode(ptr(np.ascontiguousarray(blocks)), wtype, out.size, ptr(out))
+        if wtype == Q5_K:
+            d, dm, sc, mn, q = q5_K_ints(blocks)
+            ours = d[:, None] * np.repeat(sc, 32, 1) * q - dm[:, None] * np.repeat(mn, 32, 1)
+        else:
+            d, sc, q = q6_K_ints(blocks)
+            ours = d[:, None] * np.repeat(sc, 16, 1) * q
+        assert np.allclose(out, ours.reshape(-1), rtol=0, atol=1e-12)
+        # and the packers keep the weights within their quantization step
+        assert np.max(np.abs(out - w.reshape(-1))) < 0.1 * np.max(np.abs(w))
+
+
+def test_integer_sums_brute_force():
+    rng = np.random.default_rng(22)
+    lib = oracle()
+    x = (rng.standard_normal((2, 768)) * 3).astype(np.float32)
+    w = weights(rng, 2, 768)
+    a8k = quantize(lib, "orc", x, "q8_K")
+    ad, aq, abs_ = q8_K_ints(a8k)
+    assert np.array_equal(aq.reshape(-1, 16, 16).sum(2), abs_)
+    for blocks, kind in ((synth.pack_q5_K(w), Q5_K), (synth.pack_q6_K(w), Q6_K)):
+        size = 176 if kind == Q5_K else 210
+        ints = q5_K_ints(blocks) if kind == Q5_K else q6_K_ints(blocks)
+        for sb in range(blocks.size // size):
+            wb = np.ascontiguousarray(blocks.reshape(-1)[sb * size:(sb + 1) * size])
+            ab = np.ascontiguousarray(a8k.reshape(-1)[sb * 292:(sb + 1) * 292])
+            if kind == Q5_K:
+                _, _, sc, mn, q = ints
+                want_s = int(sum(sc[sb, s] * np.dot(q[sb, 32 * s:32 * s + 32], aq[sb, 32 * s:32 * s + 32]) for s in range(8)))
+                want_m = int(sum(mn[sb, s] * (abs_[sb, 2 * s] + abs_[sb, 2 * s + 1]) for s in range(8)))
+                got_s, got_m = np.zeros(1, np.int32), np.zeros(1, np.int32)
+                lib.orc_superblock_sums_q5_K(ptr(wb), ptr(ab), ptr(got_s), ptr(got_m))
+                assert (int(got_s[0]), int(got_m[0])) == (want_s, want_m)
+            else:
+                _, sc, q = ints
+                want = int(np.dot(np.repeat(sc[sb], 16) * q[sb], aq[sb]))
+                assert lib.orc_superblock_sum_q6_K(ptr(wb), ptr(ab)) == want
+    a80 = quantize(lib, "orc", x, "q8_0").reshape(-1, 34)
+    w80 = quantize(lib, "orc", w, "q8_0").reshape(-1, 34)
+    for b in range(len(a80)):
+        want = int(np.dot(w80[b, 2:].view(np.int8).astype(np.int64), a80[b, 2:].view(np.int8).astype(np.int64)))
+        assert lib.orc_block_sums_q8_0(ptr(np.ascontiguousarray(w80[b])), ptr(np.ascontiguousarray(a80[b]))) == want
+
+
+@pytest.mark.parametrize("wtype", [Q8_0, Q5_K, Q6_K])
+def test_dot_equals_fp64_dequantized_sum(wtype):
+    rng = np.random.default_rng(23 + wtype)
+    k = 1024
+    lib = oracle()
+    x = (rng.standard_normal((4, k))).astype(np.float32)
+    w = weights(rng, 4, k)
+    if wtype == Q8_0:
+        wb, ab = quantize(lib, "orc", w, "q8_0"), quantize(lib, "orc", x, "q8_0")
+    else:
+        wb = synth.pack_q5_K(w) if wtype == Q5_K else synth.pack_q6_K(w)
+        ab = quantize(lib, "orc", x, "q8_K")
+    for r in range(4):
+        wv = np.zeros(k)
+        lib.orc_decode(ptr(np.ascontiguousarray(wb[r])), wtype, k, ptr(wv))
+        if wtype == Q8_0:
+            blk = ab[r].reshape(-1, 34)
+            av = (f16(blk, 0)[:, None] * blk[:, 2:].view(np.int8)).reshape(-1)
+            # the reference multiplies the two fp16 scales first, in fp32
+            terms = wv * av
+        else:
+            d, q, _ = q8_K_ints(ab[r])
+            av = (d[:, None] * q).reshape(-1)
+            terms = wv * av
+        got = dot(lib, "orc", wtype, wb[r], ab[r], k)
+        assert abs(got - terms.sum()) <= 2e-6 * np.abs(terms).sum() + 1e-30
+
+
+# ---- planted mistakes ----
+
+MUTANTS = {
+    1: "nearest_int without the fused multiply-add",
+    2: "hsum8 summed left to right",
+    3: "Q5_K min term without the fused multiply-add",
+    4: "Q8_0 quantizer dividing by the fp16 scale",
+    5: "Q5_K six-bit unpack, wrong high bits for sub-blocks 4..7",
+    6: "Q8_K quantizer keeping the last largest |x|",
+}
+
+
+def golden_mismatches(lib):
+    """How many golden comparisons an oracle build fails."""
+    bad = 0
+    g1 = np.load(os.path.join(GOLDEN, "g1_quantize_q8_0.npz"))
+    bad += int(not np.array_equal(quantize(lib, "orc", g1["x"], "q8_0"), g1["blocks"]))
+    g2 = np.load(os.path.join(GOLDEN, "g2_quantize_q8_K.npz"))
+    bad += int(not np.array_equal(quantize(lib, "orc", g2["x"], "q8_K"), g2["blocks"]))
+    g3 = np.load(os.path.join(GOLDEN, "g3_dots.npz"))
+    for wname, wtype in (("q8_0", Q8_0), ("q5_K", Q5_K), ("q6_K", Q6_K)):
+        for k in (256, 512, 3840):
+            w, a, y = g3[f"{wname}_{k}_w"], g3[f"{wname}_{k}_a"], g3[f"{wname}_{k}_y"]
+            got = np.array([dot(lib, "orc", wtype, w[i], a[i], k) for i in range(len(y))], np.float32)
+            bad += int(not np.array_equal(got.view(np.uint32), y.view(np.uint32)))
+    g4 = np.load(os.path.join(GOLDEN, "g4_matmul.npz"))
+    for c in range(int(g4["count"])):
+        wtype, m, n, k = (int(v) for v in g4[f"c{c}_shape"])
+        y = quant_matmul(lib, "orc", g4[f"c{c}_w"], wtype, g4[f"c{c}_x"], n, threads=2)
+        bad += int(not np.array_equal(y.view(np.uint32), g4[f"c{c}_y"].view(np.uint32)))
+    return bad
+
+
+def test_unmutated_oracle_passes_every_golden_comparison():
+    assert golden_mismatches(oracle()) == 0
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_golden_vectors_catch_planted_mistake(mutant, tmp_path):
+    so = tmp_path / f"liboracle_m{mutant}.so"
+    subprocess.run(["gcc", "-std=c11", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", "-pthread",
+                    f"-DORC_MUTANT={mutant}", os.path.join(ORACLE_DIR, "pix_oracle.c"), "-o", str(so), "-lm"],
+                   check=True, capture_output=True)
+    assert golden_mismatches(load_oracle(str(so))) > 0, MUTANTS[mutant]
