@@ -32,6 +32,7 @@ METRIC = "Q5_K/Q8_0 GEMM TOPS (% i8 MFMA peak); M=1 matvec GB/s (% HBM peak)"
 PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 MALL_DEFEAT_BYTES = 1 << 30  # rotate >= 1 GiB of weights per matvec series
+COPY_BYTES = 1 << 29  # the plain copy that calibrates the HBM byte counters
 
 GEMM_M, GEMM_K, GEMM_N = 4096, 3840, 10240
 MV_K, MV_N = 3584, 18944
@@ -87,6 +88,18 @@ class CpuBaseline:
         return self.ol.quant_matmul(self.lib, self.prefix, wb, wtype, x, rows, threads=self.threads)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/hbm_traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
+    a plain copy of known size), or None when it has not been measured."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def gemm_workload(synth):
     log("generating Q5_K GEMM inputs (M=4096 K=3840 N=10240)")
     x = synth.normal(synth.SEED_ACTIVATIONS, (GEMM_M, GEMM_K))
@@ -106,6 +119,8 @@ def main():
     ap.add_argument("--matvec-reps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one plain 512 MiB device copy (the calibration kernel for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -164,6 +179,13 @@ def main():
                                 "y": yv, "w": wbytes, "type": wtype}
             xvb.free()
             yvb.free()
+        if args.calibrate_copy:
+            src, dst = sess.alloc(COPY_BYTES), sess.alloc(COPY_BYTES)
+            sess.copy_device(dst.ptr, src.ptr, COPY_BYTES)
+            sess.synchronize()
+            log(f"calibration copy: {COPY_BYTES >> 20} MiB read + {COPY_BYTES >> 20} MiB written (copy16_kernel)")
+            src.free()
+            dst.free()
         n_cached, cached_bytes = sess.cache_info()
         log(f"weight cache: {n_cached} entries, {cached_bytes / 2**30:.2f} GiB")
 
@@ -186,7 +208,7 @@ def main():
                    "M": GEMM_M, "K": GEMM_K, "N": GEMM_N, "weight_type": "Q5_K", "activation_type": "Q8_K",
                    "outlier_channels": int(len(ch)), "device": device},
         "roofline": {"kernel": "gemm_kernel<Q5_K>", "bound": "mfma", "achieved": round(tops_gemm, 2), "peak": PEAK_INT8_TOPS,
-                     "unit": "TOP/s", "frac": round(tops_gemm / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "unit": "TOP/s", "frac": round(tops_gemm / PEAK_INT8_TOPS, 4), "traffic": measured_traffic("gemm_q5_K"),
                      "work_per_launch": f"2*M*N*K = {ops:.4e} int8 ops", "avg_launch_us": round(ms_gemm * 1e3, 2)},
         "gemm_only": {"us": round(ms_gemm * 1e3, 2), "tops": round(tops_gemm, 2)},
         "quantize": {"us": round(ms_quant * 1e3, 2), "gbs": round((GEMM_M * GEMM_K * 4 + GEMM_M * GEMM_K * 1.14) / (ms_quant * 1e-3) / 1e9, 1)},
@@ -197,7 +219,7 @@ def main():
                             f"({v['rotated_bytes'] / 2**30:.2f} GiB)",
                 "us": round(v["us"], 3), "value": round(v["gbs"], 1), "unit": "GB/s",
                 "roofline": {"bound": "hbm", "achieved": round(v["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": round(v["gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                             "frac": round(v["gbs"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(f"matvec_{k}"),
                              "work_per_launch": f"W + 4K + 4N = {v['bytes']} bytes"}}
             for k, v in matvec.items()}
 

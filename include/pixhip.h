@@ -92,6 +92,10 @@ int pixhip_synchronize(pixhip_session* session);
  * host-coherent mappings make these implicit, src/backend_vulkan.h:87-122). */
 int pixhip_copy_to_device(pixhip_session* session, void* device_dst, const void* host_src, size_t bytes);
 int pixhip_copy_to_host(pixhip_session* session, void* host_dst, const void* device_src, size_t bytes);
+/* Device-to-device copy, asynchronous on the session stream (activations stay
+ * device-resident between ops, as tensors do in the Vulkan backend's buffers;
+ * vulkan_copy_rows, src/backend_vulkan.h:151). */
+int pixhip_copy_device(pixhip_session* session, void* device_dst, const void* device_src, size_t bytes);
 
 /* ---- weights: VulkanState::weight (src/backend_vulkan.cpp:742-758) ---- */
 

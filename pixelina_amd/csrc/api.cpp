@@ -606,6 +606,16 @@ int pixhip_copy_to_device(pixhip_session* s, void* dst, const void* src, size_t 
     return PIXHIP_OK;
 }
 
+int pixhip_copy_device(pixhip_session* s, void* dst, const void* src, size_t bytes)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!bytes) return PIXHIP_OK;
+    if (!dst || !src) return fail(PIXHIP_ERR_ARGUMENT,"null pointer");
+    PIX_HIP(pixhip::launch_copy_device(dst,src,bytes,s->stream),"device copy");
+    return PIXHIP_OK;
+}
+
 int pixhip_copy_to_host(pixhip_session* s, void* dst, const void* src, size_t bytes)
 {
     int rc = use_device(s);

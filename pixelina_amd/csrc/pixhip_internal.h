@@ -103,6 +103,7 @@ struct Output {
 hipError_t launch_quantize_q8_K(const float* x, size_t rows, size_t inner, Act8K planar, void* blocks, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float* x, size_t rows, size_t inner, size_t kpad, Act80 planar, void* blocks,
                                 hipStream_t s);
+hipError_t launch_copy_device(void* dst, const void* src, size_t bytes, hipStream_t s);
 
 // repack.hip
 hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,

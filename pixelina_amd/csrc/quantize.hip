@@ -6,6 +6,8 @@
 //
 // HBM-bound byte work: one wave per Q8_K block (64 lanes x float4 = 256
 // values), one 8-lane group per Q8_0 block; reads 4 B/value, writes ~1.1 B/value.
+#include <algorithm>
+
 #include "pixhip_device.h"
 #include "pixhip_internal.h"
 
@@ -101,6 +103,25 @@ hipError_t launch_quantize_q8_0(const float* x, size_t rows, size_t inner, size_
     size_t grid = (waves + kQuantWaves - 1) / kQuantWaves;
     quantize_q8_0_kernel<<<dim3((unsigned)grid),dim3(64 * kQuantWaves),0,s>>>(x,rows,inner,kpad,planar.mpad,planar.qs,planar.d,
                                                                                static_cast<uint8_t*>(blocks));
+    return hipGetLastError();
+}
+
+// Device-to-device copy in 16-byte words (grid-stride, one load and one store
+// per word): the plain copy whose HBM byte counters calibrate the others.
+__global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t words)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride) dst[i] = src[i];
+}
+
+hipError_t launch_copy_device(void* dst, const void* src, size_t bytes, hipStream_t s)
+{
+    if (!bytes) return hipSuccess;
+    if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes) & 15)
+        return hipMemcpyAsync(dst,src,bytes,hipMemcpyDeviceToDevice,s);
+    const size_t words = bytes / 16;
+    const size_t grid = std::min<size_t>((words + 255) / 256,(size_t)1 << 16);
+    copy16_kernel<<<dim3((unsigned)grid),dim3(256),0,s>>>(static_cast<const uint4*>(src),static_cast<uint4*>(dst),words);
     return hipGetLastError();
 }
 

@@ -66,6 +66,9 @@ class Session:
         a = np.ascontiguousarray(array)
         return DeviceBuffer(self, max(a.nbytes, 4)).upload(a)
 
+    def copy_device(self, dst_ptr, src_ptr, nbytes):
+        check(self.lib.pixhip_copy_device(self.handle, dst_ptr, src_ptr, nbytes), "pixhip_copy_device")
+
     def synchronize(self):
         check(self.lib.pixhip_synchronize(self.handle), "pixhip_synchronize")
 

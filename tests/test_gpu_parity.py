@@ -165,3 +165,16 @@ def test_matvec_vs_oracle(sess, wtype, n, k):
     err = row_rel_error(y, ref).max()
     print(f"matvec type={wtype} N={n} K={k} rel={err:.2e}", flush=True)
     assert err <= TOL
+
+
+def test_copy_device_is_exact(sess):
+    rng = np.random.default_rng(31)
+    for nbytes in (16, 4096 + 16, 3 * (1 << 20) + 5):
+        data = rng.integers(0, 256, nbytes, dtype=np.uint8)
+        src = sess.to_device(data)
+        dst = sess.alloc(nbytes)
+        sess.copy_device(dst.ptr, src.ptr, nbytes)
+        sess.synchronize()
+        assert np.array_equal(dst.download(np.uint8, nbytes), data)
+        src.free()
+        dst.free()
