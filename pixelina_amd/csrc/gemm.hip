@@ -18,10 +18,12 @@
 // loaded with buffer_load_dwordx4 ... lds (HBM -> LDS, no registers).  Lane l
 // of a DMA lands at LDS base + 16*l; the source is a buffer resource (SGPRs) +
 // a per-lane offset fixed for the whole kernel (VGPR) + a wave-uniform offset
-// (SGPR), so DMA issue costs no vector ALU work.  Each lane picks its source
-// piece so that the ring holds rows of four 16-byte pieces with piece c of row
-// r at slot 4r + (c ^ g(r)), g(r) = ((r>>1) ^ (r>>3)) & 3, which keeps the MFMA
-// operand reads (ds_read_b128, 32 rows per half-wave) free of bank conflicts.
+// (SGPR), so DMA issue costs no vector ALU work.  Four consecutive lanes fetch
+// one 64-byte row (coalesced), and each lane picks its piece so that the ring
+// holds rows of four 16-byte pieces with piece c of row r at slot
+// 4r + (c ^ ((r>>2) & 3)).  With that swizzle the MFMA operand reads
+// (ds_read_b128: lane l reads row l%32, piece 2s + l/32) measured free of LDS
+// bank conflicts on gfx950; swizzles on the low row bits did not.
 // Per 256-value super-block the scale data (activation d and 16-value sums,
 // weight d, dmin and sub-block minima) rides in a double-buffered LDS region
 // loaded the same way.  Synchronisation is explicit: s_waitcnt vmcnt for this
@@ -130,8 +132,6 @@ __device__ __forceinline__ void dma(Rsrc r, uint8_t* lds_uniform, uint32_t voff,
 // activation scales.
 __device__ __forceinline__ void pad_dma(const Ctx& x, uint8_t* dst) { dma(x.rxd,dst,x.vo_lin,0); }
 
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
-
 // Bijective XCD-aware remap: hardware places workgroup b on XCD b % 8; give
 // each XCD a contiguous range of logical tiles so its L2 sees neighbours.
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks)
@@ -143,9 +143,8 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks)
 
 // DMA of stage c into `st`.  Chunk q*8 + wave of the 32 is this wave's q-th;
 // q = 0, 1 are activation rows, q = 2 the first weight plane, q = 3 the second
-// (Q8_0: the block scales).  A 64-slot chunk covers 16 rows of 64 bytes; its
-// rows start at a multiple of 16 whose parity is the wave's, which fixes the
-// swizzle pattern (vo_rows).
+// (Q8_0: the block scales).  A 64-slot chunk covers 16 rows of 64 bytes; lane
+// l fetches chunk row l/4, piece (l%4) ^ ((l/16) & 3) (vo_rows).
 template <int KIND>
 __device__ __forceinline__ void issue_stage(const GemmArgs& g, const Ctx& x, int c, uint8_t* st)
 {
@@ -300,14 +299,14 @@ __device__ __forceinline__ void step(const GemmArgs& g, const Ctx& x, int c, boo
     const v16i izero = {};
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-        const int cp = ((2 * s + x.lg) ^ x.sw) * 16;
+        const int cp = x.lr * 64 + 16 * ((2 * s + x.lg) ^ x.sw);
         v4i a[2], wh[2], wl[2];
 #pragma unroll
-        for (int i = 0; i < 2; i++) a[i] = *reinterpret_cast<const v4i*>(cur + (x.wm * 64 + i * 32 + x.lr) * 64 + cp);
+        for (int i = 0; i < 2; i++) a[i] = *reinterpret_cast<const v4i*>(cur + (x.wm * 64 + i * 32) * 64 + cp);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            wh[j] = *reinterpret_cast<const v4i*>(cur + 16 * kSlotW + (x.wn * 64 + j * 32 + x.lr) * 64 + cp);
-            if constexpr (PLANES == 2) wl[j] = *reinterpret_cast<const v4i*>(cur + 16 * kSlotW2 + (x.wn * 64 + j * 32 + x.lr) * 64 + cp);
+            wh[j] = *reinterpret_cast<const v4i*>(cur + 16 * kSlotW + (x.wn * 64 + j * 32) * 64 + cp);
+            if constexpr (PLANES == 2) wl[j] = *reinterpret_cast<const v4i*>(cur + 16 * kSlotW2 + (x.wn * 64 + j * 32) * 64 + cp);
         }
         if constexpr (KIND == KIND_Q80) {
             // One 32-value block per sub-block: fresh accumulator, fp32 epilogue.
@@ -387,12 +386,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
     x.wn = x.wave / kWavesM;
     x.lr = x.lane & 31;
     x.lg = x.lane >> 5;
-    x.sw = swz(x.lr);  // rows read by this lane are lr + 32k: same swizzle
+    x.sw = (x.lr >> 2) & 3;  // rows read by this lane are lr + 32k: same swizzle
     x.K = g.K;
     x.nchunks = g.K / kKC;
     {
-        const int l4 = x.lane >> 2, row = (x.wave & 1) * 16 + l4;
-        x.vo_rows = (uint32_t)(l4 * g.K + 16 * ((x.lane & 3) ^ swz(row)));
+        // chunk rows start at multiples of 16, so the swizzle of chunk row l/4 is (l/16) & 3
+        x.vo_rows = (uint32_t)((x.lane >> 2) * g.K + 16 * ((x.lane & 3) ^ ((x.lane >> 4) & 3)));
         x.vo_lin = 16u * x.lane;
         x.vo_bs = (uint32_t)((x.lane >> 1) * (g.K / 8) + 16 * (x.lane & 1));
         x.vo_wd = KIND == KIND_Q80? 16u * (x.lane & 31) + (x.lane >> 5) * 4u * g.Npad

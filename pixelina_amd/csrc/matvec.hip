@@ -12,6 +12,8 @@
 // Q6_K: 16 positions x 4 groups of a half super-block) and the row total is a
 // wave reduction.  Rows are dealt to waves in contiguous pairs so the whole
 // matrix streams front to back.
+#include <algorithm>
+
 #include "pixhip_device.h"
 #include "pixhip_internal.h"
 
@@ -20,26 +22,59 @@ namespace pixhip {
 constexpr int kMvWaves = 4;
 constexpr int kMvRows = 2;  // rows in flight per wave iteration
 
-// Quantize x (K values) into LDS as Q8_K: qs, d per block, and the 16-value
-// group sums.  All waves of the workgroup take part.
-__device__ __forceinline__ void stage_x_q8_K(const float* __restrict__ x, int K, int8_t* sQ, float* sD, int* sB)
+// x staging is split in two so that its global loads go out first (before
+// the first weight rows are requested) and its quantization runs while the
+// weight loads are in flight.  Each wave takes blocks wave, wave+4, ...; P
+// bounds the blocks per wave (Q8_K) or 8-block passes per wave (Q8_0).
+
+// Q8_K: one wave per 256-value block, a float4 per lane.
+template <int P>
+__device__ __forceinline__ void load_x_q8_K(const float* __restrict__ x, int K, float4 (&v)[P])
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = K / PIX_QK;
-    for (int b = wave; b < nb; b += kMvWaves) {
-        float4 v = reinterpret_cast<const float4*>(x + b * PIX_QK)[lane];
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        const int b = wave + kMvWaves * i;
+        if (b < nb) v[i] = reinterpret_cast<const float4*>(x + b * PIX_QK)[lane];
+    }
+}
+
+template <int P>
+__device__ __forceinline__ void quantize_x_q8_K(const float4 (&v)[P], int K, int8_t* sQ, float* sD, int* sB)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = K / PIX_QK;
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        const int b = wave + kMvWaves * i;
+        if (b >= nb) break;
         uint32_t packed;
         float d;
         int gsum;
-        quantize_q8_K_wave(v,lane,packed,d,gsum);
+        quantize_q8_K_wave(v[i],lane,packed,d,gsum);
         reinterpret_cast<uint32_t*>(sQ + b * PIX_QK)[lane] = packed;
         if (lane == 0) sD[b] = d;
         if ((lane & 3) == 0) sB[b * 16 + (lane >> 2)] = gsum;
     }
 }
 
-// Q8_0 staging over Kp = K rounded up to 64: the padding block is zero.
-__device__ __forceinline__ void stage_x_q8_0(const float* __restrict__ x, int K, int Kp, int8_t* sQ, float* sD)
+// Q8_0 over Kp = K rounded up to 64 (the padding block is zero): an 8-lane
+// group per 32-value block, 8 blocks per wave per pass.
+template <int P>
+__device__ __forceinline__ void load_x_q8_0(const float* __restrict__ x, int K, float4 (&v)[P])
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = K / PIX_QK8;
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        const int b = (wave + kMvWaves * i) * 8 + (lane >> 3);
+        if (b < nb) v[i] = reinterpret_cast<const float4*>(x + b * PIX_QK8)[lane & 7];
+    }
+}
+
+template <int P>
+__device__ __forceinline__ void quantize_x_q8_0(const float4 (&v)[P], int K, int Kp, int8_t* sQ, float* sD)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = K / PIX_QK8;
@@ -47,14 +82,14 @@ __device__ __forceinline__ void stage_x_q8_0(const float* __restrict__ x, int K,
         for (int i = threadIdx.x; i < Kp - K; i += blockDim.x) sQ[K + i] = 0;
         if (threadIdx.x == 0) sD[nb] = 0.0f;
     }
-    for (int b0 = wave * 8; b0 < nb; b0 += kMvWaves * 8) {
-        const int b = b0 + (lane >> 3);
-        const int bl = b < nb? b : nb - 1;
-        float4 v = reinterpret_cast<const float4*>(x + bl * PIX_QK8)[lane & 7];
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        const int b = (wave + kMvWaves * i) * 8 + (lane >> 3);
+        if ((wave + kMvWaves * i) * 8 >= nb) break;  // wave-uniform
         uint32_t packed;
         float d32;
         uint16_t dh;
-        quantize_q8_0_group(v,packed,d32,dh);
+        quantize_q8_0_group(b < nb? v[i] : make_float4(0.0f,0.0f,0.0f,0.0f),packed,d32,dh);
         if (b < nb) {
             reinterpret_cast<uint32_t*>(sQ + b * PIX_QK8)[lane & 7] = packed;
             if ((lane & 7) == 0) sD[b] = half_bits_to_float(dh);
@@ -73,6 +108,82 @@ __device__ __forceinline__ void store_row(const Output& out, size_t n, float v)
 }
 
 // ---------------------------------------------------------------- Q5_K (GGUF bytes)
+// Weight registers of kMvRows rows: unit u = lane + 64k of a row is a quarter
+// super-block (two 32-value sub-blocks): its block's first 48 bytes (d, dmin,
+// scales, qh) and its 32 bytes of nibbles.
+template <int UPL> struct Q5Rows {
+    uint4 head[kMvRows][UPL], qh0[kMvRows][UPL], qh1[kMvRows][UPL], qs0[kMvRows][UPL], qs1[kMvRows][UPL];
+};
+
+template <int UPL>
+__device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const uint8_t* __restrict__ w, size_t row_bytes, int r0, int last,
+                                        int lane, int units)
+{
+#pragma unroll
+    for (int rr = 0; rr < kMvRows; rr++) {
+        const int row = min(r0 + rr,last - 1);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = lane + 64 * k;
+            if (u < units) {
+                const uint4* p = reinterpret_cast<const uint4*>(w + (size_t)row * row_bytes + (size_t)(u >> 2) * PIX_Q5_K_BYTES);
+                f.head[rr][k] = p[0];
+                f.qh0[rr][k] = p[1];
+                f.qh1[rr][k] = p[2];
+                f.qs0[rr][k] = p[3 + 2 * (u & 3)];
+                f.qs1[rr][k] = p[4 + 2 * (u & 3)];
+            }
+        }
+    }
+}
+
+template <int UPL>
+__device__ __forceinline__ void q5_compute(const Q5Rows<UPL>& f, float part[kMvRows], const int8_t* sQ, const float* sD,
+                                           const int* sB, int lane, int units)
+{
+#pragma unroll
+    for (int rr = 0; rr < kMvRows; rr++) part[rr] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const int u = lane + 64 * k;
+        if (u >= units) continue;
+        const int b = u >> 2, j = u & 3;
+        const uint4* xq = reinterpret_cast<const uint4*>(sQ + b * PIX_QK + 64 * j);
+        const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2], x3 = xq[3];
+        const uint32_t xa[8] = {x0.x,x0.y,x0.z,x0.w,x1.x,x1.y,x1.z,x1.w};
+        const uint32_t xb[8] = {x2.x,x2.y,x2.z,x2.w,x3.x,x3.y,x3.z,x3.w};
+        const float yd = sD[b];
+        const int bs0 = sB[b * 16 + 4 * j] + sB[b * 16 + 4 * j + 1];
+        const int bs1 = sB[b * 16 + 4 * j + 2] + sB[b * 16 + 4 * j + 3];
+#pragma unroll
+        for (int rr = 0; rr < kMvRows; rr++) {
+            const uint4 h = f.head[rr][k];
+            int sc0, mn0, sc1, mn1;
+            q5_scale_min(h.y,h.z,h.w,2 * j,sc0,mn0);
+            q5_scale_min(h.y,h.z,h.w,2 * j + 1,sc1,mn1);
+            const uint32_t qhw[8] = {f.qh0[rr][k].x,f.qh0[rr][k].y,f.qh0[rr][k].z,f.qh0[rr][k].w,
+                                     f.qh1[rr][k].x,f.qh1[rr][k].y,f.qh1[rr][k].z,f.qh1[rr][k].w};
+            const uint32_t qsw[8] = {f.qs0[rr][k].x,f.qs0[rr][k].y,f.qs0[rr][k].z,f.qs0[rr][k].w,
+                                     f.qs1[rr][k].x,f.qs1[rr][k].y,f.qs1[rr][k].z,f.qs1[rr][k].w};
+            int dot0 = 0, dot1 = 0;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t lo = qsw[q] & 0x0f0f0f0fu;
+                const uint32_t hi = (qsw[q] >> 4) & 0x0f0f0f0fu;
+                const uint32_t b0 = ((qhw[q] >> (2 * j)) & 0x01010101u) << 4;
+                const uint32_t b1 = ((qhw[q] >> (2 * j + 1)) & 0x01010101u) << 4;
+                dot0 = sdot4(lo | b0,xa[q],dot0);
+                dot1 = sdot4(hi | b1,xb[q],dot1);
+            }
+            const int S = sc0 * dot0 + sc1 * dot1;
+            const int Mn = mn0 * bs0 + mn1 * bs1;
+            const float wd = half_bits_to_float((uint16_t)(h.x & 0xffffu));
+            const float wm = half_bits_to_float((uint16_t)(h.x >> 16));
+            part[rr] = __builtin_fmaf(yd,__builtin_fmaf(-wm,(float)Mn,wd * (float)S),part[rr]);
+        }
+    }
+}
+
 template <int UPL>
 __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                                     int N, int K, Output out, int rows_per_wave)
@@ -82,149 +193,125 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
-    stage_x_q8_K(x,K,sQ,sD,sB);
-    __syncthreads();
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t row_bytes = (size_t)nb * PIX_Q5_K_BYTES;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * rows_per_wave;
     const int last = min(first + rows_per_wave,N);
     const int units = nb * 4;
+    // The first rows' weights are requested before x is staged, so their
+    // latency overlaps the quantization of x; afterwards each iteration
+    // requests the next rows before computing the current ones.
+    float4 xv[4 * UPL];
+    load_x_q8_K(x,K,xv);
+    Q5Rows<UPL> cur, nxt;
+    if (first < last) q5_load(cur,w,row_bytes,first,last,lane,units);
+    quantize_x_q8_K(xv,K,sQ,sD,sB);
+    __syncthreads();
     for (int r0 = first; r0 < last; r0 += kMvRows) {
+        const bool more = r0 + kMvRows < last;
+        if (more) q5_load(nxt,w,row_bytes,r0 + kMvRows,last,lane,units);
         float part[kMvRows];
-        uint4 head[kMvRows][UPL], qh0[kMvRows][UPL], qh1[kMvRows][UPL], qs0[kMvRows][UPL], qs1[kMvRows][UPL];
-#pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
-            part[rr] = 0.0f;
-            const int row = min(r0 + rr,last - 1);
-#pragma unroll
-            for (int k = 0; k < UPL; k++) {
-                const int u = lane + 64 * k;
-                if (u < units) {
-                    const uint8_t* blk = w + (size_t)row * row_bytes + (size_t)(u >> 2) * PIX_Q5_K_BYTES;
-                    const uint4* p = reinterpret_cast<const uint4*>(blk);
-                    head[rr][k] = p[0];
-                    qh0[rr][k] = p[1];
-                    qh1[rr][k] = p[2];
-                    qs0[rr][k] = p[3 + 2 * (u & 3)];
-                    qs1[rr][k] = p[4 + 2 * (u & 3)];
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            const int u = lane + 64 * k;
-            if (u >= units) continue;
-            const int b = u >> 2, j = u & 3;
-            const uint4* xq = reinterpret_cast<const uint4*>(sQ + b * PIX_QK + 64 * j);
-            const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2], x3 = xq[3];
-            const uint32_t xa[8] = {x0.x,x0.y,x0.z,x0.w,x1.x,x1.y,x1.z,x1.w};
-            const uint32_t xb[8] = {x2.x,x2.y,x2.z,x2.w,x3.x,x3.y,x3.z,x3.w};
-            const float yd = sD[b];
-            const int bs0 = sB[b * 16 + 4 * j] + sB[b * 16 + 4 * j + 1];
-            const int bs1 = sB[b * 16 + 4 * j + 2] + sB[b * 16 + 4 * j + 3];
-#pragma unroll
-            for (int rr = 0; rr < kMvRows; rr++) {
-                const uint4 h = head[rr][k];
-                int sc0, mn0, sc1, mn1;
-                q5_scale_min(h.y,h.z,h.w,2 * j,sc0,mn0);
-                q5_scale_min(h.y,h.z,h.w,2 * j + 1,sc1,mn1);
-                const uint32_t qhw[8] = {qh0[rr][k].x,qh0[rr][k].y,qh0[rr][k].z,qh0[rr][k].w,
-                                         qh1[rr][k].x,qh1[rr][k].y,qh1[rr][k].z,qh1[rr][k].w};
-                const uint32_t qsw[8] = {qs0[rr][k].x,qs0[rr][k].y,qs0[rr][k].z,qs0[rr][k].w,
-                                         qs1[rr][k].x,qs1[rr][k].y,qs1[rr][k].z,qs1[rr][k].w};
-                int dot0 = 0, dot1 = 0;
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const uint32_t lo = qsw[q] & 0x0f0f0f0fu;
-                    const uint32_t hi = (qsw[q] >> 4) & 0x0f0f0f0fu;
-                    const uint32_t b0 = ((qhw[q] >> (2 * j)) & 0x01010101u) << 4;
-                    const uint32_t b1 = ((qhw[q] >> (2 * j + 1)) & 0x01010101u) << 4;
-                    dot0 = sdot4(lo | b0,xa[q],dot0);
-                    dot1 = sdot4(hi | b1,xb[q],dot1);
-                }
-                const int S = sc0 * dot0 + sc1 * dot1;
-                const int Mn = mn0 * bs0 + mn1 * bs1;
-                const float wd = half_bits_to_float((uint16_t)(h.x & 0xffffu));
-                const float wm = half_bits_to_float((uint16_t)(h.x >> 16));
-                part[rr] = __builtin_fmaf(yd,__builtin_fmaf(-wm,(float)Mn,wd * (float)S),part[rr]);
-            }
-        }
+        q5_compute(cur,part,sQ,sD,sB,lane,units);
 #pragma unroll
         for (int rr = 0; rr < kMvRows; rr++) {
             const float v = wave_sum(part[rr]);
             if (lane == 0 && r0 + rr < last) store_row(out,(size_t)(r0 + rr),v);
         }
+        if (more) cur = nxt;
     }
 }
 
 // ---------------------------------------------------------------- Q8_0 (planar)
+// Unit u of a row: 64 values (two blocks) of the planar quants and their two
+// fp16 scales.
+template <int UPL> struct Q80Rows {
+    uint4 q[kMvRows][UPL][4];
+    uint32_t dd[kMvRows][UPL];
+};
+
+template <int UPL>
+__device__ __forceinline__ void q80_load(Q80Rows<UPL>& f, const PlanarQ80& w, int Kp, int r0, int last, int lane, int units)
+{
+    const int nbp = Kp / PIX_QK8;
+#pragma unroll
+    for (int rr = 0; rr < kMvRows; rr++) {
+        const int row = min(r0 + rr,last - 1);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = lane + 64 * k;
+            if (u < units) {
+                const uint4* p = reinterpret_cast<const uint4*>(w.qs + (size_t)row * Kp + 64 * u);
+#pragma unroll
+                for (int t = 0; t < 4; t++) f.q[rr][k][t] = p[t];
+                f.dd[rr][k] = *reinterpret_cast<const uint32_t*>(w.d + (size_t)row * nbp + 2 * u);
+            }
+        }
+    }
+}
+
+template <int UPL>
+__device__ __forceinline__ void q80_compute(const Q80Rows<UPL>& f, float part[kMvRows], const int8_t* sQ, const float* sD, int lane,
+                                            int units)
+{
+#pragma unroll
+    for (int rr = 0; rr < kMvRows; rr++) part[rr] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const int u = lane + 64 * k;
+        if (u >= units) continue;
+        const uint4* xq = reinterpret_cast<const uint4*>(sQ + 64 * u);
+        const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2], x3 = xq[3];
+        const uint32_t xa[8] = {x0.x,x0.y,x0.z,x0.w,x1.x,x1.y,x1.z,x1.w};
+        const uint32_t xb[8] = {x2.x,x2.y,x2.z,x2.w,x3.x,x3.y,x3.z,x3.w};
+        const float xd0 = sD[2 * u], xd1 = sD[2 * u + 1];
+#pragma unroll
+        for (int rr = 0; rr < kMvRows; rr++) {
+            const uint32_t wa[8] = {f.q[rr][k][0].x,f.q[rr][k][0].y,f.q[rr][k][0].z,f.q[rr][k][0].w,
+                                    f.q[rr][k][1].x,f.q[rr][k][1].y,f.q[rr][k][1].z,f.q[rr][k][1].w};
+            const uint32_t wb[8] = {f.q[rr][k][2].x,f.q[rr][k][2].y,f.q[rr][k][2].z,f.q[rr][k][2].w,
+                                    f.q[rr][k][3].x,f.q[rr][k][3].y,f.q[rr][k][3].z,f.q[rr][k][3].w};
+            int p0 = 0, p1 = 0;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                p0 = sdot4(wa[t],xa[t],p0);
+                p1 = sdot4(wb[t],xb[t],p1);
+            }
+            const float wd0 = half_bits_to_float((uint16_t)(f.dd[rr][k] & 0xffffu));
+            const float wd1 = half_bits_to_float((uint16_t)(f.dd[rr][k] >> 16));
+            part[rr] = __builtin_fmaf(wd0 * xd0,(float)p0,part[rr]);
+            part[rr] = __builtin_fmaf(wd1 * xd1,(float)p1,part[rr]);
+        }
+    }
+}
+
 template <int UPL>
 __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w, const float* __restrict__ x, int N, int K,
                                                                     int Kp, Output out, int rows_per_wave)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int nbp = Kp / PIX_QK8;
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + Kp);
-    stage_x_q8_0(x,K,Kp,sQ,sD);
-    __syncthreads();
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * rows_per_wave;
     const int last = min(first + rows_per_wave,N);
     const int units = Kp / 64;
+    float4 xv[4 * UPL];
+    load_x_q8_0(x,K,xv);
+    Q80Rows<UPL> cur, nxt;
+    if (first < last) q80_load(cur,w,Kp,first,last,lane,units);
+    quantize_x_q8_0(xv,K,Kp,sQ,sD);
+    __syncthreads();
     for (int r0 = first; r0 < last; r0 += kMvRows) {
+        const bool more = r0 + kMvRows < last;
+        if (more) q80_load(nxt,w,Kp,r0 + kMvRows,last,lane,units);
         float part[kMvRows];
-        uint4 q[kMvRows][UPL][4];
-        uint32_t dd[kMvRows][UPL];
-#pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
-            part[rr] = 0.0f;
-            const int row = min(r0 + rr,last - 1);
-#pragma unroll
-            for (int k = 0; k < UPL; k++) {
-                const int u = lane + 64 * k;
-                if (u < units) {
-                    const uint4* p = reinterpret_cast<const uint4*>(w.qs + (size_t)row * Kp + 64 * u);
-#pragma unroll
-                    for (int t = 0; t < 4; t++) q[rr][k][t] = p[t];
-                    dd[rr][k] = *reinterpret_cast<const uint32_t*>(w.d + (size_t)row * nbp + 2 * u);
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            const int u = lane + 64 * k;
-            if (u >= units) continue;
-            const uint4* xq = reinterpret_cast<const uint4*>(sQ + 64 * u);
-            const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2], x3 = xq[3];
-            const uint32_t xa[8] = {x0.x,x0.y,x0.z,x0.w,x1.x,x1.y,x1.z,x1.w};
-            const uint32_t xb[8] = {x2.x,x2.y,x2.z,x2.w,x3.x,x3.y,x3.z,x3.w};
-            const float xd0 = sD[2 * u], xd1 = sD[2 * u + 1];
-#pragma unroll
-            for (int rr = 0; rr < kMvRows; rr++) {
-                const uint32_t wa[8] = {q[rr][k][0].x,q[rr][k][0].y,q[rr][k][0].z,q[rr][k][0].w,
-                                        q[rr][k][1].x,q[rr][k][1].y,q[rr][k][1].z,q[rr][k][1].w};
-                const uint32_t wb[8] = {q[rr][k][2].x,q[rr][k][2].y,q[rr][k][2].z,q[rr][k][2].w,
-                                        q[rr][k][3].x,q[rr][k][3].y,q[rr][k][3].z,q[rr][k][3].w};
-                int p0 = 0, p1 = 0;
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    p0 = sdot4(wa[t],xa[t],p0);
-                    p1 = sdot4(wb[t],xb[t],p1);
-                }
-                const float wd0 = half_bits_to_float((uint16_t)(dd[rr][k] & 0xffffu));
-                const float wd1 = half_bits_to_float((uint16_t)(dd[rr][k] >> 16));
-                part[rr] = __builtin_fmaf(wd0 * xd0,(float)p0,part[rr]);
-                part[rr] = __builtin_fmaf(wd1 * xd1,(float)p1,part[rr]);
-            }
-        }
+        q80_compute(cur,part,sQ,sD,lane,units);
 #pragma unroll
         for (int rr = 0; rr < kMvRows; rr++) {
             const float v = wave_sum(part[rr]);
             if (lane == 0 && r0 + rr < last) store_row(out,(size_t)(r0 + rr),v);
         }
+        if (more) cur = nxt;
     }
 }
 
@@ -240,7 +327,11 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
-    stage_x_q8_K(x,K,sQ,sD,sB);
+    {
+        float4 xv[4 * UPL];
+        load_x_q8_K(x,K,xv);
+        quantize_x_q8_K(xv,K,sQ,sD,sB);
+    }
     __syncthreads();
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -318,12 +409,27 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
     }
 }
 
-// Rows per wave: enough waves to cover every CU several times over.
-static int pick_rows_per_wave(size_t N)
+// Launch shape: one round of workgroups that exactly fills the device (the
+// kernel's occupancy times the CU count), each wave taking an even share of
+// the rows, so no second partial round of workgroups trails the first.
+template <typename Kernel>
+static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid, int& rows_per_wave)
 {
-    int rpw = 8;
-    while (rpw > kMvRows && (N + (size_t)kMvWaves * rpw - 1) / ((size_t)kMvWaves * rpw) < 1024) rpw -= kMvRows;
-    return rpw;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v,hipDeviceAttributeMultiprocessorCount,dev) == hipSuccess && v > 0)
+            cus = v;
+        else
+            cus = 256;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu,kernel,64 * kMvWaves,lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    const size_t waves_needed = (N + kMvRows - 1) / kMvRows;
+    const size_t slots = (size_t)cus * per_cu * kMvWaves;
+    const size_t waves = std::min(waves_needed,slots);
+    rows_per_wave = (int)((N + waves - 1) / waves);
+    grid = (unsigned)((N + (size_t)kMvWaves * rows_per_wave - 1) / ((size_t)kMvWaves * rows_per_wave));
 }
 
 template <typename F>
@@ -338,36 +444,42 @@ static hipError_t dispatch_upl(int units, F&& f)
 
 hipError_t launch_matvec_q5_K(const uint8_t* raw, const float* x, size_t N, size_t K, const Output& out, hipStream_t s)
 {
-    const int rpw = pick_rows_per_wave(N);
-    const unsigned grid = (unsigned)((N + (size_t)kMvWaves * rpw - 1) / ((size_t)kMvWaves * rpw));
     const size_t nb = K / PIX_QK;
     const size_t lds = K + 4 * nb + 4 * 16 * nb;
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
-        matvec_q5_K_kernel<decltype(upl)::value><<<grid,64 * kMvWaves,lds,s>>>(raw,x,(int)N,(int)K,out,rpw);
+        auto kernel = matvec_q5_K_kernel<decltype(upl)::value>;
+        unsigned grid;
+        int rpw;
+        launch_shape(kernel,lds,N,grid,rpw);
+        kernel<<<grid,64 * kMvWaves,lds,s>>>(raw,x,(int)N,(int)K,out,rpw);
         return hipGetLastError();
     });
 }
 
 hipError_t launch_matvec_q8_0(const PlanarQ80& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s)
 {
-    const int rpw = pick_rows_per_wave(N);
-    const unsigned grid = (unsigned)((N + (size_t)kMvWaves * rpw - 1) / ((size_t)kMvWaves * rpw));
     const size_t Kp = (K + 63) / 64 * 64;
     const size_t lds = Kp + 4 * (Kp / PIX_QK8);
     return dispatch_upl((int)(Kp / 64),[&](auto upl) {
-        matvec_q8_0_kernel<decltype(upl)::value><<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,(int)Kp,out,rpw);
+        auto kernel = matvec_q8_0_kernel<decltype(upl)::value>;
+        unsigned grid;
+        int rpw;
+        launch_shape(kernel,lds,N,grid,rpw);
+        kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,(int)Kp,out,rpw);
         return hipGetLastError();
     });
 }
 
 hipError_t launch_matvec_q6_K(const PlanarQ6K& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s)
 {
-    const int rpw = pick_rows_per_wave(N);
-    const unsigned grid = (unsigned)((N + (size_t)kMvWaves * rpw - 1) / ((size_t)kMvWaves * rpw));
     const size_t nb = K / PIX_QK;
     const size_t lds = K + 4 * nb + 4 * 16 * nb;
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
-        matvec_q6_K_kernel<decltype(upl)::value><<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out,rpw);
+        auto kernel = matvec_q6_K_kernel<decltype(upl)::value>;
+        unsigned grid;
+        int rpw;
+        launch_shape(kernel,lds,N,grid,rpw);
+        kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out,rpw);
         return hipGetLastError();
     });
 }
