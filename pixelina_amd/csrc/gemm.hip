@@ -132,6 +132,17 @@ __device__ __forceinline__ void dma(Rsrc r, uint8_t* lds_uniform, uint32_t voff,
 // activation scales.
 __device__ __forceinline__ void pad_dma(const Ctx& x, uint8_t* dst) { dma(x.rxd,dst,x.vo_lin,0); }
 
+// The lane index, recomputed where it is used (volatile, so the compiler
+// cannot keep derived per-lane offsets live across the loop: the scale DMAs
+// run once per super-block and their offsets would otherwise occupy VGPRs
+// the MFMA loop needs).
+__device__ __forceinline__ uint32_t lane_now()
+{
+    uint32_t l;
+    __asm__ volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 // Bijective XCD-aware remap: hardware places workgroup b on XCD b % 8; give
 // each XCD a contiguous range of logical tiles so its L2 sees neighbours.
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks)
@@ -149,24 +160,29 @@ template <int KIND>
 __device__ __forceinline__ void issue_stage(const GemmArgs& g, const Ctx& x, int c, uint8_t* st)
 {
     const uint32_t k0 = (uint32_t)c * kKC;
+    const uint32_t lane = lane_now();
+    // lane l fetches chunk row l/4, piece (l%4) ^ ((l/16) & 3)
+    const uint32_t vo_rows = (lane >> 2) * (uint32_t)x.K + 16u * ((lane & 3) ^ ((lane >> 4) & 3));
+    const uint32_t vo_lin = 16u * lane;
+    const uint32_t vo_wd = 16u * (lane & 31) + (lane >> 5) * 4u * (uint32_t)g.Npad;
 #pragma unroll
     for (int q = 0; q < kPerWave; q++) {
         const int chunk = x.wave + kWaves * q;
         uint8_t* dst = st + chunk * kChunk;
         if (q < 2) {
-            dma(x.rx,dst,x.vo_rows,(uint32_t)(x.m0 + chunk * 16) * x.K + k0);
+            dma(x.rx,dst,vo_rows,(uint32_t)(x.m0 + chunk * 16) * x.K + k0);
         } else if (q == 2 || KIND != KIND_Q80) {
             const int row0 = (chunk - (q == 2? 16 : 24)) * 16;
-            dma(q == 2? x.rwh : x.rwl,dst,x.vo_rows,(uint32_t)(x.n0 + row0) * x.K + k0);
+            dma(q == 2? x.rwh : x.rwl,dst,vo_rows,(uint32_t)(x.n0 + row0) * x.K + k0);
         } else {
             // chunks 24, 25: activation scales of blocks 2c, 2c+1; 26: weight
             // scales of both blocks; 27..31 unused.
             if (x.wave < 2)
-                dma(x.rxd,dst,x.vo_lin,(uint32_t)((2 * c + x.wave) * g.Mpad + x.m0) * 4u);
+                dma(x.rxd,dst,vo_lin,(uint32_t)((2 * c + x.wave) * g.Mpad + x.m0) * 4u);
             else if (x.wave == 2)
-                dma(x.rwd,dst,x.vo_wd,(uint32_t)(2 * c * g.Npad + x.n0) * 4u);
+                dma(x.rwd,dst,vo_wd,(uint32_t)(2 * c * g.Npad + x.n0) * 4u);
             else
-                pad_dma(x,dst);
+                dma(x.rxd,dst,vo_lin,0);
         }
     }
 }
@@ -176,26 +192,30 @@ __device__ __forceinline__ void issue_stage(const GemmArgs& g, const Ctx& x, int
 template <int KIND>
 __device__ __forceinline__ void issue_scales(const GemmArgs& g, const Ctx& x, int b, uint8_t* sc)
 {
+    const uint32_t lane = lane_now();
+    const uint32_t vo_lin = 16u * lane;
+    const uint32_t vo_bs = (lane >> 1) * (uint32_t)(x.K / 8) + 16u * (lane & 1);
+    const uint32_t vo_wd = 16u * (lane & 31) + (lane >> 5) * g.wdm_off;
 #pragma unroll
     for (int q = 0; q < kScalePerWave; q++) {
         const int chunk = x.wave + kWaves * q;
         uint8_t* dst = sc + chunk * kChunk;
         if (chunk == 0) {
-            dma(x.rxd,dst,x.vo_lin,(uint32_t)(b * g.Mpad + x.m0) * 4u);
+            dma(x.rxd,dst,vo_lin,(uint32_t)(b * g.Mpad + x.m0) * 4u);
         } else if (chunk <= 8) {
             if (KIND == KIND_Q5K)
-                dma(x.rxbs,dst,x.vo_bs,((uint32_t)(x.m0 + (chunk - 1) * 32) * (x.K / 16) + b * 16) * 2u);
+                dma(x.rxbs,dst,vo_bs,((uint32_t)(x.m0 + (chunk - 1) * 32) * (x.K / 16) + b * 16) * 2u);
             else
-                pad_dma(x,dst);
+                dma(x.rxd,dst,vo_lin,0);
         } else if (chunk <= 10) {
             if (KIND == KIND_Q5K)
-                dma(x.rwmn,dst,x.vo_lin,(uint32_t)(b * g.Npad + x.n0 + (chunk - 9) * 64) * 16u);
+                dma(x.rwmn,dst,vo_lin,(uint32_t)(b * g.Npad + x.n0 + (chunk - 9) * 64) * 16u);
             else
-                pad_dma(x,dst);
+                dma(x.rxd,dst,vo_lin,0);
         } else if (chunk == 11) {
-            dma(x.rwd,dst,x.vo_wd,(uint32_t)(b * g.Npad + x.n0) * 4u);
+            dma(x.rwd,dst,vo_wd,(uint32_t)(b * g.Npad + x.n0) * 4u);
         } else {
-            pad_dma(x,dst);
+            dma(x.rxd,dst,vo_lin,0);
         }
     }
 }

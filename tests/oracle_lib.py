@@ -84,6 +84,12 @@ def reference():
     return _ref
 
 
+def default_threads():
+    """Host threads for the oracle: every core here, at most 16 (a GPU box's
+    share of its host, whatever os.cpu_count() reports there)."""
+    return max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)))
+
+
 def ptr(a):
     return a.ctypes.data
 
@@ -118,7 +124,7 @@ def quant_matmul(lib, prefix, w, wtype, x, rows, threads=None):
     cols, k = x.shape
     y = np.full((cols, rows), np.nan, dtype=np.float32)
     if prefix == "orc":
-        ok = lib.orc_quant_matmul(ptr(w), wtype, ptr(x), ptr(y), rows, cols, k, threads or (os.cpu_count() or 1))
+        ok = lib.orc_quant_matmul(ptr(w), wtype, ptr(x), ptr(y), rows, cols, k, threads or default_threads())
     else:
         ok = lib.ref_quant_matmul(ptr(w), wtype, ptr(x), ptr(y), rows, cols, k)
     if not ok:
