@@ -10,8 +10,10 @@
 // wave streams whole rows: lane u owns one "unit" of 64 values of a row
 // (Q5_K: a quarter super-block = two 32-value sub-blocks; Q8_0: two blocks;
 // Q6_K: 16 positions x 4 groups of a half super-block) and the row total is a
-// wave reduction.  Rows are dealt to waves in contiguous pairs so the whole
-// matrix streams front to back.
+// wave reduction.  Row pairs are dealt round-robin over every wave of the
+// grid (wave g takes pairs g, g + W, g + 2W, ...), so at any moment the waves
+// of the whole device read one contiguous band of the matrix: DRAM sees a
+// front-to-back stream, as a plain copy does.
 #include <algorithm>
 
 #include "pixhip_device.h"
@@ -19,7 +21,7 @@
 
 namespace pixhip {
 
-constexpr int kMvWaves = 4;
+constexpr int kMvWaves = 8;
 constexpr int kMvRows = 2;  // rows in flight per wave iteration
 
 // x staging is split in two so that its global loads go out first (before
@@ -186,7 +188,7 @@ __device__ __forceinline__ void q5_compute(const Q5Rows<UPL>& f, float part[kMvR
 
 template <int UPL>
 __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                                    int N, int K, Output out, int rows_per_wave)
+                                                                    int N, int K, Output out)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nb = K / PIX_QK;
@@ -195,8 +197,9 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t row_bytes = (size_t)nb * PIX_Q5_K_BYTES;
-    const int first = ((int)blockIdx.x * kMvWaves + wave) * rows_per_wave;
-    const int last = min(first + rows_per_wave,N);
+    const int stride = (int)gridDim.x * kMvWaves * kMvRows;
+    const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
+    const int last = N;
     const int units = nb * 4;
     // The first rows' weights are requested before x is staged, so their
     // latency overlaps the quantization of x; afterwards each iteration
@@ -207,9 +210,9 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_
     if (first < last) q5_load(cur,w,row_bytes,first,last,lane,units);
     quantize_x_q8_K(xv,K,sQ,sD,sB);
     __syncthreads();
-    for (int r0 = first; r0 < last; r0 += kMvRows) {
-        const bool more = r0 + kMvRows < last;
-        if (more) q5_load(nxt,w,row_bytes,r0 + kMvRows,last,lane,units);
+    for (int r0 = first; r0 < last; r0 += stride) {
+        const bool more = r0 + stride < last;
+        if (more) q5_load(nxt,w,row_bytes,r0 + stride,last,lane,units);
         float part[kMvRows];
         q5_compute(cur,part,sQ,sD,sB,lane,units);
 #pragma unroll
@@ -286,14 +289,15 @@ __device__ __forceinline__ void q80_compute(const Q80Rows<UPL>& f, float part[kM
 
 template <int UPL>
 __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w, const float* __restrict__ x, int N, int K,
-                                                                    int Kp, Output out, int rows_per_wave)
+                                                                    int Kp, Output out)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + Kp);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int first = ((int)blockIdx.x * kMvWaves + wave) * rows_per_wave;
-    const int last = min(first + rows_per_wave,N);
+    const int stride = (int)gridDim.x * kMvWaves * kMvRows;
+    const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
+    const int last = N;
     const int units = Kp / 64;
     float4 xv[4 * UPL];
     load_x_q8_0(x,K,xv);
@@ -301,9 +305,9 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w,
     if (first < last) q80_load(cur,w,Kp,first,last,lane,units);
     quantize_x_q8_0(xv,K,Kp,sQ,sD);
     __syncthreads();
-    for (int r0 = first; r0 < last; r0 += kMvRows) {
-        const bool more = r0 + kMvRows < last;
-        if (more) q80_load(nxt,w,Kp,r0 + kMvRows,last,lane,units);
+    for (int r0 = first; r0 < last; r0 += stride) {
+        const bool more = r0 + stride < last;
+        if (more) q80_load(nxt,w,Kp,r0 + stride,last,lane,units);
         float part[kMvRows];
         q80_compute(cur,part,sQ,sD,lane,units);
 #pragma unroll
@@ -320,7 +324,7 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w,
 // it covers elements 128h + 32g + 16ih + i for g = 0..3, i = 0..15.
 template <int UPL>
 __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w, const float* __restrict__ x, int N, int K,
-                                                                    Output out, int rows_per_wave)
+                                                                    Output out)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nb = K / PIX_QK;
@@ -335,10 +339,11 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
     __syncthreads();
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int first = ((int)blockIdx.x * kMvWaves + wave) * rows_per_wave;
-    const int last = min(first + rows_per_wave,N);
+    const int stride = (int)gridDim.x * kMvWaves * kMvRows;
+    const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
+    const int last = N;
     const int units = nb * 4;
-    for (int r0 = first; r0 < last; r0 += kMvRows) {
+    for (int r0 = first; r0 < last; r0 += stride) {
         float part[kMvRows];
         uint4 la[kMvRows][UPL], lb[kMvRows][UPL], hh[kMvRows][UPL];
         uint2 scw[kMvRows][UPL];
@@ -410,10 +415,10 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
 }
 
 // Launch shape: one round of workgroups that exactly fills the device (the
-// kernel's occupancy times the CU count), each wave taking an even share of
-// the rows, so no second partial round of workgroups trails the first.
+// kernel's occupancy times the CU count), or fewer when there are fewer row
+// pairs than waves; the kernels stride over the rest.
 template <typename Kernel>
-static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid, int& rows_per_wave)
+static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid)
 {
     static int cus = 0;
     if (!cus) {
@@ -428,8 +433,7 @@ static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid, in
     const size_t waves_needed = (N + kMvRows - 1) / kMvRows;
     const size_t slots = (size_t)cus * per_cu * kMvWaves;
     const size_t waves = std::min(waves_needed,slots);
-    rows_per_wave = (int)((N + waves - 1) / waves);
-    grid = (unsigned)((N + (size_t)kMvWaves * rows_per_wave - 1) / ((size_t)kMvWaves * rows_per_wave));
+    grid = (unsigned)((waves + kMvWaves - 1) / kMvWaves);
 }
 
 template <typename F>
@@ -449,9 +453,8 @@ hipError_t launch_matvec_q5_K(const uint8_t* raw, const float* x, size_t N, size
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
         auto kernel = matvec_q5_K_kernel<decltype(upl)::value>;
         unsigned grid;
-        int rpw;
-        launch_shape(kernel,lds,N,grid,rpw);
-        kernel<<<grid,64 * kMvWaves,lds,s>>>(raw,x,(int)N,(int)K,out,rpw);
+        launch_shape(kernel,lds,N,grid);
+        kernel<<<grid,64 * kMvWaves,lds,s>>>(raw,x,(int)N,(int)K,out);
         return hipGetLastError();
     });
 }
@@ -463,9 +466,8 @@ hipError_t launch_matvec_q8_0(const PlanarQ80& w, const float* x, size_t N, size
     return dispatch_upl((int)(Kp / 64),[&](auto upl) {
         auto kernel = matvec_q8_0_kernel<decltype(upl)::value>;
         unsigned grid;
-        int rpw;
-        launch_shape(kernel,lds,N,grid,rpw);
-        kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,(int)Kp,out,rpw);
+        launch_shape(kernel,lds,N,grid);
+        kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,(int)Kp,out);
         return hipGetLastError();
     });
 }
@@ -477,9 +479,8 @@ hipError_t launch_matvec_q6_K(const PlanarQ6K& w, const float* x, size_t N, size
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
         auto kernel = matvec_q6_K_kernel<decltype(upl)::value>;
         unsigned grid;
-        int rpw;
-        launch_shape(kernel,lds,N,grid,rpw);
-        kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out,rpw);
+        launch_shape(kernel,lds,N,grid);
+        kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out);
         return hipGetLastError();
     });
 }
