@@ -39,11 +39,37 @@ __device__ __forceinline__ uint32_t pack_bytes(int a, int b, int c, int d)
     return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)(d & 255) << 24);
 }
 
+// Cross-lane moves within rows of 16 lanes (DPP, no LDS traffic); every lane of
+// the wave must be active.  XOR1 / XOR2 swap neighbours within quads; after
+// those, HALF_MIRROR (lane i <-> 7-i of each 8) and MIRROR (i <-> 15-i of each
+// 16) complete a reduction over 8 and 16 lanes.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v)
+{
+    return __builtin_bit_cast(float,__builtin_amdgcn_update_dpp(0,__builtin_bit_cast(int,v),CTRL,0xf,0xf,false));
+}
+template <int CTRL> __device__ __forceinline__ int dpp_i32(int v)
+{
+    return __builtin_amdgcn_update_dpp(0,v,CTRL,0xf,0xf,false);
+}
+__device__ __forceinline__ float lane_f32(float v, int lane)
+{
+    return __builtin_bit_cast(float,__builtin_amdgcn_readlane(__builtin_bit_cast(int,v),lane));
+}
+
+// Sum over the 64 lanes (every lane active), returned to every lane: rows of
+// 16 by DPP, then the four row sums in order.
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v,o,64);
-    return v;
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    v += dpp_f32<kDppMirror>(v);
+    return (lane_f32(v,0) + lane_f32(v,16)) + (lane_f32(v,32) + lane_f32(v,48));
 }
 
 // One Q8_K block (256 values) quantized by one full wave, 4 consecutive values
@@ -57,35 +83,35 @@ __device__ __forceinline__ float wave_sum(float v)
 // sum of the 16-value group this lane belongs to (group = lane/4).
 __device__ __forceinline__ void quantize_q8_K_wave(float4 v, int lane, uint32_t& packed, float& d, int& group_sum)
 {
+    (void)lane;
     float xs[4] = {v.x,v.y,v.z,v.w};
-    float amax = 0.0f, mval = 0.0f;
-    int idx = 1 << 30;
+    // largest |x| (NaN never compares greater, as in the reference's scan)
+    float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float ax = fabsf(xs[i]);
-        if (ax > amax) {
-            amax = ax;
-            mval = xs[i];
-            idx = 4 * lane + i;
-        }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float oa = __shfl_xor(amax,o,64);
-        float ov = __shfl_xor(mval,o,64);
-        int oi = __shfl_xor(idx,o,64);
-        if (oa > amax || (oa == amax && oi < idx)) {
-            amax = oa;
-            mval = ov;
-            idx = oi;
-        }
-    }
+    for (int i = 0; i < 4; i++) m = fabsf(xs[i]) > m? fabsf(xs[i]) : m;
+    m = fmaxf(m,dpp_f32<kDppXor1>(m));
+    m = fmaxf(m,dpp_f32<kDppXor2>(m));
+    m = fmaxf(m,dpp_f32<kDppHalfMirror>(m));
+    m = fmaxf(m,dpp_f32<kDppMirror>(m));
+    const float amax = fmaxf(fmaxf(lane_f32(m,0),lane_f32(m,16)),fmaxf(lane_f32(m,32),lane_f32(m,48)));
     if (amax == 0.0f) {
         packed = 0;
         d = 0.0f;
         group_sum = 0;
         return;
     }
+    // the first x (lowest index) whose |x| is that maximum: the lowest lane
+    // holding one, then its first such value
+    float mine = 0.0f;
+    bool has = false;
+#pragma unroll
+    for (int i = 3; i >= 0; i--)
+        if (fabsf(xs[i]) == amax) {
+            mine = xs[i];
+            has = true;
+        }
+    const int first = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(has));
+    const float mval = lane_f32(mine,first);
     float iscale = __fdiv_rn(-127.0f,mval);
     int q[4];
     int s = 0;
@@ -97,8 +123,8 @@ __device__ __forceinline__ void quantize_q8_K_wave(float4 v, int lane, uint32_t&
         s += q[i];
     }
     packed = pack_bytes(q[0],q[1],q[2],q[3]);
-    s += __shfl_xor(s,1,64);
-    s += __shfl_xor(s,2,64);
+    s += dpp_i32<kDppXor1>(s);
+    s += dpp_i32<kDppXor2>(s);
     group_sum = s;
     d = __fdiv_rn(1.0f,iscale);
 }
@@ -117,11 +143,9 @@ __device__ __forceinline__ void quantize_q8_0_group(float4 v, uint32_t& packed, 
         float ax = fabsf(xs[i]);
         amax = (amax < ax)? ax : amax;
     }
-#pragma unroll
-    for (int o = 4; o > 0; o >>= 1) {
-        float oa = __shfl_xor(amax,o,64);
-        amax = (amax < oa)? oa : amax;
-    }
+    amax = fmaxf(amax,dpp_f32<kDppXor1>(amax));
+    amax = fmaxf(amax,dpp_f32<kDppXor2>(amax));
+    amax = fmaxf(amax,dpp_f32<kDppHalfMirror>(amax));
     d32 = __fdiv_rn(amax,127.0f);
     float id = (d32 != 0.0f)? __fdiv_rn(1.0f,d32) : 0.0f;
     dh = float_to_half_bits(d32);
