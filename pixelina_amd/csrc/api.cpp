@@ -69,10 +69,11 @@ struct pixhip_weight {
     uint64_t inner = 0, rows = 0, gguf_bytes = 0;
     void* raw = nullptr;        // GGUF bytes (Q5_K matvec input; source of the other forms)
     void* planes = nullptr;     // Q5_K / Q6_K GEMM planes
-    void* planar = nullptr;     // Q8_0 planar (GEMM + matvec) or Q6_K planar (matvec)
+    void* planar = nullptr;     // Q8_0 planar (GEMM + matvec) or Q5_K / Q6_K planar (matvec)
     pixhip::PlanesQ5K q5{};
     pixhip::PlanesQ6K q6{};
     pixhip::PlanarQ80 q80{};
+    pixhip::PlanarQ5K q5p{};
     pixhip::PlanarQ6K q6p{};
     size_t resident = 0;
     uint64_t used = 0;
@@ -229,8 +230,20 @@ int ensure_gemm_form(pixhip_session* s, pixhip_weight* w)
 
 int ensure_matvec_form(pixhip_session* s, pixhip_weight* w)
 {
-    if (w->type != PIX_Q6_K || w->planar) return PIXHIP_OK;
+    if (w->type == PIX_Q8_0 || w->planar) return PIXHIP_OK;
     const size_t N = w->rows, K = w->inner, nb = K / PIX_QK;
+    if (w->type == PIX_Q5_K) {
+        Carver c;
+        size_t qs = c.take(N * K / 2), meta = c.take(N * (K / 64) * 16);
+        int rc = weight_alloc(s,w,c.offset,&w->planar);
+        if (rc) return rc;
+        uint8_t* base = static_cast<uint8_t*>(w->planar);
+        w->q5p = {base + qs,reinterpret_cast<const uint4*>(base + meta)};
+        PIX_HIP(pixhip::launch_repack_q5_K_planar(static_cast<const uint8_t*>(w->raw),N,K,const_cast<uint8_t*>(w->q5p.qs),
+                                                  const_cast<uint4*>(w->q5p.meta),s->stream),
+                "repack Q5_K planar");
+        return PIXHIP_OK;
+    }
     Carver c;
     size_t ql = c.take(N * K / 2), qh = c.take(N * K / 4), sc = c.take(N * K / 16), d = c.take(N * nb * 2);
     int rc = weight_alloc(s,w,c.offset,&w->planar);
@@ -347,7 +360,9 @@ int matvec(pixhip_session* s, pixhip_weight* w, const float* x, const pixhip::Ou
 {
     hipError_t e;
     if (w->type == PIX_Q5_K) {
-        e = pixhip::launch_matvec_q5_K(static_cast<const uint8_t*>(w->raw),x,w->rows,w->inner,out,s->stream);
+        int rc = ensure_matvec_form(s,w);
+        if (rc) return rc;
+        e = pixhip::launch_matvec_q5_K(w->q5p,x,w->rows,w->inner,out,s->stream);
     } else if (w->type == PIX_Q8_0) {
         e = pixhip::launch_matvec_q8_0(w->q80,x,w->rows,w->inner,out,s->stream);
     } else {

@@ -109,17 +109,16 @@ __device__ __forceinline__ void store_row(const Output& out, size_t n, float v)
     out.y[out.offset + n] = v + (out.bias? out.bias[n] : 0.0f);
 }
 
-// ---------------------------------------------------------------- Q5_K (GGUF bytes)
-// Weight registers of kMvRows rows: unit u = lane + 64k of a row is a quarter
-// super-block (two 32-value sub-blocks): its block's first 48 bytes (d, dmin,
-// scales, qh) and its 32 bytes of nibbles.
+// ---------------------------------------------------------------- Q5_K (planar)
+// Weight registers of kMvRows rows: unit u = lane + 64k of a row covers two
+// 32-value sub-blocks (2j, 2j+1 of super-block u/4): its 32 nibble bytes and
+// its 16-byte record (high bits, scales and minima, d and dmin).
 template <int UPL> struct Q5Rows {
-    uint4 head[kMvRows][UPL], qh0[kMvRows][UPL], qh1[kMvRows][UPL], qs0[kMvRows][UPL], qs1[kMvRows][UPL];
+    uint4 qs0[kMvRows][UPL], qs1[kMvRows][UPL], meta[kMvRows][UPL];
 };
 
 template <int UPL>
-__device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const uint8_t* __restrict__ w, size_t row_bytes, int r0, int last,
-                                        int lane, int units)
+__device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const PlanarQ5K& w, int K, int r0, int last, int lane, int units)
 {
 #pragma unroll
     for (int rr = 0; rr < kMvRows; rr++) {
@@ -128,12 +127,10 @@ __device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const uint8_t* __restric
         for (int k = 0; k < UPL; k++) {
             const int u = lane + 64 * k;
             if (u < units) {
-                const uint4* p = reinterpret_cast<const uint4*>(w + (size_t)row * row_bytes + (size_t)(u >> 2) * PIX_Q5_K_BYTES);
-                f.head[rr][k] = p[0];
-                f.qh0[rr][k] = p[1];
-                f.qh1[rr][k] = p[2];
-                f.qs0[rr][k] = p[3 + 2 * (u & 3)];
-                f.qs1[rr][k] = p[4 + 2 * (u & 3)];
+                const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2) + 32 * u);
+                f.qs0[rr][k] = q[0];
+                f.qs1[rr][k] = q[1];
+                f.meta[rr][k] = w.meta[(size_t)row * units + u];
             }
         }
     }
@@ -159,35 +156,31 @@ __device__ __forceinline__ void q5_compute(const Q5Rows<UPL>& f, float part[kMvR
         const int bs1 = sB[b * 16 + 4 * j + 2] + sB[b * 16 + 4 * j + 3];
 #pragma unroll
         for (int rr = 0; rr < kMvRows; rr++) {
-            const uint4 h = f.head[rr][k];
-            int sc0, mn0, sc1, mn1;
-            q5_scale_min(h.y,h.z,h.w,2 * j,sc0,mn0);
-            q5_scale_min(h.y,h.z,h.w,2 * j + 1,sc1,mn1);
-            const uint32_t qhw[8] = {f.qh0[rr][k].x,f.qh0[rr][k].y,f.qh0[rr][k].z,f.qh0[rr][k].w,
-                                     f.qh1[rr][k].x,f.qh1[rr][k].y,f.qh1[rr][k].z,f.qh1[rr][k].w};
+            const uint4 m = f.meta[rr][k];
             const uint32_t qsw[8] = {f.qs0[rr][k].x,f.qs0[rr][k].y,f.qs0[rr][k].z,f.qs0[rr][k].w,
                                      f.qs1[rr][k].x,f.qs1[rr][k].y,f.qs1[rr][k].z,f.qs1[rr][k].w};
             int dot0 = 0, dot1 = 0;
 #pragma unroll
             for (int q = 0; q < 8; q++) {
-                const uint32_t lo = qsw[q] & 0x0f0f0f0fu;
-                const uint32_t hi = (qsw[q] >> 4) & 0x0f0f0f0fu;
-                const uint32_t b0 = ((qhw[q] >> (2 * j)) & 0x01010101u) << 4;
-                const uint32_t b1 = ((qhw[q] >> (2 * j + 1)) & 0x01010101u) << 4;
-                dot0 = sdot4(lo | b0,xa[q],dot0);
-                dot1 = sdot4(hi | b1,xb[q],dot1);
+                const uint32_t t = (q < 4? m.x : m.y) >> (2 * (q & 3));
+                const uint32_t lo = (qsw[q] & 0x0f0f0f0fu) | ((t & 0x01010101u) << 4);
+                const uint32_t hi = ((qsw[q] >> 4) & 0x0f0f0f0fu) | (((t >> 1) & 0x01010101u) << 4);
+                dot0 = sdot4(lo,xa[q],dot0);
+                dot1 = sdot4(hi,xb[q],dot1);
             }
+            const int sc0 = (int)(m.z & 255u), sc1 = (int)((m.z >> 8) & 255u);
+            const int mn0 = (int)((m.z >> 16) & 255u), mn1 = (int)(m.z >> 24);
             const int S = sc0 * dot0 + sc1 * dot1;
             const int Mn = mn0 * bs0 + mn1 * bs1;
-            const float wd = half_bits_to_float((uint16_t)(h.x & 0xffffu));
-            const float wm = half_bits_to_float((uint16_t)(h.x >> 16));
+            const float wd = half_bits_to_float((uint16_t)(m.w & 0xffffu));
+            const float wm = half_bits_to_float((uint16_t)(m.w >> 16));
             part[rr] = __builtin_fmaf(yd,__builtin_fmaf(-wm,(float)Mn,wd * (float)S),part[rr]);
         }
     }
 }
 
 template <int UPL>
-__global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+__global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(PlanarQ5K w, const float* __restrict__ x,
                                                                     int N, int K, Output out)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -196,7 +189,6 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t row_bytes = (size_t)nb * PIX_Q5_K_BYTES;
     const int stride = (int)gridDim.x * kMvWaves * kMvRows;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
     const int last = N;
@@ -207,12 +199,12 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(const uint8_
     float4 xv[4 * UPL];
     load_x_q8_K(x,K,xv);
     Q5Rows<UPL> cur, nxt;
-    if (first < last) q5_load(cur,w,row_bytes,first,last,lane,units);
+    if (first < last) q5_load(cur,w,K,first,last,lane,units);
     quantize_x_q8_K(xv,K,sQ,sD,sB);
     __syncthreads();
     for (int r0 = first; r0 < last; r0 += stride) {
         const bool more = r0 + stride < last;
-        if (more) q5_load(nxt,w,row_bytes,r0 + stride,last,lane,units);
+        if (more) q5_load(nxt,w,K,r0 + stride,last,lane,units);
         float part[kMvRows];
         q5_compute(cur,part,sQ,sD,sB,lane,units);
 #pragma unroll
@@ -446,7 +438,7 @@ static hipError_t dispatch_upl(int units, F&& f)
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_matvec_q5_K(const uint8_t* raw, const float* x, size_t N, size_t K, const Output& out, hipStream_t s)
+hipError_t launch_matvec_q5_K(const PlanarQ5K& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s)
 {
     const size_t nb = K / PIX_QK;
     const size_t lds = K + 4 * nb + 4 * 16 * nb;
@@ -454,7 +446,7 @@ hipError_t launch_matvec_q5_K(const uint8_t* raw, const float* x, size_t N, size
         auto kernel = matvec_q5_K_kernel<decltype(upl)::value>;
         unsigned grid;
         launch_shape(kernel,lds,N,grid);
-        kernel<<<grid,64 * kMvWaves,lds,s>>>(raw,x,(int)N,(int)K,out);
+        kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out);
         return hipGetLastError();
     });
 }

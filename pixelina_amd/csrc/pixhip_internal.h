@@ -26,7 +26,13 @@
 //   weights Q8_0 ("planar", GEMM and matvec), rows of Kp with a zero pad block:
 //     qs int8 [Npad][Kp], d fp16 [N][Kp/32], and for the GEMM the same scales
 //     widened and transposed, dT fp32 [Kp/32][Npad]
-//   weights Q5_K for the matvec: the GGUF bytes unchanged (176-B blocks are 16-B aligned)
+//   weights Q5_K for the matvec ("q5 planar"): per row, the GGUF nibbles unchanged,
+//     qs u8 [N][K/2], and one 16-B record per 64 values (unit u = 4b + j covers
+//     sub-blocks 2j, 2j+1 of super-block b), meta [N][K/64][16]:
+//       bytes 0..7   the unit's 64 high bits: word w = 0, 1 holds, for qh words
+//                    4w..4w+3, ((qh >> 2j) & 0x03030303) << 2*(qword & 3)
+//       bytes 8..11  scale_2j, scale_2j+1, min_2j, min_2j+1 (six-bit values as bytes)
+//       bytes 12..15 d, dmin (fp16 bits, as in the block)
 //   weights Q6_K for the matvec ("q6 planar"): ql u8 [N][K/2], qh u8 [N][K/4],
 //     sc int8 [N][K/16], d fp16 [N][K/256] -- same bytes as GGUF, re-sliced so every
 //     plane is 16-B aligned (210-B blocks are only 2-B aligned).
@@ -85,6 +91,11 @@ struct PlanarQ80 {
     const float* dT;      // [Kp/32][Npad] (GEMM)
 };
 
+struct PlanarQ5K {
+    const uint8_t* qs;    // [N][K/2]
+    const uint4* meta;    // [N][K/64]
+};
+
 struct PlanarQ6K {
     const uint8_t* ql;
     const uint8_t* qh;
@@ -110,6 +121,7 @@ hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, siz
                               float* dm, _Float16* mn, hipStream_t s);
 hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
                                      hipStream_t s);
+hipError_t launch_repack_q5_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* qs, uint4* meta, hipStream_t s);
 hipError_t launch_repack_q6_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* ql, uint8_t* qh, int8_t* sc,
                                      _Float16* d, hipStream_t s);
 hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, size_t kpad, size_t rows_pad, int8_t* qs, _Float16* d,
@@ -125,7 +137,7 @@ hipError_t launch_sums_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t
 hipError_t launch_sums_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s);
 
 // matvec.hip
-hipError_t launch_matvec_q5_K(const uint8_t* raw, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
+hipError_t launch_matvec_q5_K(const PlanarQ5K& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
 hipError_t launch_matvec_q8_0(const PlanarQ80& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
 hipError_t launch_matvec_q6_K(const PlanarQ6K& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
 

@@ -158,6 +158,43 @@ hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inn
     return hipGetLastError();
 }
 
+// Q5_K matvec form: one thread per 64-value unit (the nibbles are copied, the
+// rest re-sliced into the unit's 16-byte record).
+__global__ __launch_bounds__(256) void repack_q5_K_planar_kernel(const uint8_t* __restrict__ raw, size_t rows, size_t inner,
+                                                                 uint8_t* __restrict__ qs, uint4* __restrict__ meta)
+{
+    const size_t units = inner / 64;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows * units) return;
+    const size_t row = t / units, u = t % units, b = u / 4;
+    const int j = (int)(u % 4);
+    const uint8_t* src = raw + (row * (inner / PIX_QK) + b) * PIX_Q5_K_BYTES;
+    // 176 bytes: d, dmin 0..3, scales 4..15, qh 16..47, qs 48..175
+    const uint4* q4 = reinterpret_cast<const uint4*>(src + 48 + 32 * j);
+    uint4* dq = reinterpret_cast<uint4*>(qs + row * (inner / 2) + b * 128 + 32 * j);
+    dq[0] = q4[0];
+    dq[1] = q4[1];
+    uint32_t h[2] = {0,0};
+    for (int q = 0; q < 8; q++) {
+        const uint32_t w = load_u32_aligned(src + 16 + 4 * q);
+        h[q >> 2] |= ((w >> (2 * j)) & 0x03030303u) << (2 * (q & 3));
+    }
+    const uint32_t w0 = load_u32_aligned(src + 4), w1 = load_u32_aligned(src + 8), w2 = load_u32_aligned(src + 12);
+    int sc0, mn0, sc1, mn1;
+    q5_scale_min(w0,w1,w2,2 * j,sc0,mn0);
+    q5_scale_min(w0,w1,w2,2 * j + 1,sc1,mn1);
+    meta[row * units + u] = make_uint4(h[0],h[1],(uint32_t)sc0 | ((uint32_t)sc1 << 8) | ((uint32_t)mn0 << 16) | ((uint32_t)mn1 << 24),
+                                       load_u32_aligned(src));
+}
+
+hipError_t launch_repack_q5_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* qs, uint4* meta, hipStream_t s)
+{
+    const size_t n = rows * (inner / 64);
+    if (!n) return hipSuccess;
+    repack_q5_K_planar_kernel<<<dim3((unsigned)((n + 255) / 256)),256,0,s>>>(raw,rows,inner,qs,meta);
+    return hipGetLastError();
+}
+
 hipError_t launch_repack_q6_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* ql, uint8_t* qh, int8_t* sc,
                                      _Float16* d, hipStream_t s)
 {
