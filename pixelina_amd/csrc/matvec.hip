@@ -14,6 +14,13 @@
 // grid (wave g takes pairs g, g + W, g + 2W, ...), so at any moment the waves
 // of the whole device read one contiguous band of the matrix: DRAM sees a
 // front-to-back stream, as a plain copy does.
+//
+// The loads are kept free of branches (row and unit indices are clamped into
+// the matrix; the surplus lanes' values are ignored) and no store is issued
+// while weight loads are in flight: loads and stores share the vector memory
+// counter, and a wait for the current rows would otherwise have to drain the
+// next rows' loads as well.  Each wave keeps two register sets of rows and
+// alternates between them, so one set is computed while the other streams in.
 #include <algorithm>
 
 #include "pixhip_device.h"
@@ -23,41 +30,57 @@ namespace pixhip {
 
 constexpr int kMvWaves = 8;
 constexpr int kMvRows = 2;  // rows in flight per wave iteration
+// s_waitcnt vmcnt(n) with the export and LDS/scalar counters left alone
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+constexpr int wait_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
+constexpr int kWaitVmcnt0 = wait_vmcnt(0);
+
+// The wave's index in the workgroup, as a wave-uniform (scalar) value: the row
+// loops then branch on scalars and never run with part of the wave masked off.
+__device__ __forceinline__ int wave_id()
+{
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
 
 // x staging is split in two so that its global loads go out first (before
 // the first weight rows are requested) and its quantization runs while the
-// weight loads are in flight.  Each wave takes blocks wave, wave+4, ...; P
-// bounds the blocks per wave (Q8_K) or 8-block passes per wave (Q8_0).
+// weight loads are in flight.  Each wave takes blocks wave, wave+8, ...; P
+// bounds the blocks per wave (Q8_K) or 8-block passes per wave (Q8_0).  The
+// loads past the last block re-read the last block (no branch around them).
 
 // Q8_K: one wave per 256-value block, a float4 per lane.
 template <int P>
 __device__ __forceinline__ void load_x_q8_K(const float* __restrict__ x, int K, float4 (&v)[P])
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int nb = K / PIX_QK;
 #pragma unroll
     for (int i = 0; i < P; i++) {
-        const int b = wave + kMvWaves * i;
-        if (b < nb) v[i] = reinterpret_cast<const float4*>(x + b * PIX_QK)[lane];
+        const int b = min(wave + kMvWaves * i,nb - 1);
+        v[i] = reinterpret_cast<const float4*>(x + b * PIX_QK)[lane];
     }
 }
 
 template <int P>
 __device__ __forceinline__ void quantize_x_q8_K(const float4 (&v)[P], int K, int8_t* sQ, float* sD, int* sB)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int nb = K / PIX_QK;
+    // Every pass runs (a pass past the last block quantizes the re-read last
+    // block and stores nothing), so that x's loads are used on every path and
+    // stay ahead of the weight loads.
 #pragma unroll
     for (int i = 0; i < P; i++) {
         const int b = wave + kMvWaves * i;
-        if (b >= nb) break;
         uint32_t packed;
         float d;
         int gsum;
         quantize_q8_K_wave(v[i],lane,packed,d,gsum);
-        reinterpret_cast<uint32_t*>(sQ + b * PIX_QK)[lane] = packed;
-        if (lane == 0) sD[b] = d;
-        if ((lane & 3) == 0) sB[b * 16 + (lane >> 2)] = gsum;
+        if (b < nb) {
+            reinterpret_cast<uint32_t*>(sQ + b * PIX_QK)[lane] = packed;
+            if (lane == 0) sD[b] = d;
+            if ((lane & 3) == 0) sB[b * 16 + (lane >> 2)] = gsum;
+        }
     }
 }
 
@@ -66,28 +89,28 @@ __device__ __forceinline__ void quantize_x_q8_K(const float4 (&v)[P], int K, int
 template <int P>
 __device__ __forceinline__ void load_x_q8_0(const float* __restrict__ x, int K, float4 (&v)[P])
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int nb = K / PIX_QK8;
 #pragma unroll
     for (int i = 0; i < P; i++) {
-        const int b = (wave + kMvWaves * i) * 8 + (lane >> 3);
-        if (b < nb) v[i] = reinterpret_cast<const float4*>(x + b * PIX_QK8)[lane & 7];
+        const int b = min((wave + kMvWaves * i) * 8 + (lane >> 3),nb - 1);
+        v[i] = reinterpret_cast<const float4*>(x + b * PIX_QK8)[lane & 7];
     }
 }
 
 template <int P>
 __device__ __forceinline__ void quantize_x_q8_0(const float4 (&v)[P], int K, int Kp, int8_t* sQ, float* sD)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int nb = K / PIX_QK8;
     if (Kp > K) {
         for (int i = threadIdx.x; i < Kp - K; i += blockDim.x) sQ[K + i] = 0;
         if (threadIdx.x == 0) sD[nb] = 0.0f;
     }
+    // Every pass runs, as in quantize_x_q8_K.
 #pragma unroll
     for (int i = 0; i < P; i++) {
         const int b = (wave + kMvWaves * i) * 8 + (lane >> 3);
-        if ((wave + kMvWaves * i) * 8 >= nb) break;  // wave-uniform
         uint32_t packed;
         float d32;
         uint16_t dh;
@@ -109,6 +132,80 @@ __device__ __forceinline__ void store_row(const Output& out, size_t n, float v)
     out.y[out.offset + n] = v + (out.bias? out.bias[n] : 0.0f);
 }
 
+// Row totals of one wave, parked one per lane: lane j holds row
+// base + (j / kMvRows) * stride + j % kMvRows.  They are written when all 64
+// lanes are taken (a wave with more than 64 / kMvRows row groups) and at the end.
+struct RowResults {
+    float v;
+    int slot, base;
+};
+
+__device__ __forceinline__ void results_flush(RowResults& r, int lane, int stride, int last, const Output& out)
+{
+    if (lane < r.slot) {
+        const int row = r.base + (lane / kMvRows) * stride + lane % kMvRows;
+        if (row < last) store_row(out,(size_t)row,r.v);
+    }
+    r.base += (64 / kMvRows) * stride;
+    r.slot = 0;
+}
+
+__device__ __forceinline__ void results_put(RowResults& r, const float (&part)[kMvRows], int lane, int stride, int last,
+                                            const Output& out)
+{
+#pragma unroll
+    for (int rr = 0; rr < kMvRows; rr++) {
+        const float t = wave_sum(part[rr]);
+        r.v = lane == r.slot + rr? t : r.v;
+    }
+    r.slot += kMvRows;
+    if (r.slot == 64) {
+        results_flush(r,lane,stride,last,out);
+        // Drain the stores here, so that no store is outstanding when the
+        // caller next waits for row loads.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    }
+}
+
+// The row loop of every matvec kernel.  `load(rows, r0)` requests the rows
+// r0 .. r0 + kMvRows - 1 (clamped to the matrix) into one register set,
+// `dot(rows, part)` computes their partial sums; set a holds the rows of
+// `first` on entry.  With TWO_SETS the next rows stream into set b while set
+// a is computed; without (long rows, whose two sets would not fit in the
+// registers) a wave computes a set before requesting the next.
+template <bool TWO_SETS, class Rows, class Load, class Dot>
+__device__ __forceinline__ void stream_rows(Rows& a, Rows& b, int first, int stride, int last, int lane, const Output& out,
+                                            Load load, Dot dot)
+{
+    // The loops have no exit in their middle: the compiler's wait analysis
+    // would otherwise see the exit path's loads still pending at the loop head.
+    RowResults res{0.0f,0,first};
+    float part[kMvRows];
+    int r0 = first;
+    if constexpr (TWO_SETS) {
+        for (; r0 + stride < last; r0 += 2 * stride) {
+            load(b,r0 + stride);
+            dot(a,part);
+            results_put(res,part,lane,stride,last,out);
+            load(a,r0 + 2 * stride);
+            dot(b,part);
+            results_put(res,part,lane,stride,last,out);
+        }
+    } else {
+        (void)b;
+        for (; r0 + stride < last; r0 += stride) {
+            dot(a,part);
+            results_put(res,part,lane,stride,last,out);
+            load(a,r0 + stride);
+        }
+    }
+    if (r0 < last) {  // set a holds rows r0.. (requested by the last pass)
+        dot(a,part);
+        results_put(res,part,lane,stride,last,out);
+    }
+    results_flush(res,lane,stride,last,out);
+}
+
 // ---------------------------------------------------------------- Q5_K (planar)
 // Weight registers of kMvRows rows: unit u = lane + 64k of a row covers two
 // 32-value sub-blocks (2j, 2j+1 of super-block u/4): its 32 nibble bytes and
@@ -125,13 +222,11 @@ __device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const PlanarQ5K& w, int 
         const int row = min(r0 + rr,last - 1);
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
-            const int u = lane + 64 * k;
-            if (u < units) {
-                const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2) + 32 * u);
-                f.qs0[rr][k] = q[0];
-                f.qs1[rr][k] = q[1];
-                f.meta[rr][k] = w.meta[(size_t)row * units + u];
-            }
+            const int u = min(lane + 64 * k,units - 1);
+            const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2) + 32 * u);
+            f.qs0[rr][k] = q[0];
+            f.qs1[rr][k] = q[1];
+            f.meta[rr][k] = w.meta[(size_t)row * units + u];
         }
     }
 }
@@ -188,32 +283,27 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(PlanarQ5K w,
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int stride = (int)gridDim.x * kMvWaves * kMvRows;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
     const int last = N;
     const int units = nb * 4;
     // The first rows' weights are requested before x is staged, so their
-    // latency overlaps the quantization of x; afterwards each iteration
-    // requests the next rows before computing the current ones.
-    float4 xv[4 * UPL];
+    // latency overlaps the quantization of x.
+    float4 xv[2 * UPL];
     load_x_q8_K(x,K,xv);
-    Q5Rows<UPL> cur, nxt;
-    if (first < last) q5_load(cur,w,K,first,last,lane,units);
+    __builtin_amdgcn_sched_barrier(0);
+    Q5Rows<UPL> a, b;
+    q5_load(a,w,K,first,last,lane,units);
+    __builtin_amdgcn_sched_barrier(0);
     quantize_x_q8_K(xv,K,sQ,sD,sB);
+    // x's loads were issued before the rows' 3 * kMvRows * UPL: this wait marks
+    // them complete on every path (a wave may skip its last quantization pass).
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(3 * kMvRows * UPL));
     __syncthreads();
-    for (int r0 = first; r0 < last; r0 += stride) {
-        const bool more = r0 + stride < last;
-        if (more) q5_load(nxt,w,K,r0 + stride,last,lane,units);
-        float part[kMvRows];
-        q5_compute(cur,part,sQ,sD,sB,lane,units);
-#pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
-            const float v = wave_sum(part[rr]);
-            if (lane == 0 && r0 + rr < last) store_row(out,(size_t)(r0 + rr),v);
-        }
-        if (more) cur = nxt;
-    }
+    stream_rows<true>(a,b,first,stride,last,lane,out,
+                [&](Q5Rows<UPL>& f, int r0) { q5_load(f,w,K,r0,last,lane,units); },
+                [&](const Q5Rows<UPL>& f, float (&part)[kMvRows]) { q5_compute(f,part,sQ,sD,sB,lane,units); });
 }
 
 // ---------------------------------------------------------------- Q8_0 (planar)
@@ -233,13 +323,11 @@ __device__ __forceinline__ void q80_load(Q80Rows<UPL>& f, const PlanarQ80& w, in
         const int row = min(r0 + rr,last - 1);
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
-            const int u = lane + 64 * k;
-            if (u < units) {
-                const uint4* p = reinterpret_cast<const uint4*>(w.qs + (size_t)row * Kp + 64 * u);
+            const int u = min(lane + 64 * k,units - 1);
+            const uint4* p = reinterpret_cast<const uint4*>(w.qs + (size_t)row * Kp + 64 * u);
 #pragma unroll
-                for (int t = 0; t < 4; t++) f.q[rr][k][t] = p[t];
-                f.dd[rr][k] = *reinterpret_cast<const uint32_t*>(w.d + (size_t)row * nbp + 2 * u);
-            }
+            for (int t = 0; t < 4; t++) f.q[rr][k][t] = p[t];
+            f.dd[rr][k] = *reinterpret_cast<const uint32_t*>(w.d + (size_t)row * nbp + 2 * u);
         }
     }
 }
@@ -286,34 +374,105 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w,
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + Kp);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int stride = (int)gridDim.x * kMvWaves * kMvRows;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
     const int last = N;
     const int units = Kp / 64;
-    float4 xv[4 * UPL];
+    float4 xv[2 * UPL];
     load_x_q8_0(x,K,xv);
-    Q80Rows<UPL> cur, nxt;
-    if (first < last) q80_load(cur,w,Kp,first,last,lane,units);
+    __builtin_amdgcn_sched_barrier(0);
+    Q80Rows<UPL> a, b;
+    q80_load(a,w,Kp,first,last,lane,units);
+    __builtin_amdgcn_sched_barrier(0);
     quantize_x_q8_0(xv,K,Kp,sQ,sD);
+    // x's loads precede the rows' 5 * kMvRows * UPL (see the Q5_K kernel).
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(5 * kMvRows * UPL));
     __syncthreads();
-    for (int r0 = first; r0 < last; r0 += stride) {
-        const bool more = r0 + stride < last;
-        if (more) q80_load(nxt,w,Kp,r0 + stride,last,lane,units);
-        float part[kMvRows];
-        q80_compute(cur,part,sQ,sD,lane,units);
-#pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
-            const float v = wave_sum(part[rr]);
-            if (lane == 0 && r0 + rr < last) store_row(out,(size_t)(r0 + rr),v);
-        }
-        if (more) cur = nxt;
-    }
+    stream_rows<(UPL <= 3)>(a,b,first,stride,last,lane,out,
+                [&](Q80Rows<UPL>& f, int r0) { q80_load(f,w,Kp,r0,last,lane,units); },
+                [&](const Q80Rows<UPL>& f, float (&part)[kMvRows]) { q80_compute(f,part,sQ,sD,lane,units); });
 }
 
 // ---------------------------------------------------------------- Q6_K (planar)
 // Unit u of a row: super-block b = u/4, half h = (u/2)%2, position half ih = u%2;
 // it covers elements 128h + 32g + 16ih + i for g = 0..3, i = 0..15.
+template <int UPL> struct Q6Rows {
+    uint4 la[kMvRows][UPL], lb[kMvRows][UPL], hh[kMvRows][UPL];
+    uint2 scw[kMvRows][UPL];
+    uint16_t dh[kMvRows][UPL];
+};
+
+template <int UPL>
+__device__ __forceinline__ void q6_load(Q6Rows<UPL>& f, const PlanarQ6K& w, int K, int r0, int last, int lane, int units)
+{
+    const int nb = K / PIX_QK;
+#pragma unroll
+    for (int rr = 0; rr < kMvRows; rr++) {
+        const int row = min(r0 + rr,last - 1);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = min(lane + 64 * k,units - 1);
+            const int b = u >> 2, h = (u >> 1) & 1, ih = u & 1;
+            const uint8_t* ql = w.ql + (size_t)row * (K / 2) + b * 128 + 64 * h + 16 * ih;
+            f.la[rr][k] = *reinterpret_cast<const uint4*>(ql);
+            f.lb[rr][k] = *reinterpret_cast<const uint4*>(ql + 32);
+            f.hh[rr][k] = *reinterpret_cast<const uint4*>(w.qh + (size_t)row * (K / 4) + b * 64 + 32 * h + 16 * ih);
+            f.scw[rr][k] = *reinterpret_cast<const uint2*>(w.sc + (size_t)row * (K / 16) + b * 16 + 8 * h);
+            f.dh[rr][k] = __builtin_bit_cast(uint16_t,w.d[(size_t)row * nb + b]);
+        }
+    }
+}
+
+template <int UPL>
+__device__ __forceinline__ void q6_compute(const Q6Rows<UPL>& f, float part[kMvRows], const int8_t* sQ, const float* sD,
+                                           const int* sB, int lane, int units)
+{
+#pragma unroll
+    for (int rr = 0; rr < kMvRows; rr++) part[rr] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const int u = lane + 64 * k;
+        if (u >= units) continue;
+        const int b = u >> 2, h = (u >> 1) & 1, ih = u & 1;
+        uint32_t xw[4][4];
+        int bsg[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint4 t = *reinterpret_cast<const uint4*>(sQ + b * PIX_QK + 128 * h + 32 * g + 16 * ih);
+            xw[g][0] = t.x; xw[g][1] = t.y; xw[g][2] = t.z; xw[g][3] = t.w;
+            bsg[g] = sB[b * 16 + 8 * h + 2 * g + ih];
+        }
+        const float yd = sD[b];
+#pragma unroll
+        for (int rr = 0; rr < kMvRows; rr++) {
+            const uint32_t lw[8] = {f.la[rr][k].x,f.la[rr][k].y,f.la[rr][k].z,f.la[rr][k].w,
+                                    f.lb[rr][k].x,f.lb[rr][k].y,f.lb[rr][k].z,f.lb[rr][k].w};
+            const uint32_t hw[4] = {f.hh[rr][k].x,f.hh[rr][k].y,f.hh[rr][k].z,f.hh[rr][k].w};
+            const uint32_t s0 = f.scw[rr][k].x, s1 = f.scw[rr][k].y;
+            int total = 0;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                int dot = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t low = (g & 1)? lw[4 + q] : lw[q];
+                    const uint32_t nib = (g < 2)? (low & 0x0f0f0f0fu) : ((low >> 4) & 0x0f0f0f0fu);
+                    const uint32_t top = ((hw[q] >> (2 * g)) & 0x03030303u) << 4;
+                    dot = sdot4(nib | top,xw[g][q],dot);
+                }
+                // scale of elements 128h + 32g + 16ih.. : byte 2g + ih of this half's 8 scales
+                const int sidx = 2 * g + ih;
+                const uint32_t sw = sidx < 4? s0 : s1;
+                const int sc = (int)(int8_t)(uint8_t)((sw >> (8 * (sidx & 3))) & 255u);
+                total += sc * (dot - 32 * bsg[g]);
+            }
+            const float wd = half_bits_to_float(f.dh[rr][k]);
+            part[rr] = __builtin_fmaf(yd * wd,(float)total,part[rr]);
+        }
+    }
+}
+
 template <int UPL>
 __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w, const float* __restrict__ x, int N, int K,
                                                                     Output out)
@@ -323,87 +482,28 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
-    {
-        float4 xv[4 * UPL];
-        load_x_q8_K(x,K,xv);
-        quantize_x_q8_K(xv,K,sQ,sD,sB);
-    }
-    __syncthreads();
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int stride = (int)gridDim.x * kMvWaves * kMvRows;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
     const int last = N;
     const int units = nb * 4;
-    for (int r0 = first; r0 < last; r0 += stride) {
-        float part[kMvRows];
-        uint4 la[kMvRows][UPL], lb[kMvRows][UPL], hh[kMvRows][UPL];
-        uint2 scw[kMvRows][UPL];
-        uint16_t dh[kMvRows][UPL];
-#pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
-            part[rr] = 0.0f;
-            const int row = min(r0 + rr,last - 1);
-#pragma unroll
-            for (int k = 0; k < UPL; k++) {
-                const int u = lane + 64 * k;
-                if (u < units) {
-                    const int b = u >> 2, h = (u >> 1) & 1, ih = u & 1;
-                    const uint8_t* ql = w.ql + (size_t)row * (K / 2) + b * 128 + 64 * h + 16 * ih;
-                    la[rr][k] = *reinterpret_cast<const uint4*>(ql);
-                    lb[rr][k] = *reinterpret_cast<const uint4*>(ql + 32);
-                    hh[rr][k] = *reinterpret_cast<const uint4*>(w.qh + (size_t)row * (K / 4) + b * 64 + 32 * h + 16 * ih);
-                    scw[rr][k] = *reinterpret_cast<const uint2*>(w.sc + (size_t)row * (K / 16) + b * 16 + 8 * h);
-                    dh[rr][k] = __builtin_bit_cast(uint16_t,w.d[(size_t)row * nb + b]);
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            const int u = lane + 64 * k;
-            if (u >= units) continue;
-            const int b = u >> 2, h = (u >> 1) & 1, ih = u & 1;
-            uint32_t xw[4][4];
-            int bsg[4];
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint4 t = *reinterpret_cast<const uint4*>(sQ + b * PIX_QK + 128 * h + 32 * g + 16 * ih);
-                xw[g][0] = t.x; xw[g][1] = t.y; xw[g][2] = t.z; xw[g][3] = t.w;
-                bsg[g] = sB[b * 16 + 8 * h + 2 * g + ih];
-            }
-            const float yd = sD[b];
-#pragma unroll
-            for (int rr = 0; rr < kMvRows; rr++) {
-                const uint32_t lw[8] = {la[rr][k].x,la[rr][k].y,la[rr][k].z,la[rr][k].w,lb[rr][k].x,lb[rr][k].y,lb[rr][k].z,lb[rr][k].w};
-                const uint32_t hw[4] = {hh[rr][k].x,hh[rr][k].y,hh[rr][k].z,hh[rr][k].w};
-                const uint32_t s0 = scw[rr][k].x, s1 = scw[rr][k].y;
-                int total = 0;
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    int dot = 0;
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const uint32_t low = (g & 1)? lw[4 + q] : lw[q];
-                        const uint32_t nib = (g < 2)? (low & 0x0f0f0f0fu) : ((low >> 4) & 0x0f0f0f0fu);
-                        const uint32_t top = ((hw[q] >> (2 * g)) & 0x03030303u) << 4;
-                        dot = sdot4(nib | top,xw[g][q],dot);
-                    }
-                    // scale of elements 128h + 32g + 16ih.. : byte 2g + ih of this half's 8 scales
-                    const int sidx = 2 * g + ih;
-                    const uint32_t sw = sidx < 4? s0 : s1;
-                    const int sc = (int)(int8_t)(uint8_t)((sw >> (8 * (sidx & 3))) & 255u);
-                    total += sc * (dot - 32 * bsg[g]);
-                }
-                const float wd = half_bits_to_float(dh[rr][k]);
-                part[rr] = __builtin_fmaf(yd * wd,(float)total,part[rr]);
-            }
-        }
-#pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
-            const float v = wave_sum(part[rr]);
-            if (lane == 0 && r0 + rr < last) store_row(out,(size_t)(r0 + rr),v);
-        }
-    }
+    float4 xv[2 * UPL];
+    load_x_q8_K(x,K,xv);
+    constexpr bool two_sets = UPL <= 2;
+    Q6Rows<UPL> a, b;
+    // Long rows: x is quantized before the first rows are requested, so that
+    // its staging registers are free again.
+    __builtin_amdgcn_sched_barrier(0);
+    if (two_sets) q6_load(a,w,K,first,last,lane,units);
+    __builtin_amdgcn_sched_barrier(0);
+    quantize_x_q8_K(xv,K,sQ,sD,sB);
+    // x's loads precede the rows' 5 * kMvRows * UPL (see the Q5_K kernel).
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(two_sets? 5 * kMvRows * UPL : 0));
+    if (!two_sets) q6_load(a,w,K,first,last,lane,units);
+    __syncthreads();
+    stream_rows<two_sets>(a,b,first,stride,last,lane,out,
+                [&](Q6Rows<UPL>& f, int r0) { q6_load(f,w,K,r0,last,lane,units); },
+                [&](const Q6Rows<UPL>& f, float (&part)[kMvRows]) { q6_compute(f,part,sQ,sD,sB,lane,units); });
 }
 
 // Launch shape: one round of workgroups that exactly fills the device (the
