@@ -30,6 +30,13 @@ namespace pixhip {
 
 constexpr int kMvWaves = 8;
 constexpr int kMvRows = 2;  // rows in flight per wave iteration
+// x staging passes per wave per 64 units of a row: a row of 64*UPL units has
+// at most 16*UPL Q8_K blocks (or 16*UPL passes of 8 Q8_0 blocks).
+constexpr int kXPasses = 16 / kMvWaves;
+// Workgroups per CU.  One (8 waves, each with two sets of two rows in flight)
+// streams fastest: measured against 2 or 3 smaller workgroups, 16 waves per
+// CU, and one set per wave.
+constexpr int kMvMaxWgPerCu = 1;
 // s_waitcnt vmcnt(n) with the export and LDS/scalar counters left alone
 // (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
 constexpr int wait_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
@@ -133,8 +140,9 @@ __device__ __forceinline__ void store_row(const Output& out, size_t n, float v)
 }
 
 // Row totals of one wave, parked one per lane: lane j holds row
-// base + (j / kMvRows) * stride + j % kMvRows.  They are written when all 64
-// lanes are taken (a wave with more than 64 / kMvRows row groups) and at the end.
+// base + (j / kMvRows) * stride + j % kMvRows.  They are written when no lanes
+// are left for another row group (a wave with more than 64 / kMvRows of them)
+// and at the end.
 struct RowResults {
     float v;
     int slot, base;
@@ -159,7 +167,7 @@ __device__ __forceinline__ void results_put(RowResults& r, const float (&part)[k
         r.v = lane == r.slot + rr? t : r.v;
     }
     r.slot += kMvRows;
-    if (r.slot == 64) {
+    if (r.slot > 64 - kMvRows) {
         results_flush(r,lane,stride,last,out);
         // Drain the stores here, so that no store is outstanding when the
         // caller next waits for row loads.
@@ -208,8 +216,9 @@ __device__ __forceinline__ void stream_rows(Rows& a, Rows& b, int first, int str
 
 // ---------------------------------------------------------------- Q5_K (planar)
 // Weight registers of kMvRows rows: unit u = lane + 64k of a row covers two
-// 32-value sub-blocks (2j, 2j+1 of super-block u/4): its 32 nibble bytes and
-// its 16-byte record (high bits, scales and minima, d and dmin).
+// 32-value sub-blocks (2j, 2j+1 of super-block u/4): its 32 nibble bytes (from
+// the row's two half planes) and its 16-byte record (high bits, scales and
+// minima, d and dmin).
 template <int UPL> struct Q5Rows {
     uint4 qs0[kMvRows][UPL], qs1[kMvRows][UPL], meta[kMvRows][UPL];
 };
@@ -223,9 +232,9 @@ __device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const PlanarQ5K& w, int 
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
             const int u = min(lane + 64 * k,units - 1);
-            const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2) + 32 * u);
-            f.qs0[rr][k] = q[0];
-            f.qs1[rr][k] = q[1];
+            const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2));
+            f.qs0[rr][k] = q[u];
+            f.qs1[rr][k] = q[units + u];
             f.meta[rr][k] = w.meta[(size_t)row * units + u];
         }
     }
@@ -290,7 +299,7 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(PlanarQ5K w,
     const int units = nb * 4;
     // The first rows' weights are requested before x is staged, so their
     // latency overlaps the quantization of x.
-    float4 xv[2 * UPL];
+    float4 xv[kXPasses * UPL];
     load_x_q8_K(x,K,xv);
     __builtin_amdgcn_sched_barrier(0);
     Q5Rows<UPL> a, b;
@@ -379,7 +388,7 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w,
     const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
     const int last = N;
     const int units = Kp / 64;
-    float4 xv[2 * UPL];
+    float4 xv[kXPasses * UPL];
     load_x_q8_0(x,K,xv);
     __builtin_amdgcn_sched_barrier(0);
     Q80Rows<UPL> a, b;
@@ -487,7 +496,7 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
     const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
     const int last = N;
     const int units = nb * 4;
-    float4 xv[2 * UPL];
+    float4 xv[kXPasses * UPL];
     load_x_q8_K(x,K,xv);
     constexpr bool two_sets = UPL <= 2;
     Q6Rows<UPL> a, b;
@@ -506,9 +515,9 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
                 [&](const Q6Rows<UPL>& f, float (&part)[kMvRows]) { q6_compute(f,part,sQ,sD,sB,lane,units); });
 }
 
-// Launch shape: one round of workgroups that exactly fills the device (the
-// kernel's occupancy times the CU count), or fewer when there are fewer row
-// pairs than waves; the kernels stride over the rest.
+// Launch shape: one round of workgroups, kMvMaxWgPerCu per CU (fewer when the
+// kernel's occupancy allows fewer, or when there are fewer row pairs than
+// waves); the kernels stride over the rest.
 template <typename Kernel>
 static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid)
 {
@@ -522,6 +531,7 @@ static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid)
     }
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu,kernel,64 * kMvWaves,lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    per_cu = std::min(per_cu,kMvMaxWgPerCu);
     const size_t waves_needed = (N + kMvRows - 1) / kMvRows;
     const size_t slots = (size_t)cus * per_cu * kMvWaves;
     const size_t waves = std::min(waves_needed,slots);

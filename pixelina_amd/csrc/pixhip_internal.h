@@ -26,9 +26,11 @@
 //   weights Q8_0 ("planar", GEMM and matvec), rows of Kp with a zero pad block:
 //     qs int8 [Npad][Kp], d fp16 [N][Kp/32], and for the GEMM the same scales
 //     widened and transposed, dT fp32 [Kp/32][Npad]
-//   weights Q5_K for the matvec ("q5 planar"): per row, the GGUF nibbles unchanged,
-//     qs u8 [N][K/2], and one 16-B record per 64 values (unit u = 4b + j covers
-//     sub-blocks 2j, 2j+1 of super-block b), meta [N][K/64][16]:
+//   weights Q5_K for the matvec ("q5 planar"): per row, the GGUF nibble bytes of
+//     unit u (64 values, u = 4b + j covers sub-blocks 2j, 2j+1 of super-block b)
+//     split into two half planes, qs u8 [N][2][K/64][16] (half 0: the unit's
+//     bytes 0..15, half 1: bytes 16..31), and one 16-B record per unit,
+//     meta [N][K/64][16]:
 //       bytes 0..7   the unit's 64 high bits: word w = 0, 1 holds, for qh words
 //                    4w..4w+3, ((qh >> 2j) & 0x03030303) << 2*(qword & 3)
 //       bytes 8..11  scale_2j, scale_2j+1, min_2j, min_2j+1 (six-bit values as bytes)

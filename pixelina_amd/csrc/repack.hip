@@ -170,10 +170,13 @@ __global__ __launch_bounds__(256) void repack_q5_K_planar_kernel(const uint8_t* 
     const int j = (int)(u % 4);
     const uint8_t* src = raw + (row * (inner / PIX_QK) + b) * PIX_Q5_K_BYTES;
     // 176 bytes: d, dmin 0..3, scales 4..15, qh 16..47, qs 48..175
+    // The unit's 32 nibble bytes go to two half planes of the row (bytes 0..15
+    // at 16u, bytes 16..31 at 16 * (units + u)): each of the matvec's two
+    // 16-B loads is then contiguous across the lanes of a wave.
     const uint4* q4 = reinterpret_cast<const uint4*>(src + 48 + 32 * j);
-    uint4* dq = reinterpret_cast<uint4*>(qs + row * (inner / 2) + b * 128 + 32 * j);
-    dq[0] = q4[0];
-    dq[1] = q4[1];
+    uint4* dq = reinterpret_cast<uint4*>(qs + row * (inner / 2));
+    dq[u] = q4[0];
+    dq[units + u] = q4[1];
     uint32_t h[2] = {0,0};
     for (int q = 0; q < 8; q++) {
         const uint32_t w = load_u32_aligned(src + 16 + 4 * q);
