@@ -314,10 +314,11 @@ template <int KIND> constexpr int outstanding(int P)
     return n;
 }
 
-// One iteration on stage c (PHASE = c % 4 for K-quants): start the DMA of stage
-// c+kDist into its A and W slots (and, when that stage starts a super-block,
-// its scales into other_sc), then compute on the A slot `cur` (the W slot is
-// at a fixed distance, folded into the lane's W offset) and `cur_scale`.
+// One iteration on stage c (PHASE = c % 4 for K-quants): compute on the A slot
+// `cur` (the W slot is at a fixed distance, folded into the lane's W offset)
+// and `cur_scale`, and, after the first of its two k-steps, start the DMA of
+// stage c+kDist into its A and W slots (and, when that stage starts a
+// super-block, its scales into other_sc).
 // other_sc is the scale buffer of the previous super-block, which odd waves
 // still read in the first stage of the next one (their deferred epilogue)
 // before it is refilled in a later iteration.  In every call the buffers
@@ -328,11 +329,6 @@ __device__ __forceinline__ void step(const GemmArgs& g, const Ctx& x, int c, boo
                                      const uint8_t* __restrict__ cur, const uint8_t* __restrict__ cur_scale)
 {
     constexpr int PLANES = KIND == KIND_Q80? 1 : 2;
-    if (c + kDist < x.nchunks) {
-        issue_stage<KIND>(g,x,c + kDist,dma_a,dma_w,discard);
-        if constexpr (KIND != KIND_Q80 && (PHASE + kDist) % kSBC == 0)
-            issue_scales<KIND>(g,x,(c + kDist) / kSBC,other_sc,discard);
-    }
     if constexpr (KIND != KIND_Q80 && PHASE == 0) {
         if (h1 && c > 0) {
             sb_epilogue<KIND,SUMS,0>(g,x,c / kSBC - 1,acc,other_sc);
@@ -388,6 +384,20 @@ __device__ __forceinline__ void step(const GemmArgs& g, const Ctx& x, int c, boo
                 acc.hi[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i],wh,z? izero : acc.hi[i],0,0,0);
                 acc.lo[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i],wl,z? izero : acc.lo[i],0,0,0);
             }
+        }
+        if (s == 0) {
+            // The DMAs go out after the first k-step's MFMAs rather than right
+            // after the barrier: issued there by all 16 waves at once they fill
+            // the address unit's queue, and each wave's issue stalls until its
+            // DMAs are accepted (measured ~480 cycles per stage); issued here,
+            // each wave already has MFMAs in flight while it waits.
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + kDist < x.nchunks) {
+                issue_stage<KIND>(g,x,c + kDist,dma_a,dma_w,discard);
+                if constexpr (KIND != KIND_Q80 && (PHASE + kDist) % kSBC == 0)
+                    issue_scales<KIND>(g,x,(c + kDist) / kSBC,other_sc,discard);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     if constexpr (KIND != KIND_Q80 && PHASE == kSBC - 1) {
