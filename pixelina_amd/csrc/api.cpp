@@ -44,7 +44,7 @@ constexpr size_t kTileN = PIX_GEMM_NTILE;  // GEMM feature-tile rows (weight pad
 constexpr size_t kTileM = PIX_GEMM_MTILE;  // GEMM token-tile rows (activation padding)
 constexpr size_t kAlign = 256;       // sub-allocation alignment
 constexpr double kHeapFraction = 0.85;  // VULKAN_HEAP_FRACTION, src/backend_vulkan.h:26
-constexpr size_t kMatvecMaxInner = 16384;  // matvec keeps x in LDS (64 units per lane x 4)
+constexpr size_t kMatvecMaxInner = 24576;  // matvec keeps x in LDS and a row in registers (64 units per lane x 6)
 
 bool supported_type(uint32_t t) { return t == PIX_Q8_0 || t == PIX_Q5_K || t == PIX_Q6_K; }
 size_t block_values(uint32_t t) { return t == PIX_Q8_0? PIX_QK8 : PIX_QK; }

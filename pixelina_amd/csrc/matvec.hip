@@ -6,7 +6,7 @@
 // row takes integer block dots and an fp32 epilogue.
 //
 // HBM-bound: every weight byte is read once with 128-bit loads; no MFMA.
-// Each workgroup re-quantizes x into LDS (K <= 16384 values: 16 KB), then every
+// Each workgroup re-quantizes x into LDS (K <= 24576 values: 24 KB), then every
 // wave streams whole rows: lane u owns one "unit" of 64 values of a row
 // (Q5_K: a quarter super-block = two 32-value sub-blocks; Q8_0: two blocks;
 // Q6_K: 16 positions x 4 groups of a half super-block) and the row total is a
@@ -29,7 +29,7 @@
 namespace pixhip {
 
 constexpr int kMvWaves = 8;
-constexpr int kMvRows = 2;  // rows in flight per wave iteration
+constexpr int kMvRows = 2;  // rows per register set (the longest Q8_0 and Q6_K rows use 1)
 // x staging passes per wave per 64 units of a row: a row of 64*UPL units has
 // at most 16*UPL Q8_K blocks (or 16*UPL passes of 8 Q8_0 blocks).
 constexpr int kXPasses = 16 / kMvWaves;
@@ -140,35 +140,37 @@ __device__ __forceinline__ void store_row(const Output& out, size_t n, float v)
 }
 
 // Row totals of one wave, parked one per lane: lane j holds row
-// base + (j / kMvRows) * stride + j % kMvRows.  They are written when no lanes
-// are left for another row group (a wave with more than 64 / kMvRows of them)
+// base + (j / R) * stride + j % R (R rows per set).  They are written when no
+// lanes are left for another row group (a wave with more than 64 / R of them)
 // and at the end.
 struct RowResults {
     float v;
     int slot, base;
 };
 
+template <int R>
 __device__ __forceinline__ void results_flush(RowResults& r, int lane, int stride, int last, const Output& out)
 {
     if (lane < r.slot) {
-        const int row = r.base + (lane / kMvRows) * stride + lane % kMvRows;
+        const int row = r.base + (lane / R) * stride + lane % R;
         if (row < last) store_row(out,(size_t)row,r.v);
     }
-    r.base += (64 / kMvRows) * stride;
+    r.base += (64 / R) * stride;
     r.slot = 0;
 }
 
-__device__ __forceinline__ void results_put(RowResults& r, const float (&part)[kMvRows], int lane, int stride, int last,
+template <int R>
+__device__ __forceinline__ void results_put(RowResults& r, const float (&part)[R], int lane, int stride, int last,
                                             const Output& out)
 {
 #pragma unroll
-    for (int rr = 0; rr < kMvRows; rr++) {
+    for (int rr = 0; rr < R; rr++) {
         const float t = wave_sum(part[rr]);
         r.v = lane == r.slot + rr? t : r.v;
     }
-    r.slot += kMvRows;
-    if (r.slot > 64 - kMvRows) {
-        results_flush(r,lane,stride,last,out);
+    r.slot += R;
+    if (r.slot > 64 - R) {
+        results_flush<R>(r,lane,stride,last,out);
         // Drain the stores here, so that no store is outstanding when the
         // caller next waits for row loads.
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -176,7 +178,7 @@ __device__ __forceinline__ void results_put(RowResults& r, const float (&part)[k
 }
 
 // The row loop of every matvec kernel.  `load(rows, r0)` requests the rows
-// r0 .. r0 + kMvRows - 1 (clamped to the matrix) into one register set,
+// r0 .. r0 + Rows::R - 1 (clamped to the matrix) into one register set,
 // `dot(rows, part)` computes their partial sums; set a holds the rows of
 // `first` on entry.  With TWO_SETS the next rows stream into set b while set
 // a is computed; without (long rows, whose two sets would not fit in the
@@ -187,47 +189,55 @@ __device__ __forceinline__ void stream_rows(Rows& a, Rows& b, int first, int str
 {
     // The loops have no exit in their middle: the compiler's wait analysis
     // would otherwise see the exit path's loads still pending at the loop head.
+    constexpr int R = Rows::R;
     RowResults res{0.0f,0,first};
-    float part[kMvRows];
+    float part[R];
     int r0 = first;
     if constexpr (TWO_SETS) {
         for (; r0 + stride < last; r0 += 2 * stride) {
             load(b,r0 + stride);
             dot(a,part);
-            results_put(res,part,lane,stride,last,out);
+            results_put<R>(res,part,lane,stride,last,out);
             load(a,r0 + 2 * stride);
             dot(b,part);
-            results_put(res,part,lane,stride,last,out);
+            results_put<R>(res,part,lane,stride,last,out);
         }
     } else {
         (void)b;
         for (; r0 + stride < last; r0 += stride) {
             dot(a,part);
-            results_put(res,part,lane,stride,last,out);
+            results_put<R>(res,part,lane,stride,last,out);
             load(a,r0 + stride);
         }
     }
     if (r0 < last) {  // set a holds rows r0.. (requested by the last pass)
         dot(a,part);
-        results_put(res,part,lane,stride,last,out);
+        results_put<R>(res,part,lane,stride,last,out);
     }
-    results_flush(res,lane,stride,last,out);
+    results_flush<R>(res,lane,stride,last,out);
 }
 
+// Rows per register set: two, except where two rows of a long row would not
+// fit in the registers (Q8_0 at 6 units per lane, Q6_K from 5).
+template <int UPL> constexpr int q5_rows() { return kMvRows; }
+template <int UPL> constexpr int q80_rows() { return UPL <= 5? kMvRows : 1; }
+template <int UPL> constexpr int q6_rows() { return UPL <= 4? kMvRows : 1; }
+
 // ---------------------------------------------------------------- Q5_K (planar)
-// Weight registers of kMvRows rows: unit u = lane + 64k of a row covers two
+// Weight registers of R rows: unit u = lane + 64k of a row covers two
 // 32-value sub-blocks (2j, 2j+1 of super-block u/4): its 32 nibble bytes (from
 // the row's two half planes) and its 16-byte record (high bits, scales and
 // minima, d and dmin).
-template <int UPL> struct Q5Rows {
-    uint4 qs0[kMvRows][UPL], qs1[kMvRows][UPL], meta[kMvRows][UPL];
+template <int UPL, int ROWS> struct Q5Rows {
+    static constexpr int R = ROWS;
+    uint4 qs0[R][UPL], qs1[R][UPL], meta[R][UPL];
 };
 
-template <int UPL>
-__device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const PlanarQ5K& w, int K, int r0, int last, int lane, int units)
+template <int UPL, int R>
+__device__ __forceinline__ void q5_load(Q5Rows<UPL,R>& f, const PlanarQ5K& w, int K, int r0, int last, int lane, int units)
 {
 #pragma unroll
-    for (int rr = 0; rr < kMvRows; rr++) {
+    for (int rr = 0; rr < R; rr++) {
         const int row = min(r0 + rr,last - 1);
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
@@ -240,12 +250,12 @@ __device__ __forceinline__ void q5_load(Q5Rows<UPL>& f, const PlanarQ5K& w, int 
     }
 }
 
-template <int UPL>
-__device__ __forceinline__ void q5_compute(const Q5Rows<UPL>& f, float part[kMvRows], const int8_t* sQ, const float* sD,
+template <int UPL, int R>
+__device__ __forceinline__ void q5_compute(const Q5Rows<UPL,R>& f, float part[R], const int8_t* sQ, const float* sD,
                                            const int* sB, int lane, int units)
 {
 #pragma unroll
-    for (int rr = 0; rr < kMvRows; rr++) part[rr] = 0.0f;
+    for (int rr = 0; rr < R; rr++) part[rr] = 0.0f;
 #pragma unroll
     for (int k = 0; k < UPL; k++) {
         const int u = lane + 64 * k;
@@ -259,7 +269,7 @@ __device__ __forceinline__ void q5_compute(const Q5Rows<UPL>& f, float part[kMvR
         const int bs0 = sB[b * 16 + 4 * j] + sB[b * 16 + 4 * j + 1];
         const int bs1 = sB[b * 16 + 4 * j + 2] + sB[b * 16 + 4 * j + 3];
 #pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
+        for (int rr = 0; rr < R; rr++) {
             const uint4 m = f.meta[rr][k];
             const uint32_t qsw[8] = {f.qs0[rr][k].x,f.qs0[rr][k].y,f.qs0[rr][k].z,f.qs0[rr][k].w,
                                      f.qs1[rr][k].x,f.qs1[rr][k].y,f.qs1[rr][k].z,f.qs1[rr][k].w};
@@ -293,8 +303,9 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(PlanarQ5K w,
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const int stride = (int)gridDim.x * kMvWaves * kMvRows;
-    const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
+    constexpr int R = q5_rows<UPL>();
+    const int stride = (int)gridDim.x * kMvWaves * R;
+    const int first = ((int)blockIdx.x * kMvWaves + wave) * R;
     const int last = N;
     const int units = nb * 4;
     // The first rows' weights are requested before x is staged, so their
@@ -302,33 +313,38 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(PlanarQ5K w,
     float4 xv[kXPasses * UPL];
     load_x_q8_K(x,K,xv);
     __builtin_amdgcn_sched_barrier(0);
-    Q5Rows<UPL> a, b;
-    q5_load(a,w,K,first,last,lane,units);
+    // Long rows (one register set): x is quantized before the first rows are
+    // requested, so that its staging registers are free again.
+    constexpr bool two_sets = UPL <= 4;
+    Q5Rows<UPL,R> a, b;
+    if (two_sets) q5_load(a,w,K,first,last,lane,units);
     __builtin_amdgcn_sched_barrier(0);
     quantize_x_q8_K(xv,K,sQ,sD,sB);
-    // x's loads were issued before the rows' 3 * kMvRows * UPL: this wait marks
-    // them complete on every path (a wave may skip its last quantization pass).
-    __builtin_amdgcn_s_waitcnt(wait_vmcnt(3 * kMvRows * UPL));
+    // x's loads were issued before the rows' 3 * R * UPL: this wait marks
+    // them complete on every path.
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(two_sets? 3 * R * UPL : 0));
+    if (!two_sets) q5_load(a,w,K,first,last,lane,units);
     __syncthreads();
-    stream_rows<true>(a,b,first,stride,last,lane,out,
-                [&](Q5Rows<UPL>& f, int r0) { q5_load(f,w,K,r0,last,lane,units); },
-                [&](const Q5Rows<UPL>& f, float (&part)[kMvRows]) { q5_compute(f,part,sQ,sD,sB,lane,units); });
+    stream_rows<two_sets>(a,b,first,stride,last,lane,out,
+                [&](Q5Rows<UPL,R>& f, int r0) { q5_load(f,w,K,r0,last,lane,units); },
+                [&](const Q5Rows<UPL,R>& f, float (&part)[R]) { q5_compute(f,part,sQ,sD,sB,lane,units); });
 }
 
 // ---------------------------------------------------------------- Q8_0 (planar)
 // Unit u of a row: 64 values (two blocks) of the planar quants and their two
 // fp16 scales.
-template <int UPL> struct Q80Rows {
-    uint4 q[kMvRows][UPL][4];
-    uint32_t dd[kMvRows][UPL];
+template <int UPL, int ROWS> struct Q80Rows {
+    static constexpr int R = ROWS;
+    uint4 q[R][UPL][4];
+    uint32_t dd[R][UPL];
 };
 
-template <int UPL>
-__device__ __forceinline__ void q80_load(Q80Rows<UPL>& f, const PlanarQ80& w, int Kp, int r0, int last, int lane, int units)
+template <int UPL, int R>
+__device__ __forceinline__ void q80_load(Q80Rows<UPL,R>& f, const PlanarQ80& w, int Kp, int r0, int last, int lane, int units)
 {
     const int nbp = Kp / PIX_QK8;
 #pragma unroll
-    for (int rr = 0; rr < kMvRows; rr++) {
+    for (int rr = 0; rr < R; rr++) {
         const int row = min(r0 + rr,last - 1);
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
@@ -341,12 +357,12 @@ __device__ __forceinline__ void q80_load(Q80Rows<UPL>& f, const PlanarQ80& w, in
     }
 }
 
-template <int UPL>
-__device__ __forceinline__ void q80_compute(const Q80Rows<UPL>& f, float part[kMvRows], const int8_t* sQ, const float* sD, int lane,
+template <int UPL, int R>
+__device__ __forceinline__ void q80_compute(const Q80Rows<UPL,R>& f, float part[R], const int8_t* sQ, const float* sD, int lane,
                                             int units)
 {
 #pragma unroll
-    for (int rr = 0; rr < kMvRows; rr++) part[rr] = 0.0f;
+    for (int rr = 0; rr < R; rr++) part[rr] = 0.0f;
 #pragma unroll
     for (int k = 0; k < UPL; k++) {
         const int u = lane + 64 * k;
@@ -357,7 +373,7 @@ __device__ __forceinline__ void q80_compute(const Q80Rows<UPL>& f, float part[kM
         const uint32_t xb[8] = {x2.x,x2.y,x2.z,x2.w,x3.x,x3.y,x3.z,x3.w};
         const float xd0 = sD[2 * u], xd1 = sD[2 * u + 1];
 #pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
+        for (int rr = 0; rr < R; rr++) {
             const uint32_t wa[8] = {f.q[rr][k][0].x,f.q[rr][k][0].y,f.q[rr][k][0].z,f.q[rr][k][0].w,
                                     f.q[rr][k][1].x,f.q[rr][k][1].y,f.q[rr][k][1].z,f.q[rr][k][1].w};
             const uint32_t wb[8] = {f.q[rr][k][2].x,f.q[rr][k][2].y,f.q[rr][k][2].z,f.q[rr][k][2].w,
@@ -384,40 +400,46 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w,
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + Kp);
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const int stride = (int)gridDim.x * kMvWaves * kMvRows;
-    const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
+    constexpr int R = q80_rows<UPL>();
+    const int stride = (int)gridDim.x * kMvWaves * R;
+    const int first = ((int)blockIdx.x * kMvWaves + wave) * R;
     const int last = N;
     const int units = Kp / 64;
     float4 xv[kXPasses * UPL];
     load_x_q8_0(x,K,xv);
     __builtin_amdgcn_sched_barrier(0);
-    Q80Rows<UPL> a, b;
-    q80_load(a,w,Kp,first,last,lane,units);
+    // Set a is requested before x is quantized unless the rows are long (see
+    // the Q5_K kernel); two sets up to 3 units per lane.
+    constexpr bool two_sets = UPL <= 3, rows_first = UPL <= 4;
+    Q80Rows<UPL,R> a, b;
+    if (rows_first) q80_load(a,w,Kp,first,last,lane,units);
     __builtin_amdgcn_sched_barrier(0);
     quantize_x_q8_0(xv,K,Kp,sQ,sD);
-    // x's loads precede the rows' 5 * kMvRows * UPL (see the Q5_K kernel).
-    __builtin_amdgcn_s_waitcnt(wait_vmcnt(5 * kMvRows * UPL));
+    // x's loads precede the rows' 5 * R * UPL (see the Q5_K kernel).
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(rows_first? 5 * R * UPL : 0));
+    if (!rows_first) q80_load(a,w,Kp,first,last,lane,units);
     __syncthreads();
-    stream_rows<(UPL <= 3)>(a,b,first,stride,last,lane,out,
-                [&](Q80Rows<UPL>& f, int r0) { q80_load(f,w,Kp,r0,last,lane,units); },
-                [&](const Q80Rows<UPL>& f, float (&part)[kMvRows]) { q80_compute(f,part,sQ,sD,lane,units); });
+    stream_rows<two_sets>(a,b,first,stride,last,lane,out,
+                [&](Q80Rows<UPL,R>& f, int r0) { q80_load(f,w,Kp,r0,last,lane,units); },
+                [&](const Q80Rows<UPL,R>& f, float (&part)[R]) { q80_compute(f,part,sQ,sD,lane,units); });
 }
 
 // ---------------------------------------------------------------- Q6_K (planar)
 // Unit u of a row: super-block b = u/4, half h = (u/2)%2, position half ih = u%2;
 // it covers elements 128h + 32g + 16ih + i for g = 0..3, i = 0..15.
-template <int UPL> struct Q6Rows {
-    uint4 la[kMvRows][UPL], lb[kMvRows][UPL], hh[kMvRows][UPL];
-    uint2 scw[kMvRows][UPL];
-    uint16_t dh[kMvRows][UPL];
+template <int UPL, int ROWS> struct Q6Rows {
+    static constexpr int R = ROWS;
+    uint4 la[R][UPL], lb[R][UPL], hh[R][UPL];
+    uint2 scw[R][UPL];
+    uint16_t dh[R][UPL];
 };
 
-template <int UPL>
-__device__ __forceinline__ void q6_load(Q6Rows<UPL>& f, const PlanarQ6K& w, int K, int r0, int last, int lane, int units)
+template <int UPL, int R>
+__device__ __forceinline__ void q6_load(Q6Rows<UPL,R>& f, const PlanarQ6K& w, int K, int r0, int last, int lane, int units)
 {
     const int nb = K / PIX_QK;
 #pragma unroll
-    for (int rr = 0; rr < kMvRows; rr++) {
+    for (int rr = 0; rr < R; rr++) {
         const int row = min(r0 + rr,last - 1);
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
@@ -433,12 +455,12 @@ __device__ __forceinline__ void q6_load(Q6Rows<UPL>& f, const PlanarQ6K& w, int 
     }
 }
 
-template <int UPL>
-__device__ __forceinline__ void q6_compute(const Q6Rows<UPL>& f, float part[kMvRows], const int8_t* sQ, const float* sD,
+template <int UPL, int R>
+__device__ __forceinline__ void q6_compute(const Q6Rows<UPL,R>& f, float part[R], const int8_t* sQ, const float* sD,
                                            const int* sB, int lane, int units)
 {
 #pragma unroll
-    for (int rr = 0; rr < kMvRows; rr++) part[rr] = 0.0f;
+    for (int rr = 0; rr < R; rr++) part[rr] = 0.0f;
 #pragma unroll
     for (int k = 0; k < UPL; k++) {
         const int u = lane + 64 * k;
@@ -454,7 +476,7 @@ __device__ __forceinline__ void q6_compute(const Q6Rows<UPL>& f, float part[kMvR
         }
         const float yd = sD[b];
 #pragma unroll
-        for (int rr = 0; rr < kMvRows; rr++) {
+        for (int rr = 0; rr < R; rr++) {
             const uint32_t lw[8] = {f.la[rr][k].x,f.la[rr][k].y,f.la[rr][k].z,f.la[rr][k].w,
                                     f.lb[rr][k].x,f.lb[rr][k].y,f.lb[rr][k].z,f.lb[rr][k].w};
             const uint32_t hw[4] = {f.hh[rr][k].x,f.hh[rr][k].y,f.hh[rr][k].z,f.hh[rr][k].w};
@@ -492,34 +514,35 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const int stride = (int)gridDim.x * kMvWaves * kMvRows;
-    const int first = ((int)blockIdx.x * kMvWaves + wave) * kMvRows;
+    constexpr int R = q6_rows<UPL>();
+    const int stride = (int)gridDim.x * kMvWaves * R;
+    const int first = ((int)blockIdx.x * kMvWaves + wave) * R;
     const int last = N;
     const int units = nb * 4;
     float4 xv[kXPasses * UPL];
     load_x_q8_K(x,K,xv);
     constexpr bool two_sets = UPL <= 2;
-    Q6Rows<UPL> a, b;
+    Q6Rows<UPL,R> a, b;
     // Long rows: x is quantized before the first rows are requested, so that
     // its staging registers are free again.
     __builtin_amdgcn_sched_barrier(0);
     if (two_sets) q6_load(a,w,K,first,last,lane,units);
     __builtin_amdgcn_sched_barrier(0);
     quantize_x_q8_K(xv,K,sQ,sD,sB);
-    // x's loads precede the rows' 5 * kMvRows * UPL (see the Q5_K kernel).
-    __builtin_amdgcn_s_waitcnt(wait_vmcnt(two_sets? 5 * kMvRows * UPL : 0));
+    // x's loads precede the rows' 5 * R * UPL (see the Q5_K kernel).
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(two_sets? 5 * R * UPL : 0));
     if (!two_sets) q6_load(a,w,K,first,last,lane,units);
     __syncthreads();
     stream_rows<two_sets>(a,b,first,stride,last,lane,out,
-                [&](Q6Rows<UPL>& f, int r0) { q6_load(f,w,K,r0,last,lane,units); },
-                [&](const Q6Rows<UPL>& f, float (&part)[kMvRows]) { q6_compute(f,part,sQ,sD,sB,lane,units); });
+                [&](Q6Rows<UPL,R>& f, int r0) { q6_load(f,w,K,r0,last,lane,units); },
+                [&](const Q6Rows<UPL,R>& f, float (&part)[R]) { q6_compute(f,part,sQ,sD,sB,lane,units); });
 }
 
 // Launch shape: one round of workgroups, kMvMaxWgPerCu per CU (fewer when the
 // kernel's occupancy allows fewer, or when there are fewer row pairs than
 // waves); the kernels stride over the rest.
 template <typename Kernel>
-static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid)
+static void launch_shape(Kernel kernel, size_t lds, size_t N, int rows_per_set, unsigned& grid)
 {
     static int cus = 0;
     if (!cus) {
@@ -532,12 +555,13 @@ static void launch_shape(Kernel kernel, size_t lds, size_t N, unsigned& grid)
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu,kernel,64 * kMvWaves,lds) != hipSuccess || per_cu < 1) per_cu = 1;
     per_cu = std::min(per_cu,kMvMaxWgPerCu);
-    const size_t waves_needed = (N + kMvRows - 1) / kMvRows;
+    const size_t waves_needed = (N + rows_per_set - 1) / rows_per_set;
     const size_t slots = (size_t)cus * per_cu * kMvWaves;
     const size_t waves = std::min(waves_needed,slots);
     grid = (unsigned)((waves + kMvWaves - 1) / kMvWaves);
 }
 
+// Units of 64 values per lane: rows of up to 6 * 64 * 64 = 24576 values.
 template <typename F>
 static hipError_t dispatch_upl(int units, F&& f)
 {
@@ -545,6 +569,8 @@ static hipError_t dispatch_upl(int units, F&& f)
     if (units <= 128) return f(std::integral_constant<int,2>{});
     if (units <= 192) return f(std::integral_constant<int,3>{});
     if (units <= 256) return f(std::integral_constant<int,4>{});
+    if (units <= 320) return f(std::integral_constant<int,5>{});
+    if (units <= 384) return f(std::integral_constant<int,6>{});
     return hipErrorInvalidValue;
 }
 
@@ -555,7 +581,7 @@ hipError_t launch_matvec_q5_K(const PlanarQ5K& w, const float* x, size_t N, size
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
         auto kernel = matvec_q5_K_kernel<decltype(upl)::value>;
         unsigned grid;
-        launch_shape(kernel,lds,N,grid);
+        launch_shape(kernel,lds,N,q5_rows<decltype(upl)::value>(),grid);
         kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out);
         return hipGetLastError();
     });
@@ -568,7 +594,7 @@ hipError_t launch_matvec_q8_0(const PlanarQ80& w, const float* x, size_t N, size
     return dispatch_upl((int)(Kp / 64),[&](auto upl) {
         auto kernel = matvec_q8_0_kernel<decltype(upl)::value>;
         unsigned grid;
-        launch_shape(kernel,lds,N,grid);
+        launch_shape(kernel,lds,N,q80_rows<decltype(upl)::value>(),grid);
         kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,(int)Kp,out);
         return hipGetLastError();
     });
@@ -581,7 +607,7 @@ hipError_t launch_matvec_q6_K(const PlanarQ6K& w, const float* x, size_t N, size
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
         auto kernel = matvec_q6_K_kernel<decltype(upl)::value>;
         unsigned grid;
-        launch_shape(kernel,lds,N,grid);
+        launch_shape(kernel,lds,N,q6_rows<decltype(upl)::value>(),grid);
         kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out);
         return hipGetLastError();
     });

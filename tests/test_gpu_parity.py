@@ -155,11 +155,16 @@ def test_gemm_ragged_vs_oracle(sess, wtype, m, n, k):
 
 @pytest.mark.parametrize("wtype,n,k", [(Q5_K, 1000, 256), (Q5_K, 77, 12288), (Q8_0, 999, 32), (Q8_0, 300, 3616),
                                        (Q6_K, 513, 4096), (Q6_K, 64, 12288),
-                                       (Q5_K, 150001, 256), (Q8_0, 150001, 64), (Q6_K, 150001, 256)])
+                                       (Q5_K, 150001, 256), (Q8_0, 150001, 64), (Q6_K, 150001, 256),
+                                       (Q5_K, 513, 18944), (Q8_0, 700, 18944), (Q6_K, 300, 18944),
+                                       (Q5_K, 65, 24576), (Q8_0, 66, 24576), (Q6_K, 67, 24576), (Q5_K, 64, 24832)])
 def test_matvec_vs_oracle(sess, wtype, n, k):
     """Every output row against the oracle.  The 150001-row cases give each wave
     more than 32 row pairs on a 256-CU device, so a wave's parked row totals are
-    written out while its loop still runs (as well as at its end)."""
+    written out while its loop still runs (as well as at its end).  K = 18944
+    (a decode FFN down projection) and 24576 are the long rows (5 and 6 units of
+    64 values per lane); K = 24832 is past the matvec's limit and runs on the
+    GEMM path."""
     rng = np.random.default_rng(n + k)
     wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     wb = pack(wtype, wf)
