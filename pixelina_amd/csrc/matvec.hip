@@ -217,11 +217,12 @@ __device__ __forceinline__ void stream_rows(Rows& a, Rows& b, int first, int str
     results_flush<R>(res,lane,stride,last,out);
 }
 
-// Rows per register set: two, except where two rows of a long row would not
-// fit in the registers (Q8_0 at 6 units per lane, Q6_K from 5).
-template <int UPL> constexpr int q5_rows() { return kMvRows; }
-template <int UPL> constexpr int q80_rows() { return UPL <= 5? kMvRows : 1; }
-template <int UPL> constexpr int q6_rows() { return UPL <= 4? kMvRows : 1; }
+// Rows per register set: two up to 16384 values per row, one beyond.  Long
+// rows are few at decode shapes (an FFN down projection has K = 18944 and
+// N = 3584), and one row per set spreads them over twice as many waves:
+// measured 9% faster for Q5_K and 2% for Q8_0 than two rows per set, and
+// faster than two sets of one row.
+template <int UPL> constexpr int mv_rows() { return UPL <= 4? kMvRows : 1; }
 
 // ---------------------------------------------------------------- Q5_K (planar)
 // Weight registers of R rows: unit u = lane + 64k of a row covers two
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q5_K_kernel(PlanarQ5K w,
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
     const int lane = threadIdx.x & 63, wave = wave_id();
-    constexpr int R = q5_rows<UPL>();
+    constexpr int R = mv_rows<UPL>();
     const int stride = (int)gridDim.x * kMvWaves * R;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * R;
     const int last = N;
@@ -400,7 +401,7 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q8_0_kernel(PlanarQ80 w,
     int8_t* sQ = reinterpret_cast<int8_t*>(smem);
     float* sD = reinterpret_cast<float*>(smem + Kp);
     const int lane = threadIdx.x & 63, wave = wave_id();
-    constexpr int R = q80_rows<UPL>();
+    constexpr int R = mv_rows<UPL>();
     const int stride = (int)gridDim.x * kMvWaves * R;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * R;
     const int last = N;
@@ -514,7 +515,7 @@ __global__ __launch_bounds__(64 * kMvWaves) void matvec_q6_K_kernel(PlanarQ6K w,
     float* sD = reinterpret_cast<float*>(smem + K);
     int* sB = reinterpret_cast<int*>(smem + K + 4 * nb);
     const int lane = threadIdx.x & 63, wave = wave_id();
-    constexpr int R = q6_rows<UPL>();
+    constexpr int R = mv_rows<UPL>();
     const int stride = (int)gridDim.x * kMvWaves * R;
     const int first = ((int)blockIdx.x * kMvWaves + wave) * R;
     const int last = N;
@@ -581,7 +582,7 @@ hipError_t launch_matvec_q5_K(const PlanarQ5K& w, const float* x, size_t N, size
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
         auto kernel = matvec_q5_K_kernel<decltype(upl)::value>;
         unsigned grid;
-        launch_shape(kernel,lds,N,q5_rows<decltype(upl)::value>(),grid);
+        launch_shape(kernel,lds,N,mv_rows<decltype(upl)::value>(),grid);
         kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out);
         return hipGetLastError();
     });
@@ -594,7 +595,7 @@ hipError_t launch_matvec_q8_0(const PlanarQ80& w, const float* x, size_t N, size
     return dispatch_upl((int)(Kp / 64),[&](auto upl) {
         auto kernel = matvec_q8_0_kernel<decltype(upl)::value>;
         unsigned grid;
-        launch_shape(kernel,lds,N,q80_rows<decltype(upl)::value>(),grid);
+        launch_shape(kernel,lds,N,mv_rows<decltype(upl)::value>(),grid);
         kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,(int)Kp,out);
         return hipGetLastError();
     });
@@ -607,7 +608,7 @@ hipError_t launch_matvec_q6_K(const PlanarQ6K& w, const float* x, size_t N, size
     return dispatch_upl((int)(nb * 4),[&](auto upl) {
         auto kernel = matvec_q6_K_kernel<decltype(upl)::value>;
         unsigned grid;
-        launch_shape(kernel,lds,N,q6_rows<decltype(upl)::value>(),grid);
+        launch_shape(kernel,lds,N,mv_rows<decltype(upl)::value>(),grid);
         kernel<<<grid,64 * kMvWaves,lds,s>>>(w,x,(int)N,(int)K,out);
         return hipGetLastError();
     });
