@@ -13,7 +13,7 @@
 
 namespace pixhip {
 
-constexpr int kQuantWaves = 4;
+constexpr int kQuantWaves = 8;  // waves per workgroup: 8 measured ~12% faster than 4 or 16 (Q8_K, 4096x3840)
 
 __global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_K_kernel(const float* __restrict__ x, size_t rows, size_t inner,
                                                                          size_t mpad, int8_t* __restrict__ qs, float* __restrict__ dT,
