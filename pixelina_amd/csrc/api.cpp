@@ -98,6 +98,9 @@ struct pixhip_session {
     // quantized-activation scratch
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // split-K partial outputs of small GEMM grids
+    void* partial = nullptr;
+    size_t partial_bytes = 0;
     // staging for host or misaligned pointers
     void* stage = nullptr;
     size_t stage_bytes = 0;
@@ -343,10 +346,16 @@ int multiply_stage(pixhip_session* s, pixhip_weight* w, size_t columns, const pi
         return fail(PIXHIP_ERR_STATE,"no quantized activations of this shape: run the QUANTIZE stage first");
     int rc = ensure_gemm_form(s,w);
     if (rc) return rc;
+    const size_t part_bytes = pixhip::gemm_split_bytes(columns,w->rows,round_up(w->inner,64));
+    if (part_bytes) {
+        rc = grow(s,&s->partial,&s->partial_bytes,part_bytes);
+        if (rc) return rc;
+    }
+    float* part = part_bytes? static_cast<float*>(s->partial) : nullptr;
     hipError_t e;
-    if (w->type == PIX_Q5_K) e = pixhip::launch_gemm_q5_K(s->a8k,w->q5,columns,w->rows,w->inner,out,s->stream);
-    else if (w->type == PIX_Q6_K) e = pixhip::launch_gemm_q6_K(s->a8k,w->q6,columns,w->rows,w->inner,out,s->stream);
-    else e = pixhip::launch_gemm_q8_0(s->a80,w->q80,columns,w->rows,w->inner,out,s->stream);
+    if (w->type == PIX_Q5_K) e = pixhip::launch_gemm_q5_K(s->a8k,w->q5,columns,w->rows,w->inner,out,part,s->stream);
+    else if (w->type == PIX_Q6_K) e = pixhip::launch_gemm_q6_K(s->a8k,w->q6,columns,w->rows,w->inner,out,part,s->stream);
+    else e = pixhip::launch_gemm_q8_0(s->a80,w->q80,columns,w->rows,w->inner,out,part,s->stream);
     PIX_HIP(e,"GEMM launch");
     return PIXHIP_OK;
 }
@@ -497,6 +506,7 @@ void pixhip_session_destroy(pixhip_session* s)
     trim_pool(s);
     for (auto& e : s->live) (void)hipFree(reinterpret_cast<void*>(e.first));
     if (s->scratch) (void)hipFree(s->scratch);
+    if (s->partial) (void)hipFree(s->partial);
     if (s->stage) (void)hipFree(s->stage);
     if (s->t0) (void)hipEventDestroy(s->t0);
     if (s->t1) (void)hipEventDestroy(s->t1);

@@ -42,6 +42,7 @@
 // the six-bit minima (inputs exact in fp16: min <= 63, |bsum16| <= 2032;
 // |Mn| < 2^24, so the fp32 result is exact), and the epilogue becomes
 // y += yd*(wd*S - wdmin*Mn).
+#include <algorithm>
 #include <type_traits>
 
 #include "pixhip_device.h"
@@ -102,10 +103,13 @@ struct GemmArgs {
     int M, N, K, Mpad, Npad;
     size_t ldy, yoff;
     int tiles_m, tiles_n;
+    int splits, split_chunks;  // split-K: K ranges of split_chunks stages each
+    float* part;               // split-K: fp32 partial outputs [splits][M][N]
 };
 
 struct Ctx {
-    int m0, n0, wave, wm, wn, K, nchunks;
+    int m0, n0, wave, wm, wn, K;
+    int c_begin, nchunks;  // this workgroup's stages: c_begin .. nchunks-1
     uint32_t oa, ow;  // per-lane LDS byte offsets of this wave's operand rows in a stage (k-step 0)
     uint32_t vo_rows; // per-lane DMA source offset of a 64-B row piece
     int ocol, oyd;    // this lane's feature column in the tile; first of its token rows in the wave
@@ -323,14 +327,15 @@ template <int KIND> constexpr int outstanding(int P)
 // still read in the first stage of the next one (their deferred epilogue)
 // before it is refilled in a later iteration.  In every call the buffers
 // written and the buffers read are distinct.
-template <int KIND, bool SUMS, int PHASE>
+template <int KIND, bool SUMS, int PHASE, bool DEFERRED = true>
 __device__ __forceinline__ void step(const GemmArgs& g, const Ctx& x, int c, bool h1, Acc& acc, uint8_t* __restrict__ dma_a,
                                      uint8_t* __restrict__ dma_w, uint8_t* __restrict__ other_sc, uint8_t* __restrict__ discard,
                                      const uint8_t* __restrict__ cur, const uint8_t* __restrict__ cur_scale)
 {
     constexpr int PLANES = KIND == KIND_Q80? 1 : 2;
     if constexpr (KIND != KIND_Q80 && PHASE == 0) {
-        if (h1 && c > 0) {
+        // (DEFERRED is false in a workgroup's first super-block: nothing before it.)
+        if (DEFERRED && h1) {
             sb_epilogue<KIND,SUMS,0>(g,x,c / kSBC - 1,acc,other_sc);
             sb_epilogue<KIND,SUMS,1>(g,x,c / kSBC - 1,acc,other_sc);
         }
@@ -418,8 +423,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
     uint8_t* const scale_base = lds + kStages * kStageBytes;  // after the A and W rings
     uint8_t* const discard = scale_base + 2 * kScaleBytes;
 
-    const int nblocks = g.tiles_m * g.tiles_n;
-    const int lid = xcd_remap((int)blockIdx.x,nblocks);
+    // Workgroups (tile, split): the same K range of neighbouring tiles runs
+    // together, so they share their operands in L2.
+    const int ntiles = g.tiles_m * g.tiles_n;
+    const int lid0 = xcd_remap((int)blockIdx.x,ntiles * g.splits);
+    const int split = lid0 / ntiles, lid = lid0 % ntiles;
     constexpr int GROUP = 8;  // token tiles sharing one feature tile, in launch order
     const int group = lid / (GROUP * g.tiles_n);
     const int first_m = group * GROUP;
@@ -445,7 +453,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
         x.oyd = x.wm * 64 + 4 * lg;
     }
     x.K = g.K;
-    x.nchunks = g.K / kKC;
+    x.c_begin = split * g.split_chunks;
+    x.nchunks = min(x.c_begin + g.split_chunks,g.K / kKC);
     {
         const size_t mp = (size_t)g.Mpad, np = (size_t)g.Npad, K = (size_t)g.K;
         const size_t nblk = K / (KIND == KIND_Q80? PIX_QK8 : PIX_QK);
@@ -469,38 +478,44 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
         acc.y[i] = v16f{};
     }
 
-    const int C = x.nchunks;
+    const int C0 = x.c_begin, C = x.nchunks;  // C0 starts a super-block (a multiple of kSBC)
     const bool h1 = (x.wn & 1) != 0;
-    issue_stage<KIND>(g,x,0,lds,lds + kWRing,discard);
-    if constexpr (SCALES) issue_scales<KIND>(g,x,0,scale_base,discard);
-    for (int c = 1; c < kDist; c++)
-        if (c < C) issue_stage<KIND>(g,x,c,lds + c * kHalfBytes,lds + kWRing + c * kHalfBytes,discard);
+    issue_stage<KIND>(g,x,C0,lds + (C0 % kStages) * kHalfBytes,lds + kWRing + (C0 % kStages) * kHalfBytes,discard);
+    if constexpr (SCALES) issue_scales<KIND>(g,x,C0 / kSBC,scale_base + ((C0 / kSBC) & 1) * kScaleBytes,discard);
+    for (int c = C0 + 1; c < C0 + kDist; c++)
+        if (c < C) issue_stage<KIND>(g,x,c,lds + (c % kStages) * kHalfBytes,lds + kWRing + (c % kStages) * kHalfBytes,discard);
 
     // Stage c has landed once only the DMAs issued in the kDist-1 iterations
     // before c may still be in flight (the prologue counts as iterations
     // -kDist..-1).  The last kDist-1 iterations issue fewer, so they drain.
     // (The integer-sum debug variant also stores inside the loop; stores share
     // vmcnt and may retire early, so it drains everything.)
-    auto iter = [&](auto phase, int c) {
+    auto iter = [&](auto phase, int c, auto deferred) {
         constexpr int P = decltype(phase)::value;
+        constexpr bool DEFERRED = decltype(deferred)::value;
         if (c + kDist - 1 < C && !SUMS) wait_vmcnt<outstanding<KIND>(P)>();
         else wait_vmcnt<0>();
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
         const int b = c / kSBC;
         const int sd = (c + kDist) % kStages, sc = c % kStages;
-        step<KIND,SUMS,P>(g,x,c,h1,acc,lds + sd * kHalfBytes,lds + kWRing + sd * kHalfBytes,scale_base + ((b + 1) & 1) * kScaleBytes,
+        step<KIND,SUMS,P,DEFERRED>(g,x,c,h1,acc,lds + sd * kHalfBytes,lds + kWRing + sd * kHalfBytes,scale_base + ((b + 1) & 1) * kScaleBytes,
                           discard,lds + sc * kHalfBytes,scale_base + (b & 1) * kScaleBytes);
     };
     if constexpr (KIND == KIND_Q80) {
-        for (int c = 0; c < C; c++) iter(std::integral_constant<int,0>{},c);
+        for (int c = C0; c < C; c++) iter(std::integral_constant<int,0>{},c,std::true_type{});
     } else {
-        for (int c = 0; c < C; c += kSBC) {
-            iter(std::integral_constant<int,0>{},c);
-            iter(std::integral_constant<int,1>{},c + 1);
-            iter(std::integral_constant<int,2>{},c + 2);
-            iter(std::integral_constant<int,3>{},c + 3);
-        }
+        // The first super-block is peeled (no deferred epilogue before it); the
+        // rest are counted in super-blocks, so that c % kStages is known in
+        // every iteration.
+        auto super_block = [&](int c, auto deferred) {
+            iter(std::integral_constant<int,0>{},c,deferred);
+            iter(std::integral_constant<int,1>{},c + 1,deferred);
+            iter(std::integral_constant<int,2>{},c + 2,deferred);
+            iter(std::integral_constant<int,3>{},c + 3,deferred);
+        };
+        super_block(C0,std::false_type{});
+        for (int sb = C0 / kSBC + 1; sb < C / kSBC; sb++) super_block(sb * kSBC,std::true_type{});
         if (h1) {  // deferred epilogue of the last super-block
             const int b = C / kSBC - 1;
             sb_epilogue<KIND,SUMS,0>(g,x,b,acc,scale_base + (b & 1) * kScaleBytes);
@@ -508,7 +523,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
         }
     }
 
-    if constexpr (!SUMS) {
+    if (!SUMS && g.splits > 1) {
+        // Split-K: this K range's fp32 partial outputs; splitk_reduce_kernel
+        // adds the ranges in order and applies bias, ldy and offset.
+        const uint32_t ln = lane_now();
+        const int lr = (int)(ln & 31), lg = (int)(ln >> 5);
+        const int mrow0 = x.m0 + x.wm * 64, n = x.n0 + x.wn * kWN + lr;
+        float* col = g.part + (size_t)split * g.M * g.N + n;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = mrow0 + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+                if (m < g.M && n < g.N) col[(size_t)m * g.N] = acc.y[i][r];
+            }
+        }
+    } else if constexpr (!SUMS) {
         // Bias for this lane's column, loaded once (clamped index) and drained
         // before the stores: a load left pending here would make every store
         // below wait for all earlier stores.
@@ -533,6 +563,57 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
 
 static size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
+// y[yoff + m*ldy + n] = sum over the splits, in order, of part[s][m][n] + bias[n].
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
+                                                            float* __restrict__ y, size_t ldy, size_t yoff,
+                                                            const float* __restrict__ bias)
+{
+    const size_t total = (size_t)M * N;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        float v = part[i];
+        for (int s = 1; s < splits; s++) v += part[(size_t)s * total + i];
+        const size_t m = i / N, n = i % N;
+        y[yoff + m * ldy + n] = v + (bias? bias[n] : 0.0f);
+    }
+}
+
+static int device_cus()
+{
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v,hipDeviceAttributeMultiprocessorCount,dev) == hipSuccess && v > 0)
+            cus = v;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+// Split-K for grids that leave most of the device idle: while the tiles fill
+// less than half of the CUs, each tile's K range is cut (at super-block
+// boundaries) into up to CUs/tiles pieces run by separate workgroups.
+// Returns the number of pieces (1: no split) and their length in stages.
+static int split_plan(size_t M, size_t N, size_t K, int& split_chunks)
+{
+    const size_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    const int chunks = (int)(K / kKC), groups = chunks / kSBC;
+    split_chunks = chunks;
+    const int cus = device_cus();
+    if (!tiles || tiles * 2 > (size_t)cus || groups < 2) return 1;
+    const int want = std::min<int>((int)((size_t)cus / tiles),groups);
+    if (want < 2) return 1;
+    split_chunks = (groups + want - 1) / want * kSBC;
+    return (chunks + split_chunks - 1) / split_chunks;
+}
+
+size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages)
+{
+    int chunks;
+    const int splits = split_plan(M,N,K_stages,chunks);
+    return splits > 1? (size_t)splits * M * N * sizeof(float) : 0;
+}
+
 template <int KIND, bool SUMS>
 static hipError_t launch(GemmArgs g, size_t mpad, size_t npad, hipStream_t s)
 {
@@ -546,9 +627,17 @@ static hipError_t launch(GemmArgs g, size_t mpad, size_t npad, hipStream_t s)
     if (mpad * g.K >= lim || npad * g.K >= lim || scales >= lim || mpad * (g.K / 16) * 2 >= lim) return hipErrorInvalidValue;
     g.Mpad = (int)mpad;
     g.Npad = (int)npad;
-    const int nblocks = g.tiles_m * g.tiles_n;
-    if (!nblocks) return hipSuccess;
-    gemm_kernel<KIND,SUMS><<<dim3(nblocks),dim3(kThreads),0,s>>>(g);
+    const int ntiles = g.tiles_m * g.tiles_n;
+    if (!ntiles) return hipSuccess;
+    g.splits = SUMS? 1 : split_plan((size_t)g.M,(size_t)g.N,(size_t)g.K,g.split_chunks);
+    if (g.splits > 1 && !g.part) g.splits = 1;  // no workspace: run unsplit
+    if (g.splits == 1) g.split_chunks = g.K / kKC;
+    gemm_kernel<KIND,SUMS><<<dim3(ntiles * g.splits),dim3(kThreads),0,s>>>(g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || g.splits == 1) return e;
+    const size_t total = (size_t)g.M * g.N;
+    const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256,4096);
+    splitk_reduce_kernel<<<dim3(grid),dim3(256),0,s>>>(g.part,g.splits,g.M,g.N,g.y,g.ldy,g.yoff,g.bias);
     return hipGetLastError();
 }
 
@@ -561,27 +650,33 @@ static GemmArgs base_args(size_t M, size_t N, size_t K)
     return g;
 }
 
-hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s)
+hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
+                            hipStream_t s)
 {
     GemmArgs g = base_args(M,N,K);
+    g.part = part;
     g.xq = a.qs; g.xdT = a.d; g.xbs = a.bs;
     g.whi = w.hi; g.wlo = w.lo; g.wdT = w.d; g.wdm = w.dm; g.wmn = w.mn;
     g.y = out.y; g.bias = out.bias; g.ldy = out.ldy; g.yoff = out.offset;
     return launch<KIND_Q5K,false>(g,a.mpad,w.npad,s);
 }
 
-hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s)
+hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
+                            hipStream_t s)
 {
     GemmArgs g = base_args(M,N,K);
+    g.part = part;
     g.xq = a.qs; g.xdT = a.d;
     g.whi = w.hi; g.wlo = w.lo; g.wdT = w.d;
     g.y = out.y; g.bias = out.bias; g.ldy = out.ldy; g.yoff = out.offset;
     return launch<KIND_Q6K,false>(g,a.mpad,w.npad,s);
 }
 
-hipError_t launch_gemm_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s)
+hipError_t launch_gemm_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, const Output& out, float* part,
+                            hipStream_t s)
 {
     GemmArgs g = base_args(M,N,round_up(K,kKC));
+    g.part = part;
     g.xq = a.qs; g.xdT = a.d;
     g.whi = w.qs; g.wdT = w.dT;
     g.y = out.y; g.bias = out.bias; g.ldy = out.ldy; g.yoff = out.offset;

@@ -130,9 +130,16 @@ hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, siz
                               float* dT, hipStream_t s);
 
 // gemm.hip
-hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s);
-hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s);
-hipError_t launch_gemm_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, const Output& out, hipStream_t s);
+// Split-K workspace (fp32 partial outputs) a GEMM of M x N over K (rounded up
+// to 64: the stage length) uses; 0 when it runs unsplit.  The launchers take
+// a workspace of at least that size, or null to run unsplit.
+size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages);
+hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
+                            hipStream_t s);
+hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
+                            hipStream_t s);
+hipError_t launch_gemm_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, const Output& out, float* part,
+                            hipStream_t s);
 hipError_t launch_sums_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, int32_t* scaled, int32_t* mins,
                             hipStream_t s);
 hipError_t launch_sums_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s);
