@@ -103,9 +103,24 @@ struct GemmArgs {
     int M, N, K, Mpad, Npad;
     size_t ldy, yoff;
     int tiles_m, tiles_n;
-    int splits, split_chunks;  // split-K: K ranges of split_chunks stages each
-    float* part;               // split-K: fp32 partial outputs [splits][M][N]
+    // Split-K of the last tiles: tiles full_tiles.. (in tile order) run as
+    // `splits` K ranges of split_chunks stages each, writing fp32 partials
+    // part[split][tile - full_tiles][kBM][kBN] that splitk_reduce_kernel sums.
+    int full_tiles, splits, split_chunks;
+    float* part;
 };
+
+// Tile order: GROUP token tiles share one feature tile, in launch order.
+__device__ __forceinline__ void tile_of(int lid, int tiles_m, int tiles_n, int& tm, int& tn)
+{
+    constexpr int GROUP = 8;
+    const int group = lid / (GROUP * tiles_n);
+    const int first_m = group * GROUP;
+    const int gsize = min(tiles_m - first_m,GROUP);
+    const int within = lid % (GROUP * tiles_n);
+    tm = first_m + within % gsize;
+    tn = within / gsize;
+}
 
 struct Ctx {
     int m0, n0, wave, wm, wn, K;
@@ -423,17 +438,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
     uint8_t* const scale_base = lds + kStages * kStageBytes;  // after the A and W rings
     uint8_t* const discard = scale_base + 2 * kScaleBytes;
 
-    // Workgroups (tile, split): the same K range of neighbouring tiles runs
-    // together, so they share their operands in L2.
+    // Whole tiles first (XCD-remapped), then the split tiles' pieces in launch
+    // order (consecutive pieces land on different XCDs, so the last round
+    // spreads over the whole device).
     const int ntiles = g.tiles_m * g.tiles_n;
-    const int lid0 = xcd_remap((int)blockIdx.x,ntiles * g.splits);
-    const int split = lid0 / ntiles, lid = lid0 % ntiles;
-    constexpr int GROUP = 8;  // token tiles sharing one feature tile, in launch order
-    const int group = lid / (GROUP * g.tiles_n);
-    const int first_m = group * GROUP;
-    const int gsize = min(g.tiles_m - first_m,GROUP);
-    const int within = lid % (GROUP * g.tiles_n);
-    const int tm = first_m + within % gsize, tn = within / gsize;
+    const int bid = (int)blockIdx.x;
+    const bool piece = bid >= g.full_tiles;
+    const int split_tiles = ntiles - g.full_tiles;
+    const int pidx = bid - g.full_tiles;
+    const int split = piece? pidx / split_tiles : 0;
+    const int lid = piece? g.full_tiles + pidx % split_tiles : xcd_remap(bid,g.full_tiles);
+    int tm, tn;
+    tile_of(lid,g.tiles_m,g.tiles_n,tm,tn);
 
     Ctx x;
     x.m0 = tm * kBM;
@@ -453,8 +469,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
         x.oyd = x.wm * 64 + 4 * lg;
     }
     x.K = g.K;
-    x.c_begin = split * g.split_chunks;
-    x.nchunks = min(x.c_begin + g.split_chunks,g.K / kKC);
+    x.c_begin = piece? split * g.split_chunks : 0;
+    x.nchunks = piece? min(x.c_begin + g.split_chunks,g.K / kKC) : g.K / kKC;
     {
         const size_t mp = (size_t)g.Mpad, np = (size_t)g.Npad, K = (size_t)g.K;
         const size_t nblk = K / (KIND == KIND_Q80? PIX_QK8 : PIX_QK);
@@ -523,19 +539,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
         }
     }
 
-    if (!SUMS && g.splits > 1) {
-        // Split-K: this K range's fp32 partial outputs; splitk_reduce_kernel
-        // adds the ranges in order and applies bias, ldy and offset.
+    if (!SUMS && (int)blockIdx.x >= g.full_tiles) {
+        // Split-K: this K range's fp32 partial tile; splitk_reduce_kernel adds
+        // the ranges in order and applies bias, ldy and offset.  (The piece
+        // index is recomputed here rather than kept live through the loop.)
+        const int p = (int)blockIdx.x - g.full_tiles, nsplit = g.tiles_m * g.tiles_n - g.full_tiles;
         const uint32_t ln = lane_now();
         const int lr = (int)(ln & 31), lg = (int)(ln >> 5);
-        const int mrow0 = x.m0 + x.wm * 64, n = x.n0 + x.wn * kWN + lr;
-        float* col = g.part + (size_t)split * g.M * g.N + n;
+        float* col = g.part + ((size_t)(p / nsplit) * nsplit + p % nsplit) * (kBM * kBN) + x.wn * kWN + lr;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = mrow0 + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-                if (m < g.M && n < g.N) col[(size_t)m * g.N] = acc.y[i][r];
+                const int lm = x.wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+                col[(size_t)lm * kBN] = acc.y[i][r];
             }
         }
     } else if constexpr (!SUMS) {
@@ -563,17 +580,31 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
 
 static size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
-// y[yoff + m*ldy + n] = sum over the splits, in order, of part[s][m][n] + bias[n].
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
-                                                            float* __restrict__ y, size_t ldy, size_t yoff,
-                                                            const float* __restrict__ bias)
+// For the split tiles: y[yoff + m*ldy + n] = sum over the splits, in order, of
+// the partial tiles, + bias[n].  Workgroup (tile t, slice q) of 256 threads
+// covers kReduceSlice elements of the tile, 4 consecutive features per thread.
+constexpr int kReduceSlice = 1024, kReduceSlices = kBM * kBN / kReduceSlice;
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g)
 {
-    const size_t total = (size_t)M * N;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-        float v = part[i];
-        for (int s = 1; s < splits; s++) v += part[(size_t)s * total + i];
-        const size_t m = i / N, n = i % N;
-        y[yoff + m * ldy + n] = v + (bias? bias[n] : 0.0f);
+    const int split_tiles = g.tiles_m * g.tiles_n - g.full_tiles;
+    const int t = (int)blockIdx.x / kReduceSlices, q = (int)blockIdx.x % kReduceSlices;
+    int tm, tn;
+    tile_of(g.full_tiles + t,g.tiles_m,g.tiles_n,tm,tn);
+    const size_t stride = (size_t)split_tiles * (kBM * kBN);
+    const int e = q * kReduceSlice + 4 * (int)threadIdx.x;
+    const float4* src = reinterpret_cast<const float4*>(g.part + (size_t)t * (kBM * kBN) + e);
+    float4 v = src[0];
+    for (int s = 1; s < g.splits; s++) {
+        const float4 w = src[(size_t)s * stride / 4];
+        v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+    }
+    const int m = tm * kBM + e / kBN, n0 = tn * kBN + e % kBN;
+    if (m >= g.M) return;
+    const float vv[4] = {v.x,v.y,v.z,v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + j;
+        if (n < g.N) g.y[g.yoff + (size_t)m * g.ldy + n] = vv[j] + (g.bias? g.bias[n] : 0.0f);
     }
 }
 
@@ -590,28 +621,35 @@ static int device_cus()
     return cus;
 }
 
-// Split-K for grids that leave most of the device idle: while the tiles fill
-// less than half of the CUs, each tile's K range is cut (at super-block
-// boundaries) into up to CUs/tiles pieces run by separate workgroups.
-// Returns the number of pieces (1: no split) and their length in stages.
-static int split_plan(size_t M, size_t N, size_t K, int& split_chunks)
+// One workgroup fills a CU, so the tiles run in rounds of `CUs` workgroups.
+// When the last round would fill less than half of the device, its tiles are
+// split-K: each tile's K range is cut (at super-block boundaries) into up to
+// CUs/tiles-in-the-round pieces, run by separate workgroups.  Returns the
+// number of pieces (1: no split) and sets the whole tiles and the piece
+// length in stages.
+static int split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_chunks)
 {
     const size_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
     const int chunks = (int)(K / kKC), groups = chunks / kSBC;
+    const size_t cus = (size_t)device_cus();
+    full_tiles = (int)tiles;
     split_chunks = chunks;
-    const int cus = device_cus();
-    if (!tiles || tiles * 2 > (size_t)cus || groups < 2) return 1;
-    const int want = std::min<int>((int)((size_t)cus / tiles),groups);
+    if (!tiles || groups < 2) return 1;
+    const size_t tail = tiles - (tiles - 1) / cus * cus;  // tiles of the last round
+    if (tail * 2 > cus) return 1;
+    const int want = std::min<int>((int)(cus / tail),groups);
     if (want < 2) return 1;
+    full_tiles = (int)(tiles - tail);
     split_chunks = (groups + want - 1) / want * kSBC;
     return (chunks + split_chunks - 1) / split_chunks;
 }
 
 size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages)
 {
-    int chunks;
-    const int splits = split_plan(M,N,K_stages,chunks);
-    return splits > 1? (size_t)splits * M * N * sizeof(float) : 0;
+    int full, chunks;
+    const int splits = split_plan(M,N,K_stages,full,chunks);
+    const size_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    return splits > 1? (size_t)splits * (tiles - full) * (kBM * kBN) * sizeof(float) : 0;
 }
 
 template <int KIND, bool SUMS>
@@ -629,15 +667,18 @@ static hipError_t launch(GemmArgs g, size_t mpad, size_t npad, hipStream_t s)
     g.Npad = (int)npad;
     const int ntiles = g.tiles_m * g.tiles_n;
     if (!ntiles) return hipSuccess;
-    g.splits = SUMS? 1 : split_plan((size_t)g.M,(size_t)g.N,(size_t)g.K,g.split_chunks);
-    if (g.splits > 1 && !g.part) g.splits = 1;  // no workspace: run unsplit
-    if (g.splits == 1) g.split_chunks = g.K / kKC;
-    gemm_kernel<KIND,SUMS><<<dim3(ntiles * g.splits),dim3(kThreads),0,s>>>(g);
+    g.splits = SUMS? 1 : split_plan((size_t)g.M,(size_t)g.N,(size_t)g.K,g.full_tiles,g.split_chunks);
+    if (g.splits == 1 || !g.part) {  // unsplit (or no workspace)
+        g.splits = 1;
+        g.full_tiles = ntiles;
+        g.split_chunks = g.K / kKC;
+    }
+    const int split_tiles = ntiles - g.full_tiles;
+    gemm_kernel<KIND,SUMS><<<dim3(g.full_tiles + split_tiles * g.splits),dim3(kThreads),0,s>>>(g);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || g.splits == 1) return e;
-    const size_t total = (size_t)g.M * g.N;
-    const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256,4096);
-    splitk_reduce_kernel<<<dim3(grid),dim3(256),0,s>>>(g.part,g.splits,g.M,g.N,g.y,g.ldy,g.yoff,g.bias);
+    if (e != hipSuccess || !split_tiles) return e;
+    static_assert(kReduceSlice == 4 * 256, "reduce slice: 256 threads x 4 features");
+    splitk_reduce_kernel<<<dim3(split_tiles * kReduceSlices),dim3(256),0,s>>>(g);
     return hipGetLastError();
 }
 

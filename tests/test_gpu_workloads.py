@@ -13,7 +13,11 @@ The block linears are compared on sampled token rows: each token row of
 cpu_quant_matmul depends only on that row's activations (src/kernels_quant.cpp:
 383-405), so the oracle runs on the sampled rows alone.  Every row at full size
 is covered by a size-independent property instead: the GEMM of the rows rolled by
-an offset that is not a multiple of the tile gives the same bits per token row.
+an offset that is not a multiple of the tile gives the same outputs per token
+row.  Rows that fall in a tile of the last, split-K round in one placement and
+a whole tile in the other sum the same integer block results in another fp32
+order, so the roll property is checked to 1e-6 of each row's largest output
+(an indexing mistake shows as an O(1) error).
 Float gate: max|y - r| / max|r| <= 1e-4 per token row.
 """
 import numpy as np
@@ -73,11 +77,16 @@ def check_rows(name, y, x, rows_idx, wb, wtype, n):
     assert err.max() <= TOL, (name, int(rows_idx[int(err.argmax())]))
 
 
+ROLL_TOL = 1e-6
+
+
 def check_roll(sess, key, wb, wtype, x, n, y, shift=37):
     """Rolling the token rows by a non-multiple of the tile moves every row to
-    another tile position; each row's outputs must keep their bits."""
+    another tile position; each row's outputs must stay the same (to fp32
+    summation order, see the module docstring)."""
     y2 = run_gpu(sess, key, wb, wtype, np.roll(x, shift, axis=0), n)
-    assert np.array_equal(np.roll(y, shift, axis=0).view(np.uint32), y2.view(np.uint32))
+    err = row_rel_error(y2, np.roll(y, shift, axis=0))
+    assert err.max() <= ROLL_TOL, (key, int(err.argmax()), float(err.max()))
 
 
 def test_single_q8_0_linear(sess):
