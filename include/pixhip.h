@@ -116,8 +116,9 @@ int pixhip_weight_cache_info(pixhip_session* session, uint64_t* entries, uint64_
  * output[c][r] = sum_k W[r][k] * input[c][k] for c < columns, r < rows, with
  * the numerics of cpu_quant_matmul (src/kernels_quant.cpp:369-412): the
  * activations are quantized (Q8_0 for Q8_0 weights, Q8_K for K-quants) and
- * every block dot is exact in integers.  columns == 1 runs the matvec,
- * columns > 1 the MFMA GEMM (src/backend_vulkan.cpp:963-981).  `input` and
+ * every block dot is exact in integers.  columns == 1 runs the matvec (rows
+ * of up to 24576 values; longer rows and columns > 1 run the MFMA GEMM,
+ * src/backend_vulkan.cpp:963-981).  `input` and
  * `output` may be device pointers (from pixhip_allocate or any HIP
  * allocation) or host pointers; host buffers are staged through the device
  * and the call then completes before returning.  Every output element is
