@@ -111,6 +111,62 @@ def gemm_workload(synth):
     return x, wb, ch
 
 
+def bench_fused(sess, synth, _lib, Q5_K, Q8_0, reps):
+    """The producers of a linear layer's input fused with its quantizer, at the
+    DiT block's shapes, each against the same work done unfused (the producer
+    writing fp32, then the quantize pass reading it back):
+      norm    RMS norm + weight + modulation of X[4608, 3840] -> Q8_K (QKV / FFN-in)
+      gate    SiLU(G) * U of [4608, 10240] -> Q8_0 (FFN-down input)
+    Algorithmic bytes: fp32 inputs read once, planar activations written once
+    (Q8_K 1 + 1/64 + 1/8 B per value, Q8_0 1 + 1/8)."""
+    m = 4608
+    out = {}
+
+    def timed(fn):
+        fn()
+        sess.synchronize()
+        sess.timer_start()
+        for _ in range(reps):
+            fn()
+        return sess.timer_stop() / reps
+
+    k = 3840
+    x = synth.normal(synth.SEED_ACTIVATIONS, (m, k))
+    nw = (1.0 + 0.1 * synth.normal(synth.SEED_WEIGHTS, (1, k))[0]).astype(np.float32)
+    mod = (0.1 * synth.normal(synth.SEED_OUTLIERS, (1, k))[0]).astype(np.float32)
+    xb, wb, mb, yb = sess.to_device(x), sess.to_device(nw), sess.to_device(mod), sess.alloc(m * k * 4)
+    wq = sess.weight("bench:fused:q5k", synth.pack_q5_K(synth.normal(synth.SEED_WEIGHTS, (256, k), std=0.02)), Q5_K, k, 256)
+    fused_ms = timed(lambda: _lib.check(sess.norm_quantize(Q5_K, xb.ptr, m, k, wb.ptr, 1e-5, 0, mb.ptr), "norm_quantize"))
+    sep_ms = timed(lambda: (_lib.check(sess.norm_quantize(0, xb.ptr, m, k, wb.ptr, 1e-5, 0, mb.ptr, yb.ptr), "norm"),
+                            _lib.check(sess.matmul_stage(wq, yb.ptr, m, None, _lib.STAGE_QUANTIZE), "quantize")))
+    alg = m * k * 4 + m * k * (1 + 1 / 64 + 1 / 8) + 2 * k * 4
+    out["norm_q8_K"] = {"workload": f"RMS norm + weight + modulation, X[{m},{k}] -> Q8_K", "us": round(fused_ms * 1e3, 2),
+                        "gbs": round(alg / (fused_ms * 1e-3) / 1e9, 1), "frac": round(alg / (fused_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                        "unfused_us": round(sep_ms * 1e3, 2), "bytes": int(alg)}
+    for b in (xb, wb, mb, yb):
+        b.free()
+
+    k = 10240
+    g = synth.normal(synth.SEED_ACTIVATIONS, (m, k), std=3.0)
+    u = synth.normal(synth.SEED_WEIGHTS, (m, k))
+    gb, ub, yb = sess.to_device(g), sess.to_device(u), sess.alloc(m * k * 4)
+    del g, u
+    wq = sess.weight("bench:fused:q80", np.zeros((256, k // 32 * 34), np.uint8), Q8_0, k, 256)
+    fused_ms = timed(lambda: _lib.check(sess.silu_gate_quantize(Q8_0, gb.ptr, ub.ptr, m, k), "silu_gate_quantize"))
+    sep_ms = timed(lambda: (_lib.check(sess.silu_gate_quantize(0, gb.ptr, ub.ptr, m, k, yb.ptr), "silu_gate"),
+                            _lib.check(sess.matmul_stage(wq, yb.ptr, m, None, _lib.STAGE_QUANTIZE), "quantize")))
+    alg = m * k * 8 + m * k * (1 + 1 / 8)
+    out["silu_gate_q8_0"] = {"workload": f"SiLU(G) * U, [{m},{k}] -> Q8_0", "us": round(fused_ms * 1e3, 2),
+                             "gbs": round(alg / (fused_ms * 1e-3) / 1e9, 1),
+                             "frac": round(alg / (fused_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                             "unfused_us": round(sep_ms * 1e3, 2), "bytes": int(alg)}
+    for b in (gb, ub, yb):
+        b.free()
+    for name, v in out.items():
+        log(f"fused {name}: {v['us']} us ({v['gbs']} GB/s); unfused {v['unfused_us']} us")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -119,6 +175,7 @@ def main():
     ap.add_argument("--matvec-reps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--no-fused", action="store_true", help="skip the fused norm / SiLU-gate producers")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one plain 512 MiB device copy (the calibration kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -179,6 +236,7 @@ def main():
                                 "y": yv, "w": wbytes, "type": wtype}
             xvb.free()
             yvb.free()
+        fused = {} if args.no_fused else bench_fused(sess, synth, _lib, Q5_K, Q8_0, args.steps)
         if args.calibrate_copy:
             src, dst = sess.alloc(COPY_BYTES), sess.alloc(COPY_BYTES)
             sess.copy_device(dst.ptr, src.ptr, COPY_BYTES)
@@ -222,6 +280,9 @@ def main():
                              "frac": round(v["gbs"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(f"matvec_{k}"),
                              "work_per_launch": f"W + 4K + 4N = {v['bytes']} bytes"}}
             for k, v in matvec.items()}
+
+    if fused:
+        line["fused"] = fused
 
     if not args.no_cpu:
         threads = cpu_threads()

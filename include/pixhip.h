@@ -158,6 +158,36 @@ int pixhip_quantize_q8_0(pixhip_session* session, const float* input, void* bloc
  * block_q8_K (292 B: fp32 d, int8 qs[256], int16 bsums[16]).  Device pointers. */
 int pixhip_quantize_q8_K(pixhip_session* session, const float* input, void* blocks, size_t rows, size_t inner);
 
+/* ---- producers of a linear layer's input, fused with its quantizer ---- */
+
+/* tensor_norm (src/tensor.cpp:174-197; vulkan_norm, src/backend_vulkan.cpp:1096-1110)
+ * over `rows` rows of `inner` values: y = (float)(x - mean) * inverse * weight[c]
+ * with the mean (centered != 0 only) and the mean square taken in double and
+ * inverse = (float)(1 / sqrt(mean square + epsilon)); norm_weight NULL is the
+ * reference's empty weight.  When `modulation` is not NULL, y is then scaled as
+ * z_modulate does (src/inference.cpp:263-277): y * (1.0f + modulation[c]).
+ * `type` names the weight type of the linear layers that consume y (8, 13, 14)
+ * and quantizes y for them as pixhip_matmul would (Q8_0 for 8, Q8_K else) into
+ * the session's activations: follow with pixhip_matmul_stage(...,
+ * PIXHIP_STAGE_MULTIPLY) for each consumer of that type and inner size.
+ * type 0 only normalizes.  Optional outputs (NULL to skip): `normalized` fp32
+ * [rows][inner] (the tensor the reference returns), `blocks` the reference's
+ * block layout (block_q8_0 / block_q8_K, as pixhip_quantize_q8_0 / _q8_K).
+ * Device pointers; input, norm_weight, modulation and normalized 16-byte
+ * aligned. */
+int pixhip_norm_quantize(pixhip_session* session, uint32_t type, const float* input, size_t rows, size_t inner,
+                         const float* norm_weight, float epsilon, int centered, const float* modulation, float* normalized,
+                         void* blocks);
+
+/* tensor_silu (src/tensor.cpp:199-209) then tensor_gate (:334-345), i.e. the
+ * SwiGLU product gate = gate / (1.0f + expf(-gate)) * up in fp32 (src/
+ * inference.cpp:331-335), quantized for the consumers of weight type `type`
+ * as pixhip_norm_quantize does.  `gated` (NULL to skip; may equal `gate`)
+ * receives the fp32 product, `blocks` the reference's block layout.  Device
+ * pointers; gate, up and gated 16-byte aligned. */
+int pixhip_silu_gate_quantize(pixhip_session* session, uint32_t type, const float* gate, const float* up, size_t rows,
+                              size_t inner, float* gated, void* blocks);
+
 /* ---- integer parity gate ---- */
 
 /* Runs the GEMM kernel's integer path and writes, for every (column c, row r,

@@ -28,6 +28,10 @@
  *   4 Q8_0 quantizer dividing by the fp16-rounded scale
  *   5 Q5_K six-bit unpack of sub-blocks 4..7 taking the wrong high bits
  *   6 Q8_K quantizer keeping the last (not the first) largest |x|
+ *   7 norm adding epsilon after the square root
+ *   8 norm multiplying by the weight before the inverse
+ *   9 centered norm subtracting the mean in fp32
+ *  10 SiLU as v * (1 / (1 + e)) instead of a division
  */
 #ifndef ORC_MUTANT
 #define ORC_MUTANT 0
@@ -468,5 +472,67 @@ void orc_decode(const void* data, uint32_t type, size_t count, double* out)
             for (int e = 0; e < QK_K; e++) o[e] = d * sc[e / 16] * (q6_value(p,e) - 32);
             p += Q6_K_BYTES;
         }
+    }
+}
+
+/* ---- neighbours of the linear layer (producers of its input) ---- */
+
+/* tensor_norm, src/tensor.cpp:174-197, one row at a time: the mean (centered
+ * only) and the sum of squared deviations are accumulated in double in index
+ * order; inverse = (float)(1/sqrt(square/channels + epsilon)) in double;
+ * out = (float)(x - mean) * inverse * weight[c] in fp32, left to right
+ * (weight NULL: the reference's empty weight multiplies by 1). */
+void orc_norm_rows(const float* x, size_t rows, size_t channels, const float* weight, float epsilon, int centered, float* out)
+{
+    for (size_t r = 0; r < rows; r++) {
+        const float* from = x + r * channels;
+        float* to = out + r * channels;
+        double mean = 0, square = 0;
+        if (centered) {
+            for (size_t c = 0; c < channels; c++) mean += from[c];
+            mean /= (double)channels;
+        }
+        for (size_t c = 0; c < channels; c++) {
+            double t = (double)from[c] - mean;
+            square += t * t;
+        }
+#if ORC_MUTANT == 7
+        float inverse = (float)(1.0 / (sqrt(square / (double)channels) + (double)epsilon));
+#else
+        float inverse = (float)(1.0 / sqrt(square / (double)channels + (double)epsilon));
+#endif
+        for (size_t c = 0; c < channels; c++) {
+#if ORC_MUTANT == 8
+            to[c] = (float)((double)from[c] - mean) * (weight? weight[c] : 1.0f) * inverse;
+#elif ORC_MUTANT == 9
+            float v = (from[c] - (float)mean) * inverse;
+            to[c] = v * (weight? weight[c] : 1.0f);
+#else
+            float v = (float)((double)from[c] - mean) * inverse;
+            to[c] = v * (weight? weight[c] : 1.0f);
+#endif
+        }
+    }
+}
+
+/* z_modulate, src/inference.cpp:263-277: x[r][c] *= (1.0f + scale[c]) in fp32. */
+void orc_modulate_rows(float* x, size_t rows, size_t channels, const float* scale)
+{
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < channels; c++) x[r * channels + c] = x[r * channels + c] * (1.0f + scale[c]);
+}
+
+/* tensor_silu, src/tensor.cpp:199-209 (value /= 1.0f + expf(-value)), then
+ * tensor_gate, :334-345 (value *= up), elementwise in fp32; `out` may be `gate`. */
+void orc_silu_gate(const float* gate, const float* up, size_t count, float* out)
+{
+    for (size_t i = 0; i < count; i++) {
+        float v = gate[i];
+#if ORC_MUTANT == 10
+        v = v * (1.0f / (1.0f + expf(-v)));
+#else
+        v = v / (1.0f + expf(-v));
+#endif
+        out[i] = v * up[i];
     }
 }

@@ -46,6 +46,9 @@ int orc_quant_matmul(const void* w, uint32_t type, const float* x, float* y,
                      size_t rows, size_t columns, size_t inner, int threads);
 void orc_decode(const void* data, uint32_t type, size_t count, double* out);
 uint64_t orc_row_bytes(uint64_t inner, uint32_t type);
+void orc_norm_rows(const float* x, size_t rows, size_t channels, const float* weight, float epsilon, int centered, float* out);
+void orc_modulate_rows(float* x, size_t rows, size_t channels, const float* scale);
+void orc_silu_gate(const float* gate, const float* up, size_t count, float* out);
 
 #ifdef __cplusplus
 }

@@ -86,4 +86,29 @@ uint64_t ref_row_bytes(uint64_t inner, uint32_t type)
     return weight_bytes({inner},type);
 }
 
+/* tensor_norm, src/tensor.cpp:174-197, on `rows` x `channels` (weight NULL:
+ * the empty weight vector).  Returns 1 when the reference produced output. */
+int ref_norm_rows(const float* x, size_t rows, size_t channels, const float* weight, float epsilon, int centered, float* out)
+{
+    PixTensor in(rows,channels);
+    std::copy(x,x + rows * channels,in.values.begin());
+    std::vector<float> w;
+    if (weight) w.assign(weight,weight + channels);
+    PixTensor o = tensor_norm(in,w,epsilon,centered != 0);
+    if (o.values.size() != rows * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
+/* tensor_silu, src/tensor.cpp:199-209, then tensor_gate, :334-345 */
+void ref_silu_gate(const float* gate, const float* up, size_t count, float* out)
+{
+    PixTensor g(1,count),u(1,count);
+    std::copy(gate,gate + count,g.values.begin());
+    std::copy(up,up + count,u.values.begin());
+    tensor_silu(g);
+    tensor_gate(g,u);
+    std::copy(g.values.begin(),g.values.end(),out);
+}
+
 }

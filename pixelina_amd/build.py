@@ -18,6 +18,7 @@ SOURCES = [
     "csrc/repack.hip",
     "csrc/gemm.hip",
     "csrc/matvec.hip",
+    "csrc/fuse.hip",
     "csrc/api.cpp",
     "host/backend_hip.cpp",
 ]

@@ -311,31 +311,50 @@ bool device_visible(pixhip_session* s, const void* p, const void** dev)
     return false;
 }
 
-int quantize_stage(pixhip_session* s, const pixhip_weight* w, const float* x, size_t columns)
+// Sizes the session's activation scratch for `columns` rows of K values of
+// activation kind 1 (Q8_K) or 2 (Q8_0) and points s->a8k / s->a80 into it.
+// The activations then belong to the next MULTIPLY stages (set_act_shape).
+int act_buffers(pixhip_session* s, int kind, size_t columns, size_t K, pixhip::ActOut* out)
 {
-    const size_t K = w->inner, mpad = round_up(columns,kTileM);
-    if (w->type == PIX_Q8_0) {
+    const size_t mpad = round_up(columns,kTileM);
+    Carver c;
+    uint8_t* base;
+    if (kind == 2) {
         const size_t kp = round_up(K,64);
-        Carver c;
         size_t qs = c.take(mpad * kp), d = c.take((kp / PIX_QK8) * mpad * 4);
         int rc = grow(s,&s->scratch,&s->scratch_bytes,c.offset);
         if (rc) return rc;
-        uint8_t* base = static_cast<uint8_t*>(s->scratch);
+        base = static_cast<uint8_t*>(s->scratch);
         s->a80 = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<float*>(base + d),mpad};
-        PIX_HIP(pixhip::launch_quantize_q8_0(x,columns,K,kp,s->a80,nullptr,s->stream),"quantize Q8_0");
-        s->act_kind = 2;
+        if (out) *out = {s->a80.qs,s->a80.d,nullptr,mpad,nullptr,nullptr};
     } else {
-        Carver c;
         size_t qs = c.take(mpad * K), d = c.take((K / PIX_QK) * mpad * 4), bs = c.take(mpad * (K / 16) * 2);
         int rc = grow(s,&s->scratch,&s->scratch_bytes,c.offset);
         if (rc) return rc;
-        uint8_t* base = static_cast<uint8_t*>(s->scratch);
+        base = static_cast<uint8_t*>(s->scratch);
         s->a8k = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<float*>(base + d),reinterpret_cast<_Float16*>(base + bs),mpad};
-        PIX_HIP(pixhip::launch_quantize_q8_K(x,columns,K,s->a8k,nullptr,s->stream),"quantize Q8_K");
-        s->act_kind = 1;
+        if (out) *out = {s->a8k.qs,s->a8k.d,s->a8k.bs,mpad,nullptr,nullptr};
     }
+    s->act_kind = 0;  // until the producer is enqueued
+    return PIXHIP_OK;
+}
+
+void set_act_shape(pixhip_session* s, int kind, size_t columns, size_t K)
+{
+    s->act_kind = kind;
     s->act_columns = columns;
     s->act_inner = K;
+}
+
+int quantize_stage(pixhip_session* s, const pixhip_weight* w, const float* x, size_t columns)
+{
+    const size_t K = w->inner;
+    const int kind = w->type == PIX_Q8_0? 2 : 1;
+    int rc = act_buffers(s,kind,columns,K,nullptr);
+    if (rc) return rc;
+    if (kind == 2) PIX_HIP(pixhip::launch_quantize_q8_0(x,columns,K,round_up(K,64),s->a80,nullptr,s->stream),"quantize Q8_0");
+    else PIX_HIP(pixhip::launch_quantize_q8_K(x,columns,K,s->a8k,nullptr,s->stream),"quantize Q8_K");
+    set_act_shape(s,kind,columns,K);
     return PIXHIP_OK;
 }
 
@@ -755,6 +774,73 @@ int pixhip_quantize_q8_K(pixhip_session* s, const float* input, void* blocks, si
         return fail(PIXHIP_ERR_ARGUMENT,"input must be 16-byte aligned, blocks 4-byte aligned");
     PIX_HIP(pixhip::launch_quantize_q8_K(input,rows,inner,pixhip::Act8K{nullptr,nullptr,nullptr,0},blocks,s->stream),
             "quantize Q8_K");
+    return PIXHIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Shared checks and set-up of the fused producers: the activation kind of
+// `type` (0: none), the scratch activations for the MULTIPLY stages, and the
+// optional outputs.
+int fused_setup(pixhip_session* s, uint32_t type, size_t rows, size_t inner, float* result, void* blocks, int* kind,
+                pixhip::ActOut* out)
+{
+    if (type && !supported_type(type)) return fail(PIXHIP_ERR_UNSUPPORTED,"unsupported weight type " + std::to_string(type));
+    *kind = !type? 0 : (type == PIX_Q8_0? 2 : 1);
+    const size_t block = *kind == 1? PIX_QK : PIX_QK8;
+    if (!rows || !inner || inner % block || inner > INT32_MAX || rows > INT32_MAX)
+        return fail(PIXHIP_ERR_ARGUMENT,"rows must be positive and inner a positive multiple of " + std::to_string(block));
+    if (!*kind && !result) return fail(PIXHIP_ERR_ARGUMENT,"nothing to write: no type and no fp32 output");
+    if (!*kind && blocks) return fail(PIXHIP_ERR_ARGUMENT,"blocks need a weight type");
+    if (reinterpret_cast<uintptr_t>(result) % 16 || reinterpret_cast<uintptr_t>(blocks) % (*kind == 1? 4 : 2))
+        return fail(PIXHIP_ERR_ARGUMENT,"fp32 output must be 16-byte aligned, blocks 4-byte (Q8_K) or 2-byte (Q8_0) aligned");
+    *out = {nullptr,nullptr,nullptr,0,nullptr,nullptr};
+    if (*kind) {
+        int rc = act_buffers(s,*kind,rows,inner,out);
+        if (rc) return rc;
+    }
+    out->blocks = blocks;
+    out->y = result;
+    return PIXHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pixhip_norm_quantize(pixhip_session* s, uint32_t type, const float* input, size_t rows, size_t inner, const float* norm_weight,
+                         float epsilon, int centered, const float* modulation, float* normalized, void* blocks)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!input || reinterpret_cast<uintptr_t>(input) % 16) return fail(PIXHIP_ERR_ARGUMENT,"input must be a 16-byte aligned device pointer");
+    if ((reinterpret_cast<uintptr_t>(norm_weight) | reinterpret_cast<uintptr_t>(modulation)) % 16)
+        return fail(PIXHIP_ERR_ARGUMENT,"norm weight and modulation must be 16-byte aligned");
+    int kind;
+    pixhip::ActOut out;
+    if ((rc = fused_setup(s,type,rows,inner,normalized,blocks,&kind,&out))) return rc;
+    const size_t kpad = kind == 2? round_up(inner,64) : inner;
+    PIX_HIP(pixhip::launch_norm_quantize(input,rows,inner,norm_weight,epsilon,centered != 0,modulation,kind,kpad,out,s->stream),
+            "norm + quantize");
+    if (kind) set_act_shape(s,kind,rows,inner);
+    return PIXHIP_OK;
+}
+
+int pixhip_silu_gate_quantize(pixhip_session* s, uint32_t type, const float* gate, const float* up, size_t rows, size_t inner,
+                              float* gated, void* blocks)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!gate || !up || (reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up)) % 16)
+        return fail(PIXHIP_ERR_ARGUMENT,"gate and up must be 16-byte aligned device pointers");
+    int kind;
+    pixhip::ActOut out;
+    if ((rc = fused_setup(s,type,rows,inner,gated,blocks,&kind,&out))) return rc;
+    const size_t kpad = kind == 2? round_up(inner,64) : inner;
+    PIX_HIP(pixhip::launch_silu_gate_quantize(gate,up,rows,inner,kind,kpad,out,s->stream),"silu * gate + quantize");
+    if (kind) set_act_shape(s,kind,rows,inner);
     return PIXHIP_OK;
 }
 

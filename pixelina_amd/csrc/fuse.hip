@@ -1,0 +1,392 @@
+// Producers of a linear layer's input fused with its activation quantizer, so
+// the fp32 tensor between them need not make a round trip through HBM:
+//   - tensor_norm (src/tensor.cpp:174-197), optionally followed by z_modulate
+//     (src/inference.cpp:263-277): the RMS / layer norm in front of the DiT
+//     block's QKV and FFN-in linears;
+//   - tensor_silu (src/tensor.cpp:199-209) then tensor_gate (:334-345): the
+//     SwiGLU product in front of the FFN-down linear.
+// Each writes the planar activations the GEMM reads (Q8_K for K-quant weights,
+// Q8_0 for Q8_0 weights), and when asked the fp32 result (what the reference's
+// op returns) and the reference's block layout.
+//
+// Byte work, bound by HBM and by the quantizer's vector-ALU work.  A norm reads
+// a row once: one to four waves per token row (two for rows of 2049-4096
+// values: measured 18% faster than one wave of 16 chunks at 3 waves per SIMD,
+// and as fast as four), holding the row in registers (a 256-value chunk per
+// float4 per lane) from the sum of squares to the quantizer.  The gate
+// product is one wave per 256-value chunk.
+#include <type_traits>
+
+#include "pixhip_device.h"
+#include "pixhip_internal.h"
+
+namespace pixhip {
+
+constexpr int kNormWaves = 4;
+constexpr size_t kStageMaxK = 4096;  // norm vectors staged in LDS up to this row length (32 KB)
+constexpr int kGateWaves = 8;
+
+struct FuseArgs {
+    const float* x;      // norm input [rows][K] or gate [rows][K]
+    const float* u;      // up [rows][K] (gate product)
+    const float* w;      // norm weight [K] or null
+    const float* mod;    // modulation scale [K] or null
+    size_t rows, K;
+    float eps;
+    int centered;
+    int kind;            // 0 none, 1 Q8_K, 2 Q8_0
+    int stage_vectors;   // norm: weight and modulation staged in dynamic LDS
+    size_t kpad, mpad;   // Q8_0 planar row stride; planar rows allocated
+    int8_t* qs;          // planar activations (null: none)
+    float* d;
+    _Float16* bs;
+    uint8_t* blocks;     // reference block layout (null: none)
+    float* y;            // fp32 result (null: none)
+};
+
+// Values k0..k0+3 of a row (k0 = 256c + 4*lane), zeros past the row's end.
+// The load itself is unconditional (clamped to the row's last four values) and
+// the zeros are selected afterwards: a load under a per-lane branch makes the
+// compiler wait for it at the branch's end, which would serialise the loads.
+__device__ __forceinline__ float4 load4(const float* row, size_t K, size_t k0)
+{
+    const float4 t = *reinterpret_cast<const float4*>(row + (k0 < K? k0 : K - 4));
+    const bool in = k0 < K;
+    return make_float4(in? t.x : 0.f,in? t.y : 0.f,in? t.z : 0.f,in? t.w : 0.f);
+}
+
+// Writes chunk c (values 256c..256c+255) of `row`: lane l holds values
+// 256c+4l..+3 in v (zeros past the end).  Every lane of the wave must call it.
+// Q8_K: the chunk is one block.  Q8_0: lanes 8g..8g+7 form block 8c+g; blocks
+// between K/32 and kpad/32 are the planar padding (zeros, zero scale).
+template <int KIND>
+__device__ __forceinline__ void store_chunk(const FuseArgs& a, size_t row, int c, int lane, float4 v)
+{
+    const size_t K = a.K, k0 = (size_t)c * 256 + 4 * lane;
+    if (a.y && k0 < K) *reinterpret_cast<float4*>(a.y + row * K + k0) = v;
+    if constexpr (KIND == 1) {
+        uint32_t packed;
+        float d;
+        int gsum;
+        quantize_q8_K_wave(v,lane,packed,d,gsum);
+        const size_t nb = K / PIX_QK;
+        if (a.qs) {
+            reinterpret_cast<uint32_t*>(a.qs + row * K + (size_t)c * PIX_QK)[lane] = packed;
+            if (lane == 0) a.d[(size_t)c * a.mpad + row] = d;
+            const int t = lane >> 2;  // 16-value group, stored even groups first
+            if ((lane & 3) == 0) a.bs[row * (K / 16) + (size_t)c * 16 + (t & 1) * 8 + (t >> 1)] = (_Float16)(float)gsum;
+        }
+        if (a.blocks) {
+            uint8_t* blk = a.blocks + (row * nb + c) * PIX_Q8_K_BYTES;
+            reinterpret_cast<uint32_t*>(blk + 4)[lane] = packed;
+            if (lane == 0) *reinterpret_cast<float*>(blk) = d;
+            if ((lane & 3) == 0) reinterpret_cast<int16_t*>(blk + 4 + PIX_QK)[lane >> 2] = (int16_t)gsum;
+        }
+    } else if constexpr (KIND == 2) {
+        uint32_t packed;
+        float d32;
+        uint16_t dh;
+        quantize_q8_0_group(v,packed,d32,dh);
+        const size_t b = (size_t)c * 8 + (lane >> 3), nb = K / PIX_QK8, nbp = a.kpad / PIX_QK8;
+        if (a.qs && b < nbp) {
+            reinterpret_cast<uint32_t*>(a.qs + row * a.kpad + b * PIX_QK8)[lane & 7] = packed;
+            if ((lane & 7) == 0) a.d[b * a.mpad + row] = half_bits_to_float(dh);
+        }
+        if (a.blocks && b < nb) {
+            uint8_t* out = a.blocks + (row * nb + b) * PIX_Q8_0_BYTES;
+            uint16_t* q16 = reinterpret_cast<uint16_t*>(out + 2 + 4 * (lane & 7));
+            q16[0] = (uint16_t)(packed & 0xffffu);
+            q16[1] = (uint16_t)(packed >> 16);
+            if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(out) = dh;
+        }
+    }
+}
+
+// Chunks a row is written in: K values, plus the Q8_0 padding block.
+__device__ __forceinline__ int row_chunks(const FuseArgs& a)
+{
+    return (int)(((a.kind == 2? a.kpad : a.K) + 255) / 256);
+}
+
+template <int CTRL> __device__ __forceinline__ double dpp_f64(double v)
+{
+    const int2 h = __builtin_bit_cast(int2,v);
+    return __builtin_bit_cast(double,make_int2(dpp_i32<CTRL>(h.x),dpp_i32<CTRL>(h.y)));
+}
+__device__ __forceinline__ double lane_f64(double v, int lane)
+{
+    const int2 h = __builtin_bit_cast(int2,v);
+    return __builtin_bit_cast(double,make_int2(__builtin_amdgcn_readlane(h.x,lane),__builtin_amdgcn_readlane(h.y,lane)));
+}
+
+// Sum over the 64 lanes in double (every lane active), the same value in every
+// lane: rows of 16 by DPP, then the four row sums in order.
+__device__ __forceinline__ double wave_sum_f64(double v)
+{
+    v += dpp_f64<kDppXor1>(v);
+    v += dpp_f64<kDppXor2>(v);
+    v += dpp_f64<kDppHalfMirror>(v);
+    v += dpp_f64<kDppMirror>(v);
+    return (lane_f64(v,0) + lane_f64(v,16)) + (lane_f64(v,32) + lane_f64(v,48));
+}
+
+// Sum over the WPR waves of one row (consecutive waves of the workgroup).
+// Every wave of the workgroup must call it when WPR > 1 (it synchronises).
+template <int WPR>
+__device__ __forceinline__ double row_sum(double v, double* red, int wave)
+{
+    v = wave_sum_f64(v);
+    if constexpr (WPR == 1) {
+        return v;
+    } else {
+        if ((threadIdx.x & 63) == 0) red[wave] = v;
+        __syncthreads();
+        const int first = wave / WPR * WPR;
+        double t = red[first];
+#pragma unroll
+        for (int i = 1; i < WPR; i++) t += red[first + i];
+        __syncthreads();  // red is reused by the next sum
+        return t;
+    }
+}
+
+// WPR waves (1, 2 or 4) per token row, four waves per workgroup.  Wave `part`
+// of a row owns chunks part, part + WPR, ...; with CACHE > 0 it keeps them (at
+// most CACHE) in registers from the sums to the quantizer, with CACHE == 0
+// (rows of more than 64 chunks) each pass re-reads the row.  CENTERED: layer
+// norm (subtract the mean) rather than RMS norm.
+//   mean   = (sum of x, in double) / K                      (centered only)
+//   square = sum of (x - mean)^2 in double
+//   inv    = (float)(1 / sqrt(square / K + eps))            (double)
+//   y      = (float)(x - mean) * inv * w[k]  [* (1 + mod[k])]  (fp32)
+// The double sums are formed in another order than the reference's running
+// sum; `inv` is the fp32 rounding of a double that differs from the
+// reference's in its last bits only.
+template <int KIND, int WPR, int CACHE, bool CENTERED>
+__global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs a)
+{
+    constexpr int kRows = kNormWaves / WPR;  // rows per workgroup
+    __shared__ double red[kNormWaves];
+    // The norm weight and 1 + modulation, staged once per workgroup when the
+    // launch gives dynamic LDS for them (2 * K floats), else read from memory.
+    extern __shared__ float4 vec_lds[];
+    const int lane = (int)(threadIdx.x & 63);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const size_t row = (size_t)blockIdx.x * kRows + wave / WPR;
+    const int part = wave % WPR;
+    const bool live = row < a.rows;  // wave-uniform
+    const size_t K = a.K;
+    const bool staged = a.stage_vectors != 0;
+    if (WPR == 1 && !staged && !live) return;  // no barrier to reach
+    const float* src = a.x + (live? row : 0) * K;
+    const int nch = row_chunks(a);
+    const int mine = live && nch > part? (nch - part + WPR - 1) / WPR : 0;  // chunks of this wave
+    constexpr int kSlots = CACHE > 0? CACHE : 1;
+    float4 v[kSlots];
+    if constexpr (CACHE > 0) {
+        // all of this wave's chunks at once (past `mine` they are zeros)
+#pragma unroll
+        for (int j = 0; j < CACHE; j++) v[j] = load4(src,K,j < mine? (size_t)(part + WPR * j) * 256 + 4 * lane : K);
+    }
+    if (staged) {
+        // The workgroup's copy of the vectors, every thread (also of a dead
+        // row: it reaches the barrier below).  Unconditional loads (clamped
+        // index; a missing vector reads the row instead and is replaced by
+        // its neutral value), issued behind the row loads.
+        constexpr int kIters = (int)(kStageMaxK / 4 / (64 * kNormWaves));
+        const float4* wsrc = reinterpret_cast<const float4*>(a.w? a.w : src);
+        const float4* msrc = reinterpret_cast<const float4*>(a.mod? a.mod : src);
+        float4 wv[kIters], mv[kIters];
+#pragma unroll
+        for (int it = 0; it < kIters; it++) {
+            const size_t i = threadIdx.x + (size_t)it * 64 * kNormWaves, ic = i < K / 4? i : K / 4 - 1;
+            wv[it] = wsrc[ic];
+            mv[it] = msrc[ic];
+        }
+#pragma unroll
+        for (int it = 0; it < kIters; it++) {
+            const size_t i = threadIdx.x + (size_t)it * 64 * kNormWaves;
+            if (i < K / 4) {
+                vec_lds[i] = a.w? wv[it] : make_float4(1.f,1.f,1.f,1.f);
+                const float4 m = a.mod? mv[it] : make_float4(0.f,0.f,0.f,0.f);
+                vec_lds[K / 4 + i] = make_float4(__fadd_rn(1.0f,m.x),__fadd_rn(1.0f,m.y),__fadd_rn(1.0f,m.z),__fadd_rn(1.0f,m.w));
+            }
+        }
+        __syncthreads();
+    }
+    if (WPR == 1 && !live) return;
+    auto chunk = [&](int j) -> float4 {
+        if constexpr (CACHE > 0) return v[j];
+        else return load4(src,K,(size_t)(part + WPR * j) * 256 + 4 * lane);
+    };
+    const int J = CACHE > 0? CACHE : mine;
+
+    double mean = 0.0;
+    if constexpr (CENTERED) {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            if (j < mine) {
+                const float4 t = chunk(j);
+                s += ((double)t.x + (double)t.y) + ((double)t.z + (double)t.w);
+            }
+        }
+        mean = row_sum<WPR>(s,red,wave) / (double)K;
+    }
+    double sq = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const size_t k0 = (size_t)(part + WPR * j) * 256 + 4 * lane;
+        if (j < mine && k0 < K) {
+            const float4 t = chunk(j);
+            const double e0 = (double)t.x - mean, e1 = (double)t.y - mean, e2 = (double)t.z - mean, e3 = (double)t.w - mean;
+            sq += (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+        }
+    }
+    sq = row_sum<WPR>(sq,red,wave);
+    if (!live) return;  // after the last barrier
+    const float inv = (float)(1.0 / sqrt(sq / (double)K + (double)a.eps));
+
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        if (j < mine) {  // wave-uniform
+            const int c = part + WPR * j;
+            const size_t k0 = (size_t)c * 256 + 4 * lane;
+            float4 y = make_float4(0.f,0.f,0.f,0.f);
+            if (k0 < K) {
+                const float4 t = chunk(j);
+                // weight and 1 + modulation: 1.0 where absent (multiplying by
+                // 1.0 is exact, as the reference's empty weight is)
+                float4 w4, m4;
+                if (staged) {
+                    w4 = vec_lds[k0 / 4];
+                    m4 = vec_lds[K / 4 + k0 / 4];
+                } else {
+                    w4 = a.w? *reinterpret_cast<const float4*>(a.w + k0) : make_float4(1.f,1.f,1.f,1.f);
+                    m4 = a.mod? *reinterpret_cast<const float4*>(a.mod + k0) : make_float4(0.f,0.f,0.f,0.f);
+                    m4 = make_float4(__fadd_rn(1.0f,m4.x),__fadd_rn(1.0f,m4.y),__fadd_rn(1.0f,m4.z),__fadd_rn(1.0f,m4.w));
+                }
+                const float xs[4] = {t.x,t.y,t.z,t.w}, ws[4] = {w4.x,w4.y,w4.z,w4.w}, ms[4] = {m4.x,m4.y,m4.z,m4.w};
+                float ys[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    // (float)(x - 0.0) is x: no double arithmetic without a mean
+                    const float c = CENTERED? (float)((double)xs[e] - mean) : xs[e];
+                    ys[e] = __fmul_rn(__fmul_rn(__fmul_rn(c,inv),ws[e]),ms[e]);
+                }
+                y = make_float4(ys[0],ys[1],ys[2],ys[3]);
+            }
+            store_chunk<KIND>(a,row,c,lane,y);
+        }
+    }
+}
+
+// SiLU of one value as the reference's tensor_silu computes it in fp32:
+// v / (1.0f + expf(-v)).  expf is taken as the fp32 rounding of a double
+// exponential (within 1e-16 relative of e^-v): the correctly rounded value.
+// The reference's glibc expf rounds the other way for ~0.07% of arguments
+// (those within ~0.0004 ulp of an fp32 midpoint).
+__device__ __forceinline__ float silu_ref(float v)
+{
+    const float e = (float)exp(-(double)v);
+    return __fdiv_rn(v,__fadd_rn(1.0f,e));
+}
+
+// One wave per 256-value chunk of one row: y = silu(gate) * up.
+template <int KIND>
+__global__ __launch_bounds__(64 * kGateWaves) void silu_gate_quantize_kernel(FuseArgs a)
+{
+    // 32-bit chunk indices (the host checks rows * chunks < 2^32)
+    const uint32_t nch = (uint32_t)row_chunks(a);
+    const uint32_t chunk = blockIdx.x * kGateWaves + (threadIdx.x >> 6);
+    if (chunk >= (uint32_t)a.rows * nch) return;  // whole wave exits together
+    const int lane = (int)(threadIdx.x & 63);
+    const size_t row = chunk / nch;
+    const int c = (int)(chunk % nch);
+    const size_t k0 = (size_t)c * 256 + 4 * lane;
+    float4 y = make_float4(0.f,0.f,0.f,0.f);
+    if (k0 < a.K) {
+        const float4 g = *reinterpret_cast<const float4*>(a.x + row * a.K + k0);
+        const float4 u = *reinterpret_cast<const float4*>(a.u + row * a.K + k0);
+        y = make_float4(__fmul_rn(silu_ref(g.x),u.x),__fmul_rn(silu_ref(g.y),u.y),__fmul_rn(silu_ref(g.z),u.z),
+                        __fmul_rn(silu_ref(g.w),u.w));
+    }
+    store_chunk<KIND>(a,row,c,lane,y);
+}
+
+template <int KIND>
+static hipError_t launch_norm_kind(const FuseArgs& a, hipStream_t s)
+{
+    const size_t nch = ((a.kind == 2? a.kpad : a.K) + 255) / 256;
+    const dim3 block(64 * kNormWaves);
+    auto grid = [&](int wpr) { return dim3((unsigned)((a.rows + kNormWaves / wpr - 1) / (kNormWaves / wpr))); };
+    // weight and 1 + modulation in LDS (2 * K floats) for rows of up to 4096 values
+    FuseArgs b = a;
+    b.stage_vectors = a.K <= kStageMaxK? 1 : 0;
+    const size_t lds = b.stage_vectors? 2 * a.K * sizeof(float) : 0;
+    auto go = [&](auto centered) {
+        constexpr bool C = decltype(centered)::value;
+        if (nch <= 1) norm_quantize_kernel<KIND,1,1,C><<<grid(1),block,lds,s>>>(b);
+        else if (nch <= 2) norm_quantize_kernel<KIND,1,2,C><<<grid(1),block,lds,s>>>(b);
+        else if (nch <= 4) norm_quantize_kernel<KIND,1,4,C><<<grid(1),block,lds,s>>>(b);
+        else if (nch <= 8) norm_quantize_kernel<KIND,1,8,C><<<grid(1),block,lds,s>>>(b);
+        else if (nch <= 16) norm_quantize_kernel<KIND,2,8,C><<<grid(2),block,lds,s>>>(b);
+        else if (nch <= 32) norm_quantize_kernel<KIND,4,8,C><<<grid(4),block,lds,s>>>(b);
+        else if (nch <= 64) norm_quantize_kernel<KIND,4,16,C><<<grid(4),block,lds,s>>>(b);
+        else norm_quantize_kernel<KIND,4,0,C><<<grid(4),block,lds,s>>>(b);
+    };
+    if (a.centered) go(std::true_type{});
+    else go(std::false_type{});
+    return hipGetLastError();
+}
+
+static FuseArgs fuse_args(size_t rows, size_t K, int kind, size_t kpad, const ActOut& out)
+{
+    FuseArgs a = {};
+    a.rows = rows;
+    a.K = K;
+    a.kind = kind;
+    a.kpad = kind == 2? kpad : K;
+    a.mpad = out.mpad;
+    a.qs = out.qs;
+    a.d = out.d;
+    a.bs = out.bs;
+    a.blocks = static_cast<uint8_t*>(out.blocks);
+    a.y = out.y;
+    return a;
+}
+
+hipError_t launch_norm_quantize(const float* x, size_t rows, size_t K, const float* weight, float eps, bool centered,
+                                const float* modulation, int kind, size_t kpad, const ActOut& out, hipStream_t s)
+{
+    if (!rows) return hipSuccess;
+    if (rows > 0x7fffffffu) return hipErrorInvalidValue;
+    FuseArgs a = fuse_args(rows,K,kind,kpad,out);
+    a.x = x;
+    a.w = weight;
+    a.mod = modulation;
+    a.eps = eps;
+    a.centered = centered? 1 : 0;
+    if (kind == 1) return launch_norm_kind<1>(a,s);
+    if (kind == 2) return launch_norm_kind<2>(a,s);
+    return launch_norm_kind<0>(a,s);
+}
+
+hipError_t launch_silu_gate_quantize(const float* gate, const float* up, size_t rows, size_t K, int kind, size_t kpad,
+                                     const ActOut& out, hipStream_t s)
+{
+    FuseArgs a = fuse_args(rows,K,kind,kpad,out);
+    a.x = gate;
+    a.u = up;
+    const size_t total = rows * (((kind == 2? a.kpad : K) + 255) / 256);
+    if (!total) return hipSuccess;
+    if (total >= ((size_t)1 << 32) - 64 * kGateWaves) return hipErrorInvalidValue;
+    const size_t grid = (total + kGateWaves - 1) / kGateWaves;
+    const dim3 g((unsigned)grid), b(64 * kGateWaves);
+    if (kind == 1) silu_gate_quantize_kernel<1><<<g,b,0,s>>>(a);
+    else if (kind == 2) silu_gate_quantize_kernel<2><<<g,b,0,s>>>(a);
+    else silu_gate_quantize_kernel<0><<<g,b,0,s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace pixhip

@@ -75,54 +75,60 @@ __device__ __forceinline__ float wave_sum(float v)
 // One Q8_K block (256 values) quantized by one full wave, 4 consecutive values
 // per lane (lane l holds x[4l..4l+3]).  Semantics of quantize_row_q8_K_ref
 // (src/kernels_quant.cpp:80-118):
-//   max = the first x with the largest |x| (strict '>' scan, :89-95), so the
-//   wave arg-max breaks ties toward the lowest index;  amax == 0 zeroes the
-//   block (:96-102);  iscale = -127/max;  q = min(127, nearest_int(iscale*x));
-//   bsums = sums of 16;  d = 1/iscale.
+//   max = the first x with the largest |x| (strict '>' scan, :89-95), so ties
+//   go to the lowest index;  amax == 0 zeroes the block (:96-102);
+//   iscale = -127/max;  q = min(127, nearest_int(iscale*x));  bsums = sums of
+//   16;  d = 1/iscale.
 // Outputs: packed 4 quantized bytes of this lane, the block scale d, and the
 // sum of the 16-value group this lane belongs to (group = lane/4).
+// The largest |x| is reduced over the wave; the sign of its first occurrence
+// comes from ballots of |x| == amax and x < 0 per element position (wave-
+// uniform bit work on the scalar unit).  The quantized values are the low
+// bytes of the fused multiply-add's bit patterns, packed by v_perm, and a
+// lane's 4-value sum is one signed dot product of its packed bytes with ones.
 __device__ __forceinline__ void quantize_q8_K_wave(float4 v, int lane, uint32_t& packed, float& d, int& group_sum)
 {
     (void)lane;
     float xs[4] = {v.x,v.y,v.z,v.w};
-    // largest |x| (NaN never compares greater, as in the reference's scan)
+    // largest |x| (NaN never compares greater, as in the reference's scan).
+    // The lane's maximum is a non-negative float, never NaN, so the wave
+    // maximum is the unsigned maximum of the bit patterns.
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) m = fabsf(xs[i]) > m? fabsf(xs[i]) : m;
-    m = fmaxf(m,dpp_f32<kDppXor1>(m));
-    m = fmaxf(m,dpp_f32<kDppXor2>(m));
-    m = fmaxf(m,dpp_f32<kDppHalfMirror>(m));
-    m = fmaxf(m,dpp_f32<kDppMirror>(m));
-    const float amax = fmaxf(fmaxf(lane_f32(m,0),lane_f32(m,16)),fmaxf(lane_f32(m,32),lane_f32(m,48)));
+    uint32_t mb = __float_as_uint(m);
+    mb = max(mb,(uint32_t)dpp_i32<kDppXor1>((int)mb));
+    mb = max(mb,(uint32_t)dpp_i32<kDppXor2>((int)mb));
+    mb = max(mb,(uint32_t)dpp_i32<kDppHalfMirror>((int)mb));
+    mb = max(mb,(uint32_t)dpp_i32<kDppMirror>((int)mb));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)mb,0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)mb,16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)mb,32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)mb,48);
+    const float amax = __uint_as_float(max(max(r0,r1),max(r2,r3)));
     if (amax == 0.0f) {
         packed = 0;
         d = 0.0f;
         group_sum = 0;
         return;
     }
-    // the first x (lowest index) whose |x| is that maximum: the lowest lane
-    // holding one, then its first such value
-    float mine = 0.0f;
-    bool has = false;
-#pragma unroll
-    for (int i = 3; i >= 0; i--)
-        if (fabsf(xs[i]) == amax) {
-            mine = xs[i];
-            has = true;
-        }
-    const int first = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(has));
-    const float mval = lane_f32(mine,first);
-    float iscale = __fdiv_rn(-127.0f,mval);
-    int q[4];
-    int s = 0;
+    // the first x (lowest index 4*lane + i) whose |x| is that maximum: the
+    // lowest lane holding one, then its lowest position; only its sign is
+    // needed (its magnitude is amax)
+    uint64_t eq[4], ng[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        int t = nearest_int_fused(iscale,xs[i]);
-        t = t < 127? t : 127;
-        q[i] = (int)(int8_t)(uint8_t)(t & 255);
-        s += q[i];
+        eq[i] = __builtin_amdgcn_ballot_w64(fabsf(xs[i]) == amax);
+        ng[i] = __builtin_amdgcn_ballot_w64(xs[i] < 0.0f);
     }
-    packed = pack_bytes(q[0],q[1],q[2],q[3]);
+    const uint64_t bit = 1ull << __builtin_ctzll(eq[0] | eq[1] | eq[2] | eq[3]);
+    const uint64_t neg = (eq[0] & bit)? ng[0] : (eq[1] & bit)? ng[1] : (eq[2] & bit)? ng[2] : ng[3];
+    const float mval = __builtin_bit_cast(float,__builtin_bit_cast(uint32_t,amax) | ((neg & bit)? 0x80000000u : 0u));
+    const float iscale = __fdiv_rn(-127.0f,mval);
+    uint32_t t[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) t[i] = (uint32_t)min(nearest_int_fused(iscale,xs[i]),127);
+    // low bytes of t[0..3] -> bytes 0..3 (0x0c selects a zero byte)
+    packed = __builtin_amdgcn_perm(t[1],t[0],0x0c0c0400u) | __builtin_amdgcn_perm(t[3],t[2],0x04000c0cu);
+    int s = __builtin_amdgcn_sdot4((int)packed,0x01010101,0,false);
     s += dpp_i32<kDppXor1>(s);
     s += dpp_i32<kDppXor2>(s);
     group_sum = s;

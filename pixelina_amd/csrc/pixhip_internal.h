@@ -118,6 +118,21 @@ hipError_t launch_quantize_q8_0(const float* x, size_t rows, size_t inner, size_
                                 hipStream_t s);
 hipError_t launch_copy_device(void* dst, const void* src, size_t bytes, hipStream_t s);
 
+// fuse.hip: producers of a linear layer's input with its quantizer.  kind 0
+// (fp32 result only), 1 (Q8_K planar), 2 (Q8_0 planar, row stride kpad).
+struct ActOut {
+    int8_t* qs;       // planar activations (null: none)
+    float* d;
+    _Float16* bs;     // Q8_K 16-value sums
+    size_t mpad;
+    void* blocks;     // reference block layout (null: none)
+    float* y;         // fp32 result (null: none)
+};
+hipError_t launch_norm_quantize(const float* x, size_t rows, size_t K, const float* weight, float eps, bool centered,
+                                const float* modulation, int kind, size_t kpad, const ActOut& out, hipStream_t s);
+hipError_t launch_silu_gate_quantize(const float* gate, const float* up, size_t rows, size_t K, int kind, size_t kpad,
+                                     const ActOut& out, hipStream_t s);
+
 // repack.hip
 hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
                               float* dm, _Float16* mn, hipStream_t s);

@@ -19,10 +19,11 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_K_kernel(const f
                                                                          size_t mpad, int8_t* __restrict__ qs, float* __restrict__ dT,
                                                                          _Float16* __restrict__ bs, uint8_t* __restrict__ blocks)
 {
-    const size_t nb = inner / PIX_QK;
-    const size_t total = rows * nb;
+    // 32-bit block indices (the host checks rows * blocks < 2^32)
+    const uint32_t nb = (uint32_t)(inner / PIX_QK);
+    const uint32_t total = (uint32_t)(rows * nb);
     const int lane = threadIdx.x & 63;
-    const size_t block = (size_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+    const uint32_t block = blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
     if (block >= total) return;  // whole wave exits together
     const size_t row = block / nb, b = block % nb;
     const float* src = x + row * inner + b * PIX_QK;
@@ -39,7 +40,7 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_K_kernel(const f
         if ((lane & 3) == 0) bs[row * (inner / 16) + b * 16 + (t & 1) * 8 + (t >> 1)] = (_Float16)(float)gsum;
     }
     if (blocks) {
-        uint8_t* blk = blocks + block * PIX_Q8_K_BYTES;
+        uint8_t* blk = blocks + (size_t)block * PIX_Q8_K_BYTES;
         reinterpret_cast<uint32_t*>(blk + 4)[lane] = packed;
         if (lane == 0) *reinterpret_cast<float*>(blk) = d;
         if ((lane & 3) == 0) reinterpret_cast<int16_t*>(blk + 4 + PIX_QK)[lane >> 2] = (int16_t)gsum;
@@ -53,16 +54,17 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_0_kernel(const f
                                                                          size_t kpad, size_t mpad, int8_t* __restrict__ qs,
                                                                          float* __restrict__ dT, uint8_t* __restrict__ blocks)
 {
-    const size_t nb = inner / PIX_QK8, nbp = kpad / PIX_QK8;
-    const size_t total = rows * nbp;
+    // 32-bit block indices (the host checks rows * blocks < 2^32)
+    const uint32_t nb = (uint32_t)(inner / PIX_QK8), nbp = (uint32_t)(kpad / PIX_QK8);
+    const uint32_t total = (uint32_t)(rows * nbp);
     const int lane = threadIdx.x & 63;
-    const size_t wave_block = ((size_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6)) * 8;
+    const uint32_t wave_block = (blockIdx.x * kQuantWaves + (threadIdx.x >> 6)) * 8;
     if (wave_block >= total) return;
-    const size_t block = wave_block + (lane >> 3);
+    const uint32_t block = wave_block + (lane >> 3);
     const bool valid = block < total;
     // Lanes past the end mirror the last block so every lane joins the 8-lane
     // shuffles; only valid lanes store.
-    const size_t blk = valid? block : total - 1;
+    const uint32_t blk = valid? block : total - 1;
     const size_t row = blk / nbp, b = blk % nbp;
     const bool real = b < nb;
     float4 v = real? reinterpret_cast<const float4*>(x + row * inner + b * PIX_QK8)[lane & 7] : make_float4(0.f,0.f,0.f,0.f);
@@ -88,6 +90,7 @@ hipError_t launch_quantize_q8_K(const float* x, size_t rows, size_t inner, Act8K
 {
     size_t total = rows * (inner / PIX_QK);
     if (!total) return hipSuccess;
+    if (total >= ((size_t)1 << 32) - 64 * kQuantWaves) return hipErrorInvalidValue;
     size_t grid = (total + kQuantWaves - 1) / kQuantWaves;
     quantize_q8_K_kernel<<<dim3((unsigned)grid),dim3(64 * kQuantWaves),0,s>>>(x,rows,inner,planar.mpad,planar.qs,planar.d,planar.bs,
                                                                                static_cast<uint8_t*>(blocks));
@@ -99,6 +102,7 @@ hipError_t launch_quantize_q8_0(const float* x, size_t rows, size_t inner, size_
 {
     size_t total = rows * (kpad / PIX_QK8);
     if (!total) return hipSuccess;
+    if (total >= ((size_t)1 << 32) - 64 * kQuantWaves) return hipErrorInvalidValue;
     size_t waves = (total + 7) / 8;
     size_t grid = (waves + kQuantWaves - 1) / kQuantWaves;
     quantize_q8_0_kernel<<<dim3((unsigned)grid),dim3(64 * kQuantWaves),0,s>>>(x,rows,inner,kpad,planar.mpad,planar.qs,planar.d,

@@ -109,6 +109,14 @@ class Session:
     def quantize_q8_K(self, x_ptr, blocks_ptr, rows, inner):
         return self.lib.pixhip_quantize_q8_K(self.handle, x_ptr, blocks_ptr, rows, inner)
 
+    def norm_quantize(self, wtype, x_ptr, rows, inner, norm_weight_ptr=None, eps=1e-5, centered=False,
+                      modulation_ptr=None, normalized_ptr=None, blocks_ptr=None):
+        return self.lib.pixhip_norm_quantize(self.handle, wtype, x_ptr, rows, inner, norm_weight_ptr, eps, int(centered),
+                                             modulation_ptr, normalized_ptr, blocks_ptr)
+
+    def silu_gate_quantize(self, wtype, gate_ptr, up_ptr, rows, inner, gated_ptr=None, blocks_ptr=None):
+        return self.lib.pixhip_silu_gate_quantize(self.handle, wtype, gate_ptr, up_ptr, rows, inner, gated_ptr, blocks_ptr)
+
     def block_sums(self, weight, x_ptr, columns, sums_ptr, mins_ptr=None):
         return self.lib.pixhip_block_sums(self.handle, weight, x_ptr, columns, sums_ptr, mins_ptr)
 

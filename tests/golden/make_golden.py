@@ -10,6 +10,13 @@ Fixtures (numpy .npz, data only):
                         depends on the fused multiply-add of nearest_int
   g3_dots.npz           pix_dot_q8_0 / q5_K / q6_K on random rows
   g4_matmul.npz         cpu_quant_matmul on small shapes and a decode slice
+  g5_norm.npz           tensor_norm (RMS and centered, with and without a
+                        weight) on crafted and random rows, and the Q8_K /
+                        Q8_0 blocks of its outputs
+  g6_silu_gate.npz      tensor_silu then tensor_gate on special and random
+                        values, and the Q8_K / Q8_0 blocks of the product
+
+    python tests/golden/make_golden.py g5 g6   # only the named fixtures
 """
 import os
 import sys
@@ -21,7 +28,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.dirname(HERE))
 
-from oracle_lib import Q5_K, Q6_K, Q8_0, dot, quant_matmul, quantize, reference  # noqa: E402
+from oracle_lib import Q5_K, Q6_K, Q8_0, dot, norm_rows, quant_matmul, quantize, reference, silu_gate  # noqa: E402
 from pixelina_amd import synth  # noqa: E402
 
 
@@ -74,10 +81,59 @@ def fused_tie_rows(count, seed=7):
     return np.stack(found)
 
 
+def norm_rows_crafted(k):
+    rng = np.random.default_rng(55)
+    rows = [np.zeros(k, np.float32),                                    # square 0: inverse = 1/sqrt(eps)
+            np.full(k, 3.75, np.float32),                               # constant: centered -> 0
+            np.linspace(-1e-20, 1e-20, k).astype(np.float32),           # eps dominates
+            (rng.standard_normal(k) * 1e18).astype(np.float32),         # squares past fp32 range
+            np.where(np.arange(k) == 17, 1000.0, 0.0).astype(np.float32),  # one spike
+            (rng.standard_normal(k) + 40.0).astype(np.float32)]         # large mean
+    return np.stack(rows)
+
+
+def write_g5(ref):
+    rng = np.random.default_rng(505)
+    k = 512
+    x = np.concatenate([norm_rows_crafted(k), (rng.standard_normal((10, k)) * rng.choice([1e-3, 1.0, 50.0], (10, 1))).astype(np.float32)])
+    w = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    g = {"x": x, "w": w, "eps": np.array([1e-5, 1e-6], np.float32)}
+    for centered in (0, 1):
+        for wi, wv in (("none", None), ("w", w)):
+            eps = float(g["eps"][centered])
+            y = norm_rows(ref, "ref", x, wv, eps, centered)
+            key = f"c{centered}_{wi}"
+            g[f"{key}_y"] = y
+            g[f"{key}_q8_K"] = quantize(ref, "ref", y, "q8_K")
+            g[f"{key}_q8_0"] = quantize(ref, "ref", y, "q8_0")
+    np.savez_compressed(os.path.join(HERE, "g5_norm.npz"), **g)
+
+
+def write_g6(ref):
+    rng = np.random.default_rng(606)
+    rows, k = 6, 512
+    gate = (rng.standard_normal((rows, k)) * 6.0).astype(np.float32)
+    up = rng.standard_normal((rows, k)).astype(np.float32)
+    special = np.array([0.0, -0.0, 1e-30, -1e-30, 88.0, -88.0, 89.0, -89.0, 104.0, -104.0, 200.0, -200.0,
+                        20.0, -20.0, 0.5, -0.5], np.float32)
+    gate[0, :special.size] = special
+    up[0, :special.size] = 1.0
+    y = silu_gate(ref, "ref", gate, up)
+    np.savez_compressed(os.path.join(HERE, "g6_silu_gate.npz"), gate=gate, up=up, y=y,
+                        q8_K=quantize(ref, "ref", y, "q8_K"), q8_0=quantize(ref, "ref", y, "q8_0"))
+
+
 def main():
     ref = reference()
     if ref is None:
         raise SystemExit("oracle/_ref/libpixref.so missing: run `make -C oracle ref` first")
+    only = set(sys.argv[1:])
+    if only:
+        if "g5" in only:
+            write_g5(ref)
+        if "g6" in only:
+            write_g6(ref)
+        return
     rng = np.random.default_rng(20260101)
 
     # G1
@@ -138,6 +194,8 @@ def main():
         g4[f"c{i}_shape"] = np.array([wtype, m, n, k], dtype=np.int64)
     g4["count"] = np.array(len(cases))
     np.savez_compressed(os.path.join(HERE, "g4_matmul.npz"), **g4)
+    write_g5(ref)
+    write_g6(ref)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -40,6 +40,9 @@ def load_oracle(path):
         "orc_quant_matmul": (_int, [_vp, _u32, _vp, _vp, _sz, _sz, _sz, _int]),
         "orc_decode": (None, [_vp, _u32, _sz, _vp]),
         "orc_row_bytes": (ctypes.c_uint64, [ctypes.c_uint64, _u32]),
+        "orc_norm_rows": (None, [_vp, _sz, _sz, _vp, ctypes.c_float, _int, _vp]),
+        "orc_modulate_rows": (None, [_vp, _sz, _sz, _vp]),
+        "orc_silu_gate": (None, [_vp, _vp, _sz, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -76,6 +79,8 @@ def reference():
             "ref_decode": (None, [_vp, _u32, _sz, _vp]),
             "ref_half_float": (ctypes.c_float, [ctypes.c_uint16]),
             "ref_row_bytes": (ctypes.c_uint64, [ctypes.c_uint64, _u32]),
+            "ref_norm_rows": (_int, [_vp, _sz, _sz, _vp, ctypes.c_float, _int, _vp]),
+            "ref_silu_gate": (None, [_vp, _vp, _sz, _vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -130,6 +135,33 @@ def quant_matmul(lib, prefix, w, wtype, x, rows, threads=None):
     if not ok:
         raise ValueError("quant_matmul rejected its arguments")
     return y
+
+
+def norm_rows(lib, prefix, x, weight, eps, centered):
+    """tensor_norm over the rows of x (float32 [R, C]); weight None = empty."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, ch = x.shape
+    out = np.full_like(x, np.nan)
+    wp = None if weight is None else ptr(np.ascontiguousarray(weight, dtype=np.float32))
+    r = getattr(lib, f"{prefix}_norm_rows")(ptr(x), rows, ch, wp, eps, int(centered), ptr(out))
+    if prefix == "ref" and not r:
+        raise ValueError("tensor_norm returned an empty tensor")
+    return out
+
+
+def modulate_rows(lib, x, scale):
+    """z_modulate: x * (1 + scale[c]), through the oracle."""
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    lib.orc_modulate_rows(ptr(x), x.shape[0], x.shape[1], ptr(np.ascontiguousarray(scale, dtype=np.float32)))
+    return x
+
+
+def silu_gate(lib, prefix, gate, up):
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.full_like(g, np.nan)
+    getattr(lib, f"{prefix}_silu_gate")(ptr(g), ptr(u), g.size, ptr(out))
+    return out
 
 
 def decode(lib, w, wtype, count):

@@ -8,7 +8,7 @@ import os
 import numpy as np
 import pytest
 
-from oracle_lib import (Q5_K, Q6_K, Q8_0, dot, oracle, quant_matmul, quantize, reference)
+from oracle_lib import (Q5_K, Q6_K, Q8_0, dot, norm_rows, oracle, quant_matmul, quantize, reference, silu_gate)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 WTYPES = {"q8_0": Q8_0, "q5_K": Q5_K, "q6_K": Q6_K}
@@ -100,3 +100,35 @@ def test_oracle_equals_compiled_reference_on_random_inputs(seed):
         yo = quant_matmul(lib, "orc", wb, wtype, x, 7, threads=2)
         yr = quant_matmul(REF, "ref", wb, wtype, x, 7)
         assert np.array_equal(bits(yo), bits(yr)), wtype
+
+
+@pytest.mark.parametrize("centered", [0, 1])
+@pytest.mark.parametrize("wi", ["none", "w"])
+def test_norm_matches_reference_vectors(centered, wi):
+    """tensor_norm (src/tensor.cpp:174-197) and the blocks its output quantizes to."""
+    g = golden("g5_norm")
+    y = norm_rows(oracle(), "orc", g["x"], None if wi == "none" else g["w"], float(g["eps"][centered]), centered)
+    key = f"c{centered}_{wi}"
+    assert np.array_equal(bits(y), bits(g[f"{key}_y"]))
+    assert np.array_equal(quantize(oracle(), "orc", y, "q8_K"), g[f"{key}_q8_K"])
+    assert np.array_equal(quantize(oracle(), "orc", y, "q8_0"), g[f"{key}_q8_0"])
+    ref = reference()
+    if ref is not None:
+        x = np.random.default_rng(centered).standard_normal((8, 3840)).astype(np.float32) * 3 + centered
+        w = None if wi == "none" else np.linspace(0.5, 1.5, 3840).astype(np.float32)
+        assert np.array_equal(bits(norm_rows(oracle(), "orc", x, w, 1e-5, centered)), bits(norm_rows(ref, "ref", x, w, 1e-5, centered)))
+
+
+def test_silu_gate_matches_reference_vectors():
+    """tensor_silu then tensor_gate (src/tensor.cpp:199-209, :334-345)."""
+    g = golden("g6_silu_gate")
+    y = silu_gate(oracle(), "orc", g["gate"], g["up"])
+    assert np.array_equal(bits(y), bits(g["y"]))
+    assert np.array_equal(quantize(oracle(), "orc", y, "q8_K"), g["q8_K"])
+    assert np.array_equal(quantize(oracle(), "orc", y, "q8_0"), g["q8_0"])
+    ref = reference()
+    if ref is not None:
+        rng = np.random.default_rng(9)
+        gate = (rng.standard_normal(1 << 18) * 10).astype(np.float32)
+        up = rng.standard_normal(gate.size).astype(np.float32)
+        assert np.array_equal(bits(silu_gate(oracle(), "orc", gate, up)), bits(silu_gate(ref, "ref", gate, up)))

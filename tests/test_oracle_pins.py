@@ -9,7 +9,8 @@ import subprocess
 import numpy as np
 import pytest
 
-from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, dot, load_oracle, oracle, ptr, quant_matmul, quantize)
+from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, dot, load_oracle, norm_rows, oracle, ptr, quant_matmul, quantize,
+                        silu_gate)
 from pixelina_amd import synth
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -239,6 +240,60 @@ def test_dot_equals_fp64_dequantized_sum(wtype):
         assert abs(got - terms.sum()) <= 2e-6 * np.abs(terms).sum() + 1e-30
 
 
+# ---- neighbours of the linear layer: norm and SiLU-gate ----
+
+def test_norm_properties():
+    """What the mathematics fixes about tensor_norm's output, independent of
+    the oracle's formula: unit mean square (up to epsilon), zero mean when
+    centered, exact scale invariance by powers of two at epsilon 0, the
+    weight applied last (y_w == fl(y * w)), and the degenerate rows."""
+    o = oracle()
+    rng = np.random.default_rng(41)
+    k = 768
+    x = (rng.standard_normal((16, k)) * rng.choice([1e-2, 1.0, 30.0], (16, 1)) + rng.choice([0.0, 5.0], (16, 1))).astype(np.float32)
+    w = (1.0 + 0.3 * rng.standard_normal(k)).astype(np.float32)
+    for centered in (0, 1):
+        y = norm_rows(o, "orc", x, None, 0.0, centered).astype(np.float64)
+        assert np.allclose((y * y).mean(axis=1), 1.0, rtol=0, atol=2e-6)
+        if centered:
+            assert np.abs(y.mean(axis=1)).max() < 1e-6
+        y1 = norm_rows(o, "orc", x, None, 0.0, centered)
+        y4 = norm_rows(o, "orc", x * np.float32(4.0), None, 0.0, centered)
+        assert np.array_equal(y1.view(np.uint32), y4.view(np.uint32))
+        yn = norm_rows(o, "orc", x, None, 1e-5, centered)
+        yw = norm_rows(o, "orc", x, w, 1e-5, centered)
+        assert np.array_equal(yw.view(np.uint32), (yn * w).astype(np.float32).view(np.uint32))
+    z = np.zeros((2, 256), np.float32)
+    z[1] = 2.5
+    assert not norm_rows(o, "orc", z[:1], None, 1e-5, 0).any()
+    assert not norm_rows(o, "orc", z, None, 1e-5, 1).any()      # constant rows center to zero
+    y = norm_rows(o, "orc", z[1:], None, 0.0, 0)
+    assert np.all(y == 1.0)                                      # 2.5 * (1/2.5)
+
+
+def test_silu_gate_properties():
+    """silu(v)*u against the closed form in float64 (within two fp32 ulps: the
+    rounded exponential, sum and quotient), the
+    identity silu(v) - silu(-v) = v, the exact limits, and the gate applied
+    last: y(g, u) == fl(y(g, 1) * u)."""
+    o = oracle()
+    rng = np.random.default_rng(43)
+    g = (rng.standard_normal(1 << 16) * 8.0).astype(np.float32)
+    u = rng.standard_normal(g.size).astype(np.float32)
+    one = np.ones_like(g)
+    s = silu_gate(o, "orc", g, one)
+    exact = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    assert (np.abs(s - exact) <= 2.0 * ulp + 1e-45).all()
+    sn = silu_gate(o, "orc", -g, one)
+    assert (np.abs((s.astype(np.float64) - sn) - g) <= 4 * np.spacing(np.abs(g))).all()
+    y = silu_gate(o, "orc", g, u)
+    assert np.array_equal(y.view(np.uint32), (s * u).astype(np.float32).view(np.uint32))
+    lim = np.array([0.0, 104.0, 200.0, -104.0], np.float32)
+    out = silu_gate(o, "orc", lim, np.ones(4, np.float32))
+    assert out[0] == 0 and out[1] == 104.0 and out[2] == 200.0 and out[3] == 0.0
+
+
 # ---- planted mistakes ----
 
 MUTANTS = {
@@ -248,6 +303,10 @@ MUTANTS = {
     4: "Q8_0 quantizer dividing by the fp16 scale",
     5: "Q5_K six-bit unpack, wrong high bits for sub-blocks 4..7",
     6: "Q8_K quantizer keeping the last largest |x|",
+    7: "norm adding epsilon after the square root",
+    8: "norm multiplying by the weight before the inverse",
+    9: "centered norm subtracting the mean in fp32",
+    10: "SiLU as a reciprocal times v",
 }
 
 
@@ -269,6 +328,14 @@ def golden_mismatches(lib):
         wtype, m, n, k = (int(v) for v in g4[f"c{c}_shape"])
         y = quant_matmul(lib, "orc", g4[f"c{c}_w"], wtype, g4[f"c{c}_x"], n, threads=2)
         bad += int(not np.array_equal(y.view(np.uint32), g4[f"c{c}_y"].view(np.uint32)))
+    g5 = np.load(os.path.join(GOLDEN, "g5_norm.npz"))
+    for centered in (0, 1):
+        for wi in ("none", "w"):
+            y = norm_rows(lib, "orc", g5["x"], None if wi == "none" else g5["w"], float(g5["eps"][centered]), centered)
+            bad += int(not np.array_equal(y.view(np.uint32), g5[f"c{centered}_{wi}_y"].view(np.uint32)))
+    g6 = np.load(os.path.join(GOLDEN, "g6_silu_gate.npz"))
+    y = silu_gate(lib, "orc", g6["gate"], g6["up"])
+    bad += int(not np.array_equal(y.view(np.uint32), g6["y"].view(np.uint32)))
     return bad
 
 
