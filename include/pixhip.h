@@ -110,6 +110,10 @@ int pixhip_weight_get(pixhip_session* session, const char* key, const void* host
 /* Number of cached weights and their resident bytes. */
 int pixhip_weight_cache_info(pixhip_session* session, uint64_t* entries, uint64_t* bytes);
 
+/* The type and shape a handle was created with (PixWeight::type and shape
+ * {inner, rows}, src/model.h:33-39). */
+int pixhip_weight_shape(const pixhip_weight* weight, uint32_t* type, uint64_t* inner, uint64_t* rows);
+
 /* ---- the op: vulkan_matmul / VulkanState::multiply ---- */
 
 /* vulkan_matmul (src/backend_vulkan.h:139, src/backend_vulkan.cpp:1083-1094):

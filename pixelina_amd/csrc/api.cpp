@@ -721,6 +721,15 @@ int pixhip_weight_cache_info(pixhip_session* s, uint64_t* entries, uint64_t* byt
     return PIXHIP_OK;
 }
 
+int pixhip_weight_shape(const pixhip_weight* w, uint32_t* type, uint64_t* inner, uint64_t* rows)
+{
+    if (!w || !type || !inner || !rows) return fail(PIXHIP_ERR_ARGUMENT,"null weight handle or output pointer");
+    *type = w->type;
+    *inner = w->inner;
+    *rows = w->rows;
+    return PIXHIP_OK;
+}
+
 int pixhip_matmul(pixhip_session* s, const pixhip_weight* w, const float* input, size_t columns, float* output)
 {
     return run(s,w,input,columns,output,nullptr,0,0,PIXHIP_STAGE_QUANTIZE | PIXHIP_STAGE_MULTIPLY,true);

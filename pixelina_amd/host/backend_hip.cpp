@@ -100,6 +100,75 @@ bool hip_matmul_weight(pixhip_weight* weight, const float* input, size_t columns
     return active_state && pixhip_matmul(active_state->session,weight,input,columns,output) == PIXHIP_OK;
 }
 
+namespace {
+
+// A device copy of a host vector for the duration of one call (null stays null).
+struct DeviceVector {
+    pixhip_session* s;
+    void* p = nullptr;
+    bool ok = true;
+    DeviceVector(pixhip_session* session, const float* host, size_t count) : s(session)
+    {
+        if (!host) return;
+        p = pixhip_allocate(s,count * sizeof(float));
+        ok = p && pixhip_copy_to_device(s,p,host,count * sizeof(float)) == PIXHIP_OK;
+    }
+    ~DeviceVector()
+    {
+        if (p) pixhip_free(s,p);
+    }
+    const float* get() const { return static_cast<const float*>(p); }
+};
+
+// The GEMM of the session's last quantized activations with `w` into a host
+// (or device) output of rows x `rows of w` floats.
+bool multiply_into(pixhip_session* s, pixhip_weight* w, size_t rows, size_t out_rows, float* output)
+{
+    const size_t bytes = rows * out_rows * sizeof(float);
+    void* dev = pixhip_allocate(s,bytes);
+    if (!dev) return false;
+    bool ok = pixhip_matmul_stage(s,w,nullptr,rows,static_cast<float*>(dev),nullptr,0,0,PIXHIP_STAGE_MULTIPLY) == PIXHIP_OK &&
+              pixhip_copy_to_host(s,output,dev,bytes) == PIXHIP_OK;
+    pixhip_free(s,dev);
+    return ok;
+}
+
+uint64_t weight_rows(const pixhip_weight* w)
+{
+    uint32_t type = 0;
+    uint64_t inner = 0, rows = 0;
+    return pixhip_weight_shape(w,&type,&inner,&rows) == PIXHIP_OK? rows : 0;
+}
+
+}  // namespace
+
+bool hip_norm_multiply(uint32_t type, pixhip_weight* const* weights, float* const* outputs, size_t count, const float* input,
+                       size_t rows, size_t channels, const float* norm_weight, float epsilon, bool centered,
+                       const float* modulation, float* normalized)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    if (!s || !weights || !outputs) return false;
+    DeviceVector w(s,norm_weight,channels), m(s,modulation,channels);
+    if (!w.ok || !m.ok) return false;
+    if (pixhip_norm_quantize(s,type,input,rows,channels,w.get(),epsilon,centered? 1 : 0,m.get(),normalized,nullptr) != PIXHIP_OK)
+        return false;
+    for (size_t i = 0; i < count; i++) {
+        const uint64_t n = weights[i]? weight_rows(weights[i]) : 0;
+        if (!n || !multiply_into(s,weights[i],rows,n,outputs[i])) return false;
+    }
+    return true;
+}
+
+bool hip_silu_gate_multiply(uint32_t type, pixhip_weight* down, const float* gate, const float* up, size_t rows, size_t channels,
+                            float* output, float* gated)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    if (!s || !down) return false;
+    const uint64_t n = weight_rows(down);
+    if (!n || pixhip_silu_gate_quantize(s,type,gate,up,rows,channels,gated,nullptr) != PIXHIP_OK) return false;
+    return multiply_into(s,down,rows,n,output);
+}
+
 bool hip_available(std::string &description)
 {
     HipSession session;

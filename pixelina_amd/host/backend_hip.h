@@ -106,6 +106,29 @@ bool hip_matmul(const File &file, const Weight &weight, const float* input, size
     return w && hip_matmul_weight(w,input,columns,output);
 }
 
+// Producers of a linear layer's input fused with its quantizer (no Vulkan
+// counterpart: there tensor_norm / tensor_silu + tensor_gate run as their own
+// ops and each tensor_linear quantizes its input again).
+//
+// hip_norm_multiply: tensor_norm (src/tensor.cpp:174-197), then z_modulate
+// (src/inference.cpp:263-277) when `modulation` is not null, feeding `count`
+// linear layers that share the weight-type class of `type` and `channels`
+// inputs (e.g. the DiT block's FFN gate and up, src/inference.cpp:331-332):
+// the normalized rows are quantized once and every weight's GEMM reads them.
+// outputs[i] receives [rows][rows of weight i]; `normalized` (may be null) the
+// fp32 tensor the reference returns.  norm_weight / modulation are host
+// vectors of `channels` floats (as tensor_vector returns them), or null.
+bool hip_norm_multiply(uint32_t type, pixhip_weight* const* weights, float* const* outputs, size_t count, const float* input,
+                       size_t rows, size_t channels, const float* norm_weight, float epsilon, bool centered,
+                       const float* modulation, float* normalized);
+
+// hip_silu_gate_multiply: tensor_silu(gate) then tensor_gate(gate, up)
+// (src/tensor.cpp:199-209, :334-345) feeding the linear `down`
+// (src/inference.cpp:333-336): output [rows][rows of down]; `gated` (may be
+// null, may equal gate) receives the fp32 product.
+bool hip_silu_gate_multiply(uint32_t type, pixhip_weight* down, const float* gate, const float* up, size_t rows, size_t channels,
+                            float* output, float* gated);
+
 bool hip_available(std::string &description);
 
 #endif /* PIXELINA_BACKEND_HIP_H */

@@ -85,6 +85,11 @@ class Session:
                                          ctypes.byref(h)), "pixhip_weight_get")
         return h.value
 
+    def weight_shape(self, weight):
+        t, k, n = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64()
+        check(self.lib.pixhip_weight_shape(weight, ctypes.byref(t), ctypes.byref(k), ctypes.byref(n)), "pixhip_weight_shape")
+        return t.value, k.value, n.value
+
     def cache_info(self):
         n, b = ctypes.c_uint64(), ctypes.c_uint64()
         check(self.lib.pixhip_weight_cache_info(self.handle, ctypes.byref(n), ctypes.byref(b)), "pixhip_weight_cache_info")

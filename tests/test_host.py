@@ -54,7 +54,7 @@ def test_ctypes_table_matches_header():
 def test_cpp_shim_is_linked(lib):
     out = subprocess.run(["nm", "-DC", "--defined-only", _lib.LIBRARY], capture_output=True, text=True, check=True).stdout
     for sym in ("HipSession::initialize(int)", "hip_active_state()", "hip_synchronize()", "hip_matmul_weight(",
-                "hip_allocate(", "hip_free("):
+                "hip_allocate(", "hip_free(", "hip_norm_multiply(", "hip_silu_gate_multiply("):
         assert sym in out, sym
 
 
@@ -79,11 +79,15 @@ def test_entry_points_without_a_session(lib):
     assert lib.pixhip_matmul_ex(None, None, None, 1, None, None, 0, 0) == state
     assert lib.pixhip_quantize_q8_0(None, None, None, 1, 32) == state
     assert lib.pixhip_quantize_q8_K(None, None, None, 1, 256) == state
+    assert lib.pixhip_norm_quantize(None, 13, None, 1, 256, None, 1e-5, 0, None, None, None) == state
+    assert lib.pixhip_silu_gate_quantize(None, 8, None, None, 1, 32, None, None) == state
     assert lib.pixhip_synchronize(None) == state
     assert lib.pixhip_allocate(None, 16) is None
     lib.pixhip_free(None, None)  # no-op
     lib.pixhip_session_destroy(None)  # no-op
     assert b"session" in lib.pixhip_last_error()
+    t, k, n = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64()
+    assert lib.pixhip_weight_shape(None, ctypes.byref(t), ctypes.byref(k), ctypes.byref(n)) == _lib.ERR_ARGUMENT
 
 
 # ---- seeded inputs ----
