@@ -97,12 +97,20 @@ pixhip_weight* hip_weight(const std::string &key, const void* host_bytes, uint64
                           uint64_t rows);
 bool hip_matmul_weight(pixhip_weight* weight, const float* input, size_t columns, float* output);
 
+// The cached device form of one weight of a model file, keyed as
+// VulkanState::weight keys it (src/backend_vulkan.cpp:744).
+template <class File, class Weight>
+pixhip_weight* hip_weight_of(const File &file, const Weight &weight)
+{
+    if (weight.shape.size() != 2) return nullptr;
+    const std::string key = file.filename + ":" + weight.name + ":" + std::to_string(weight.offset) + ":" + std::to_string(weight.bytes);
+    return hip_weight(key,file.data + weight.offset,weight.bytes,weight.type,weight.shape[0],weight.shape[1]);
+}
+
 template <class File, class Weight>
 bool hip_matmul(const File &file, const Weight &weight, const float* input, size_t columns, float* output)
 {
-    if (weight.shape.size() != 2) return false;
-    const std::string key = file.filename + ":" + weight.name + ":" + std::to_string(weight.offset) + ":" + std::to_string(weight.bytes);
-    pixhip_weight* w = hip_weight(key,file.data + weight.offset,weight.bytes,weight.type,weight.shape[0],weight.shape[1]);
+    pixhip_weight* w = hip_weight_of(file,weight);
     return w && hip_matmul_weight(w,input,columns,output);
 }
 
