@@ -170,8 +170,10 @@ def bench_fused(sess, synth, _lib, Q5_K, Q8_0, reps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    # ~20 ms of untimed steps: the first 5-20 ms of work on an idle device run
+    # up to 30% slower (clock / power ramp) before the GEMM settles
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--matvec-reps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-matvec", action="store_true")
