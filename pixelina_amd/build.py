@@ -12,6 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 OBJDIR = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libpixhip.so")
+SHIM_CHECK = os.path.join(HERE, "shim_check")
 
 SOURCES = [
     "csrc/quantize.hip",
@@ -68,6 +69,14 @@ def build(verbose=False):
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIBRARY)
+    # The shim driver the GPU tests run (host code over the library).
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "host"),
+           os.path.join(HERE, "host", "shim_check.cpp"), "-o", SHIM_CHECK + ".tmp", "-L", HERE, "-lpixhip",
+           "-Wl,-rpath,$ORIGIN"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"shim_check build failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(SHIM_CHECK + ".tmp", SHIM_CHECK)
     if verbose:
         print(f"built {LIBRARY}")
     return LIBRARY
