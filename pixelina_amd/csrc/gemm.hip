@@ -558,7 +558,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
     } else if constexpr (!SUMS) {
         // Bias for this lane's column, loaded once (clamped index) and drained
         // before the stores: a load left pending here would make every store
-        // below wait for all earlier stores.
+        // below wait for all earlier stores.  The output is stored
+        // non-temporally: written once and not read here, it would otherwise
+        // push the weights and activations out of the last-level cache
+        // (measured: quantize + GEMM 403 -> 392 us at the DiT FFN shape).
         const uint32_t ln = lane_now();
         const int lr = (int)(ln & 31), lg = (int)(ln >> 5);
         const int mrow0 = x.m0 + x.wm * 64, ncol0 = x.n0 + x.wn * kWN;
@@ -572,7 +575,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = mrow0 + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-                if (full || (m < g.M && n < g.N)) col[(size_t)m * g.ldy] = acc.y[i][r] + bv;
+                if (full || (m < g.M && n < g.N)) __builtin_nontemporal_store(acc.y[i][r] + bv,col + (size_t)m * g.ldy);
             }
         }
     }
