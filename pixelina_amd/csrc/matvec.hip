@@ -28,6 +28,20 @@
 
 namespace pixhip {
 
+// A 16-byte load marked non-temporal: each weight byte is read once, so its
+// lines need not stay in the caches.  Only for loads whose 64 lanes cover
+// consecutive 16-byte pieces (the Q5_K planes: measured 10.17 -> 9.6 us at
+// 18944 x 3584); where lanes read 64-byte runs in four loads (the Q8_0 rows)
+// the later loads re-use the lines the first one fetched, and marking them
+// non-temporal made that kernel 1.7x slower.
+typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint4* p)
+{
+    const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(p));
+    return make_uint4(t.x,t.y,t.z,t.w);
+}
+
+
 constexpr int kMvWaves = 8;
 constexpr int kMvRows = 2;  // rows per register set (the longest Q8_0 and Q6_K rows use 1)
 // x staging passes per wave per 64 units of a row: a row of 64*UPL units has
@@ -244,9 +258,9 @@ __device__ __forceinline__ void q5_load(Q5Rows<UPL,R>& f, const PlanarQ5K& w, in
         for (int k = 0; k < UPL; k++) {
             const int u = min(lane + 64 * k,units - 1);
             const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2));
-            f.qs0[rr][k] = q[u];
-            f.qs1[rr][k] = q[units + u];
-            f.meta[rr][k] = w.meta[(size_t)row * units + u];
+            f.qs0[rr][k] = load_stream(q + u);
+            f.qs1[rr][k] = load_stream(q + units + u);
+            f.meta[rr][k] = load_stream(w.meta + (size_t)row * units + u);
         }
     }
 }
