@@ -216,6 +216,20 @@ int ensure_gemm_form(pixhip_session* s, pixhip_weight* w)
                                            const_cast<_Float16*>(w->q5.mn),s->stream),
                 "repack Q5_K");
     }
+    if (w->type == PIX_Q8_0 && !w->planes) {
+        const size_t kp = round_up(K,64);
+        Carver c;
+        size_t qs = c.take(npad * kp), dT = c.take((kp / PIX_QK8) * npad * 4);
+        int rc = weight_alloc(s,w,c.offset,&w->planes);
+        if (rc) return rc;
+        uint8_t* base = static_cast<uint8_t*>(w->planes);
+        PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");
+        w->q80.qs = reinterpret_cast<int8_t*>(base + qs);
+        w->q80.dT = reinterpret_cast<float*>(base + dT);
+        PIX_HIP(pixhip::launch_repack_q8_0(static_cast<const uint8_t*>(w->raw),N,K,kp,npad,const_cast<int8_t*>(w->q80.qs),
+                                           const_cast<float*>(w->q80.dT),nullptr,nullptr,s->stream),
+                "repack Q8_0 (GEMM)");
+    }
     if (w->type == PIX_Q6_K && !w->planes) {
         Carver c;
         size_t hi = c.take(npad * K), lo = c.take(npad * K), d = c.take(nb * npad * 4);
@@ -233,8 +247,23 @@ int ensure_gemm_form(pixhip_session* s, pixhip_weight* w)
 
 int ensure_matvec_form(pixhip_session* s, pixhip_weight* w)
 {
-    if (w->type == PIX_Q8_0 || w->planar) return PIXHIP_OK;
+    if (w->planar) return PIXHIP_OK;
     const size_t N = w->rows, K = w->inner, nb = K / PIX_QK;
+    if (w->type == PIX_Q8_0) {
+        const size_t kp = round_up(K,64);
+        Carver c;
+        size_t qs = c.take(N * kp), d = c.take(N * (kp / PIX_QK8) * 2);
+        int rc = weight_alloc(s,w,c.offset,&w->planar);
+        if (rc) return rc;
+        uint8_t* base = static_cast<uint8_t*>(w->planar);
+        PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");  // the padding unit's half
+        w->q80.qs_mv = reinterpret_cast<int8_t*>(base + qs);
+        w->q80.d = reinterpret_cast<_Float16*>(base + d);
+        PIX_HIP(pixhip::launch_repack_q8_0(static_cast<const uint8_t*>(w->raw),N,K,kp,0,nullptr,nullptr,const_cast<int8_t*>(w->q80.qs_mv),
+                                           const_cast<_Float16*>(w->q80.d),s->stream),
+                "repack Q8_0 (matvec)");
+        return PIXHIP_OK;
+    }
     if (w->type == PIX_Q5_K) {
         Carver c;
         size_t qs = c.take(N * K / 2), meta = c.take(N * (K / 64) * 16);
@@ -260,21 +289,6 @@ int ensure_matvec_form(pixhip_session* s, pixhip_weight* w)
     return PIXHIP_OK;
 }
 
-int build_q8_0(pixhip_session* s, pixhip_weight* w)
-{
-    const size_t N = w->rows, K = w->inner, npad = round_up(N,kTileN), kp = round_up(K,64);
-    Carver c;
-    size_t qs = c.take(npad * kp), d = c.take(N * (kp / PIX_QK8) * 2), dT = c.take((kp / PIX_QK8) * npad * 4);
-    int rc = weight_alloc(s,w,c.offset,&w->planar);
-    if (rc) return rc;
-    uint8_t* base = static_cast<uint8_t*>(w->planar);
-    PIX_HIP(hipMemsetAsync(base,0,c.offset,s->stream),"hipMemsetAsync");
-    w->q80 = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<_Float16*>(base + d),reinterpret_cast<float*>(base + dT)};
-    PIX_HIP(pixhip::launch_repack_q8_0(static_cast<const uint8_t*>(w->raw),N,K,kp,npad,const_cast<int8_t*>(w->q80.qs),
-                                       const_cast<_Float16*>(w->q80.d),const_cast<float*>(w->q80.dT),s->stream),
-            "repack Q8_0");
-    return PIXHIP_OK;
-}
 
 int check_shape(uint32_t type, uint64_t inner, uint64_t rows)
 {
@@ -392,6 +406,8 @@ int matvec(pixhip_session* s, pixhip_weight* w, const float* x, const pixhip::Ou
         if (rc) return rc;
         e = pixhip::launch_matvec_q5_K(w->q5p,x,w->rows,w->inner,out,s->stream);
     } else if (w->type == PIX_Q8_0) {
+        int rc = ensure_matvec_form(s,w);
+        if (rc) return rc;
         e = pixhip::launch_matvec_q8_0(w->q80,x,w->rows,w->inner,out,s->stream);
     } else {
         int rc = ensure_matvec_form(s,w);
@@ -703,7 +719,6 @@ int pixhip_weight_get(pixhip_session* s, const char* key, const void* host_bytes
         if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
         if (e != hipSuccess) rc = hip_fail(e,"weight upload");
     }
-    if (!rc && type == PIX_Q8_0) rc = build_q8_0(s,w);
     if (rc) {
         release_weight(s,w);
         return rc;

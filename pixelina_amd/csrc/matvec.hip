@@ -364,10 +364,11 @@ __device__ __forceinline__ void q80_load(Q80Rows<UPL,R>& f, const PlanarQ80& w, 
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
             const int u = min(lane + 64 * k,units - 1);
-            const uint4* p = reinterpret_cast<const uint4*>(w.qs + (size_t)row * Kp + 64 * u);
+            // piece t of unit u at (t*units + u)*16: each load is lane-contiguous
+            const uint4* p = reinterpret_cast<const uint4*>(w.qs_mv + (size_t)row * Kp);
 #pragma unroll
-            for (int t = 0; t < 4; t++) f.q[rr][k][t] = p[t];
-            f.dd[rr][k] = *reinterpret_cast<const uint32_t*>(w.d + (size_t)row * nbp + 2 * u);
+            for (int t = 0; t < 4; t++) f.q[rr][k][t] = load_stream(p + t * units + u);
+            f.dd[rr][k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w.d + (size_t)row * nbp + 2 * u));
         }
     }
 }

@@ -88,9 +88,10 @@ struct PlanesQ6K {
 };
 
 struct PlanarQ80 {
-    const int8_t* qs;     // [Npad][Kp]
-    const _Float16* d;    // [N][Kp/32]   (matvec)
+    const int8_t* qs;     // [Npad][Kp] (GEMM)
     const float* dT;      // [Kp/32][Npad] (GEMM)
+    const int8_t* qs_mv;  // [N][4][Kp/64][16]: each row piece-major (matvec)
+    const _Float16* d;    // [N][Kp/32] (matvec)
 };
 
 struct PlanarQ5K {
@@ -141,8 +142,10 @@ hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inn
 hipError_t launch_repack_q5_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* qs, uint4* meta, hipStream_t s);
 hipError_t launch_repack_q6_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* ql, uint8_t* qh, int8_t* sc,
                                      _Float16* d, hipStream_t s);
-hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, size_t kpad, size_t rows_pad, int8_t* qs, _Float16* d,
-                              float* dT, hipStream_t s);
+// Q8_0 forms: the GEMM's (qs, dT: pass null to skip) and the matvec's
+// (qs_mv, d: pass null to skip), from the GGUF blocks.
+hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, size_t kpad, size_t rows_pad, int8_t* qs, float* dT,
+                              int8_t* qs_mv, _Float16* d, hipStream_t s);
 
 // gemm.hip
 // Split-K workspace (fp32 partial outputs) a GEMM of M x N over K (rounded up

@@ -118,11 +118,16 @@ __global__ __launch_bounds__(256) void repack_q6_K_planar_kernel(const uint8_t* 
 // Q8_0: 34-byte blocks (2-byte aligned) -> int8 plane + fp16 scale plane with
 // row stride kpad (the caller zero-fills the padding once at allocation).
 // One 8-lane group per block, 4 values per lane.
+// Block b of a row holds values 32b..32b+31: unit b/2, 16-byte pieces
+// 2(b%2) and 2(b%2)+1 of it.  The matvec form stores piece p of unit u at
+// (p*units + u)*16 in the row, so that a load of piece p by 64 lanes reading
+// consecutive units is one contiguous 1 KB run.
 __global__ __launch_bounds__(256) void repack_q8_0_kernel(const uint8_t* __restrict__ raw, size_t rows, size_t inner,
                                                           size_t kpad, size_t rows_pad, int8_t* __restrict__ qs,
-                                                          _Float16* __restrict__ d, float* __restrict__ dT)
+                                                          float* __restrict__ dT, int8_t* __restrict__ qs_mv,
+                                                          _Float16* __restrict__ d)
 {
-    const size_t nb = inner / PIX_QK8;
+    const size_t nb = inner / PIX_QK8, units = kpad / 64;
     const size_t blk = ((size_t)blockIdx.x * 256 + threadIdx.x) >> 3;
     if (blk >= rows * nb) return;
     const int part = threadIdx.x & 7;
@@ -130,11 +135,15 @@ __global__ __launch_bounds__(256) void repack_q8_0_kernel(const uint8_t* __restr
     const uint8_t* src = raw + blk * PIX_Q8_0_BYTES;
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src + 2 + 4 * part);
     uint32_t v = (uint32_t)s16[0] | ((uint32_t)s16[1] << 16);
-    *reinterpret_cast<uint32_t*>(qs + row * kpad + b * PIX_QK8 + 4 * part) = v;
-    if (part == 0) {
-        const uint16_t h = *reinterpret_cast<const uint16_t*>(src);
-        d[row * (kpad / PIX_QK8) + b] = __builtin_bit_cast(_Float16,h);
-        dT[b * rows_pad + row] = half_bits_to_float(h);
+    const uint16_t h = *reinterpret_cast<const uint16_t*>(src);
+    if (qs) {
+        *reinterpret_cast<uint32_t*>(qs + row * kpad + b * PIX_QK8 + 4 * part) = v;
+        if (part == 0) dT[b * rows_pad + row] = half_bits_to_float(h);
+    }
+    if (qs_mv) {
+        const size_t piece = 2 * (b & 1) + (part >> 2), u = b >> 1;
+        *reinterpret_cast<uint32_t*>(qs_mv + row * kpad + (piece * units + u) * 16 + 4 * (part & 3)) = v;
+        if (part == 0) d[row * (kpad / PIX_QK8) + b] = __builtin_bit_cast(_Float16,h);
     }
 }
 
@@ -207,12 +216,12 @@ hipError_t launch_repack_q6_K_planar(const uint8_t* raw, size_t rows, size_t inn
     return hipGetLastError();
 }
 
-hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, size_t kpad, size_t rows_pad, int8_t* qs, _Float16* d,
-                              float* dT, hipStream_t s)
+hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, size_t kpad, size_t rows_pad, int8_t* qs, float* dT,
+                              int8_t* qs_mv, _Float16* d, hipStream_t s)
 {
     size_t blocks = rows * (inner / PIX_QK8);
     if (!blocks) return hipSuccess;
-    repack_q8_0_kernel<<<(unsigned)((blocks * 8 + 255) / 256),256,0,s>>>(raw,rows,inner,kpad,rows_pad,qs,d,dT);
+    repack_q8_0_kernel<<<(unsigned)((blocks * 8 + 255) / 256),256,0,s>>>(raw,rows,inner,kpad,rows_pad,qs,dT,qs_mv,d);
     return hipGetLastError();
 }
 
