@@ -461,12 +461,15 @@ __device__ __forceinline__ void q6_load(Q6Rows<UPL,R>& f, const PlanarQ6K& w, in
         for (int k = 0; k < UPL; k++) {
             const int u = min(lane + 64 * k,units - 1);
             const int b = u >> 2, h = (u >> 1) & 1, ih = u & 1;
-            const uint8_t* ql = w.ql + (size_t)row * (K / 2) + b * 128 + 64 * h + 16 * ih;
-            f.la[rr][k] = *reinterpret_cast<const uint4*>(ql);
-            f.lb[rr][k] = *reinterpret_cast<const uint4*>(ql + 32);
-            f.hh[rr][k] = *reinterpret_cast<const uint4*>(w.qh + (size_t)row * (K / 4) + b * 64 + 32 * h + 16 * ih);
+            // ql as two unit-major planes of 16-byte pieces; qh is unit-major as
+            // stored (b*64 + 32h + 16ih = 16u): every load is lane-contiguous
+            const uint4* ql = reinterpret_cast<const uint4*>(w.ql + (size_t)row * (K / 2));
+            f.la[rr][k] = load_stream(ql + u);
+            f.lb[rr][k] = load_stream(ql + units + u);
+            f.hh[rr][k] = load_stream(reinterpret_cast<const uint4*>(w.qh + (size_t)row * (K / 4)) + u);
             f.scw[rr][k] = *reinterpret_cast<const uint2*>(w.sc + (size_t)row * (K / 16) + b * 16 + 8 * h);
             f.dh[rr][k] = __builtin_bit_cast(uint16_t,w.d[(size_t)row * nb + b]);
+            (void)ih;
         }
     }
 }

@@ -108,8 +108,20 @@ __global__ __launch_bounds__(256) void repack_q6_K_planar_kernel(const uint8_t* 
     const size_t row = blk / nb, b = blk % nb;
     const uint8_t* src = raw + blk * PIX_Q6_K_BYTES;
     // 210 bytes: ql 0..127, qh 128..191, scales 192..207, d 208..209.
-    ql[row * (inner / 2) + b * 128 + lane] = src[lane];
-    ql[row * (inner / 2) + b * 128 + 64 + lane] = src[64 + lane];
+    // ql byte j of the block (half h = j/64, r = j%64) belongs to 64-value unit
+    // u = 4b + 2h + (r%32)/16, as its first 16-byte piece when r < 32 and its
+    // second when r >= 32.  The row's ql is stored as two planes of pieces,
+    // unit-major (first pieces at u*16, second at (units + u)*16), so that a
+    // load of either piece by 64 lanes reading consecutive units is one
+    // contiguous 1 KB run.
+    const size_t units = inner / 64;
+    uint8_t* qrow = ql + row * (inner / 2);
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const int r = lane;  // byte 64*hh + lane
+        const size_t u = 4 * b + 2 * hh + ((r & 31) >> 4);
+        qrow[((r < 32? 0 : units) + u) * 16 + (r & 15)] = src[64 * hh + lane];
+    }
     qh[row * (inner / 4) + b * 64 + lane] = src[128 + lane];
     if (lane < 16) sc[row * (inner / 16) + b * 16 + lane] = (int8_t)src[192 + lane];
     if (lane == 0) d[row * nb + b] = __builtin_bit_cast(_Float16,(uint16_t)(src[208] | (src[209] << 8)));
