@@ -192,6 +192,33 @@ int pixhip_norm_quantize(pixhip_session* session, uint32_t type, const float* in
 int pixhip_silu_gate_quantize(pixhip_session* session, uint32_t type, const float* gate, const float* up, size_t rows,
                               size_t inner, float* gated, void* blocks);
 
+/* ---- elementwise ops of the layer around the linears ---- */
+
+/* Operation ids of vulkan_pointwise (src/vulkan_ops.h:24-49). */
+#define PIXHIP_OP_SILU 2u        /* tensor_silu, src/tensor.cpp:199-209: v / (1.0f + expf(-v)) */
+#define PIXHIP_OP_GATE 3u        /* tensor_gate, :334-345: v * second[i] */
+#define PIXHIP_OP_ADD 4u         /* tensor_add, :321-332: v + second[i] */
+#define PIXHIP_OP_BIAS 14u       /* tensor_bias, :226-240 (vulkan_bias): v + second[i % channels] */
+#define PIXHIP_OP_GELU_EXACT 18u /* tensor_gelu(exact), :211-224: 0.5f*v*(1 + erff(v/sqrt 2)) */
+#define PIXHIP_OP_GELU_TANH 19u  /* tensor_gelu(approximate): 0.5f*v*(1 + tanhf(0.7978845608f*(v + 0.044715f*v^3))) */
+
+/* vulkan_pointwise(operation, destination, second, nullptr) (src/backend_vulkan.cpp:1112-1127)
+ * and vulkan_bias: `destination` [rows][channels] updated in place with the
+ * fp32 arithmetic of the CPU op named above, in its order.  `second` is
+ * [rows][channels] for GATE and ADD, [channels] for BIAS, unused (NULL) for
+ * SILU and GELU.  expf / erff / tanhf are correctly rounded here (glibc's are
+ * within about an ulp).  Device pointers, 4-byte aligned. */
+int pixhip_pointwise(pixhip_session* session, unsigned operation, float* destination, const float* second, size_t rows,
+                     size_t channels);
+
+/* tensor_rope (src/tensor.cpp:429-452; vulkan_rope, src/backend_vulkan.h:145):
+ * in place on `tensor` [rows][heads * dim]; for each head and pair i < dim/2,
+ * (first, second) = (2i, 2i+1) when `interleaved`, else (i, i + dim/2), and
+ * (a, b) -> (a*c - b*s, a*s + b*c) with c, s = cosine, sine [rows][dim/2][i],
+ * in fp32 without contraction (bit-exact).  Device pointers. */
+int pixhip_rope(pixhip_session* session, float* tensor, size_t rows, size_t channels, size_t heads, const float* cosine,
+                const float* sine, int interleaved);
+
 /* ---- integer parity gate ---- */
 
 /* Runs the GEMM kernel's integer path and writes, for every (column c, row r,

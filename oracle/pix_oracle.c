@@ -32,6 +32,8 @@
  *   8 norm multiplying by the weight before the inverse
  *   9 centered norm subtracting the mean in fp32
  *  10 SiLU as v * (1 / (1 + e)) instead of a division
+ *  11 RoPE with the sine's sign flipped
+ *  12 tanh GELU with v*v instead of v*v*v
  */
 #ifndef ORC_MUTANT
 #define ORC_MUTANT 0
@@ -535,4 +537,55 @@ void orc_silu_gate(const float* gate, const float* up, size_t count, float* out)
 #endif
         out[i] = v * up[i];
     }
+}
+
+/* tensor_gelu, src/tensor.cpp:211-224, in place: approximate (tanh) form
+ * 0.5f*v*(1 + tanhf(0.7978845608f*(v + 0.044715f*v*v*v))), exact form
+ * 0.5f*v*(1 + erff(v/1.4142135623730951f)), fp32 left to right. */
+void orc_gelu(float* x, size_t count, int approximate)
+{
+    for (size_t i = 0; i < count; i++) {
+        float v = x[i];
+#if ORC_MUTANT == 12
+        float argument = approximate? tanhf(0.7978845608028654f * (v + 0.044715f * v * v)) : erff(v / 1.4142135623730951f);
+#else
+        float argument = approximate? tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)) : erff(v / 1.4142135623730951f);
+#endif
+        x[i] = 0.5f * v * (1 + argument);
+    }
+}
+
+/* tensor_bias, src/tensor.cpp:226-240: x[r][c] += bias[c]. */
+void orc_bias(float* x, size_t rows, size_t channels, const float* bias)
+{
+    for (size_t i = 0; i < rows * channels; i++) x[i] += bias[i % channels];
+}
+
+/* tensor_add, src/tensor.cpp:321-332: x[i] += y[i]. */
+void orc_add(float* x, const float* y, size_t count)
+{
+    for (size_t i = 0; i < count; i++) x[i] += y[i];
+}
+
+/* tensor_rope, src/tensor.cpp:429-452, in place on rows x (heads * dim):
+ * for each pair i < dim/2 of each head, (first, second) = (2i, 2i+1) when
+ * interleaved, else (i, i + dim/2); a, b = the pair, c, s = cosine and sine
+ * [row][i]; first = a*c - b*s, second = a*s + b*c (fp32, no contraction). */
+void orc_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, int interleaved)
+{
+    size_t dim = channels / heads;
+    for (size_t row = 0; row < rows; row++)
+        for (size_t head = 0; head < heads; head++) {
+            float* data = x + row * channels + head * dim;
+            for (size_t i = 0; i < dim / 2; i++) {
+                size_t first = interleaved? i * 2 : i, second = interleaved? i * 2 + 1 : i + dim / 2;
+                float a = data[first], b = data[second];
+                float c = cosine[row * dim / 2 + i], s = sine[row * dim / 2 + i];
+#if ORC_MUTANT == 11
+                s = -s;
+#endif
+                data[first] = a * c - b * s;
+                data[second] = a * s + b * c;
+            }
+        }
 }

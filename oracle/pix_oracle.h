@@ -49,6 +49,10 @@ uint64_t orc_row_bytes(uint64_t inner, uint32_t type);
 void orc_norm_rows(const float* x, size_t rows, size_t channels, const float* weight, float epsilon, int centered, float* out);
 void orc_modulate_rows(float* x, size_t rows, size_t channels, const float* scale);
 void orc_silu_gate(const float* gate, const float* up, size_t count, float* out);
+void orc_gelu(float* x, size_t count, int approximate);
+void orc_bias(float* x, size_t rows, size_t channels, const float* bias);
+void orc_add(float* x, const float* y, size_t count);
+void orc_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, int interleaved);
 
 #ifdef __cplusplus
 }

@@ -111,4 +111,42 @@ void ref_silu_gate(const float* gate, const float* up, size_t count, float* out)
     std::copy(g.values.begin(),g.values.end(),out);
 }
 
+/* tensor_gelu, src/tensor.cpp:211-224 */
+void ref_gelu(float* x, size_t count, int approximate)
+{
+    PixTensor t(1,count);
+    std::copy(x,x + count,t.values.begin());
+    tensor_gelu(t,approximate != 0);
+    std::copy(t.values.begin(),t.values.end(),x);
+}
+
+/* tensor_bias, src/tensor.cpp:226-240 */
+void ref_bias(float* x, size_t rows, size_t channels, const float* bias)
+{
+    PixTensor t(rows,channels);
+    std::copy(x,x + rows * channels,t.values.begin());
+    tensor_bias(t,std::vector<float>(bias,bias + channels));
+    std::copy(t.values.begin(),t.values.end(),x);
+}
+
+/* tensor_add, src/tensor.cpp:321-332 */
+void ref_add(float* x, const float* y, size_t count)
+{
+    PixTensor a(1,count),b(1,count);
+    std::copy(x,x + count,a.values.begin());
+    std::copy(y,y + count,b.values.begin());
+    tensor_add(a,b);
+    std::copy(a.values.begin(),a.values.end(),x);
+}
+
+/* tensor_rope, src/tensor.cpp:429-452 */
+void ref_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, int interleaved)
+{
+    PixTensor t(rows,channels);
+    std::copy(x,x + rows * channels,t.values.begin());
+    const size_t half = rows * (channels / heads) / 2;
+    tensor_rope(t,heads,std::vector<float>(cosine,cosine + half),std::vector<float>(sine,sine + half),interleaved != 0);
+    std::copy(t.values.begin(),t.values.end(),x);
+}
+
 }

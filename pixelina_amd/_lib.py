@@ -58,6 +58,8 @@ SIGNATURES = {
     "pixhip_quantize_q8_K": (_int, [_vp, _vp, _vp, _sz, _sz]),
     "pixhip_norm_quantize": (_int, [_vp, _u32, _vp, _sz, _sz, _vp, ctypes.c_float, _int, _vp, _vp, _vp]),
     "pixhip_silu_gate_quantize": (_int, [_vp, _u32, _vp, _vp, _sz, _sz, _vp, _vp]),
+    "pixhip_pointwise": (_int, [_vp, ctypes.c_uint, _vp, _vp, _sz, _sz]),
+    "pixhip_rope": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
     "pixhip_block_sums": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "pixhip_timer_start": (_int, [_vp]),
     "pixhip_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),

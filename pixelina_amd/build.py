@@ -20,6 +20,7 @@ SOURCES = [
     "csrc/gemm.hip",
     "csrc/matvec.hip",
     "csrc/fuse.hip",
+    "csrc/ops.hip",
     "csrc/api.cpp",
     "host/backend_hip.cpp",
 ]

@@ -868,6 +868,34 @@ int pixhip_silu_gate_quantize(pixhip_session* s, uint32_t type, const float* gat
     return PIXHIP_OK;
 }
 
+int pixhip_pointwise(pixhip_session* s, unsigned operation, float* destination, const float* second, size_t rows, size_t channels)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    const bool needs_second = operation == PIXHIP_OP_GATE || operation == PIXHIP_OP_ADD || operation == PIXHIP_OP_BIAS;
+    if (operation != PIXHIP_OP_SILU && operation != PIXHIP_OP_GELU_EXACT && operation != PIXHIP_OP_GELU_TANH && !needs_second)
+        return fail(PIXHIP_ERR_UNSUPPORTED,"unsupported pointwise operation " + std::to_string(operation));
+    if (!rows || !channels || !destination || (needs_second && !second))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    if ((reinterpret_cast<uintptr_t>(destination) | reinterpret_cast<uintptr_t>(second)) % 4)
+        return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    PIX_HIP(pixhip::launch_pointwise((int)operation,destination,second,rows,channels,s->stream),"pointwise");
+    return PIXHIP_OK;
+}
+
+int pixhip_rope(pixhip_session* s, float* tensor, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine,
+                int interleaved)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!tensor || !cosine || !sine || !rows || !heads || channels % heads || (channels / heads) % 2)
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer, or channels not heads x an even head size");
+    if ((reinterpret_cast<uintptr_t>(tensor) | reinterpret_cast<uintptr_t>(cosine) | reinterpret_cast<uintptr_t>(sine)) % 4)
+        return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    PIX_HIP(pixhip::launch_rope(tensor,rows,channels,heads,cosine,sine,interleaved != 0,s->stream),"rope");
+    return PIXHIP_OK;
+}
+
 int pixhip_block_sums(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t columns, int32_t* sums, int32_t* mins)
 {
     int rc = use_device(s);

@@ -134,6 +134,12 @@ hipError_t launch_norm_quantize(const float* x, size_t rows, size_t K, const flo
 hipError_t launch_silu_gate_quantize(const float* gate, const float* up, size_t rows, size_t K, int kind, size_t kpad,
                                      const ActOut& out, hipStream_t s);
 
+// ops.hip: elementwise ops in place (operation ids of src/vulkan_ops.h:24-49)
+constexpr int kOpSilu = 2, kOpGate = 3, kOpAdd = 4, kOpBias = 14, kOpGeluExact = 18, kOpGeluTanh = 19;
+hipError_t launch_pointwise(int op, float* x, const float* other, size_t rows, size_t channels, hipStream_t s);
+hipError_t launch_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, bool interleaved,
+                       hipStream_t s);
+
 // repack.hip
 hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
                               float* dm, _Float16* mn, hipStream_t s);

@@ -122,6 +122,12 @@ class Session:
     def silu_gate_quantize(self, wtype, gate_ptr, up_ptr, rows, inner, gated_ptr=None, blocks_ptr=None):
         return self.lib.pixhip_silu_gate_quantize(self.handle, wtype, gate_ptr, up_ptr, rows, inner, gated_ptr, blocks_ptr)
 
+    def pointwise(self, op, dst_ptr, second_ptr, rows, channels):
+        return self.lib.pixhip_pointwise(self.handle, op, dst_ptr, second_ptr, rows, channels)
+
+    def rope(self, x_ptr, rows, channels, heads, cos_ptr, sin_ptr, interleaved):
+        return self.lib.pixhip_rope(self.handle, x_ptr, rows, channels, heads, cos_ptr, sin_ptr, int(interleaved))
+
     def block_sums(self, weight, x_ptr, columns, sums_ptr, mins_ptr=None):
         return self.lib.pixhip_block_sums(self.handle, weight, x_ptr, columns, sums_ptr, mins_ptr)
 

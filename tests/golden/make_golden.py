@@ -15,8 +15,10 @@ Fixtures (numpy .npz, data only):
                         Q8_0 blocks of its outputs
   g6_silu_gate.npz      tensor_silu then tensor_gate on special and random
                         values, and the Q8_K / Q8_0 blocks of the product
+  g7_ops.npz            tensor_gelu (both forms), tensor_bias, tensor_add and
+                        tensor_rope (split and interleaved halves)
 
-    python tests/golden/make_golden.py g5 g6   # only the named fixtures
+    python tests/golden/make_golden.py g5 g6 g7   # only the named fixtures
 """
 import os
 import sys
@@ -28,7 +30,8 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.dirname(HERE))
 
-from oracle_lib import Q5_K, Q6_K, Q8_0, dot, norm_rows, quant_matmul, quantize, reference, silu_gate  # noqa: E402
+from oracle_lib import (Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, norm_rows, quant_matmul, quantize, reference,  # noqa: E402
+                        rope, silu_gate)
 from pixelina_amd import synth  # noqa: E402
 
 
@@ -123,6 +126,21 @@ def write_g6(ref):
                         q8_K=quantize(ref, "ref", y, "q8_K"), q8_0=quantize(ref, "ref", y, "q8_0"))
 
 
+def write_g7(ref):
+    rng = np.random.default_rng(707)
+    rows, heads, dim = 5, 4, 64
+    x = (rng.standard_normal((rows, heads * dim)) * 3.0).astype(np.float32)
+    x[0, :12] = [0.0, -0.0, 1e-30, -1e-30, 10.0, -10.0, 6.0, -6.0, 40.0, -40.0, 0.5, -0.5]
+    b = rng.standard_normal(heads * dim).astype(np.float32)
+    y = rng.standard_normal((rows, heads * dim)).astype(np.float32)
+    theta = rng.uniform(0, 2 * np.pi, (rows, dim // 2))
+    cos, sin = np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
+    np.savez_compressed(os.path.join(HERE, "g7_ops.npz"), x=x, b=b, y=y, cos=cos, sin=sin, heads=np.array(heads),
+                        gelu_exact=gelu(ref, "ref", x, 0), gelu_tanh=gelu(ref, "ref", x, 1), bias=bias(ref, "ref", x, b),
+                        add=add(ref, "ref", x, y), rope_split=rope(ref, "ref", x, heads, cos, sin, 0),
+                        rope_interleaved=rope(ref, "ref", x, heads, cos, sin, 1))
+
+
 def main():
     ref = reference()
     if ref is None:
@@ -133,6 +151,8 @@ def main():
             write_g5(ref)
         if "g6" in only:
             write_g6(ref)
+        if "g7" in only:
+            write_g7(ref)
         return
     rng = np.random.default_rng(20260101)
 
@@ -196,6 +216,7 @@ def main():
     np.savez_compressed(os.path.join(HERE, "g4_matmul.npz"), **g4)
     write_g5(ref)
     write_g6(ref)
+    write_g7(ref)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -43,6 +43,10 @@ def load_oracle(path):
         "orc_norm_rows": (None, [_vp, _sz, _sz, _vp, ctypes.c_float, _int, _vp]),
         "orc_modulate_rows": (None, [_vp, _sz, _sz, _vp]),
         "orc_silu_gate": (None, [_vp, _vp, _sz, _vp]),
+        "orc_gelu": (None, [_vp, _sz, _int]),
+        "orc_bias": (None, [_vp, _sz, _sz, _vp]),
+        "orc_add": (None, [_vp, _vp, _sz]),
+        "orc_rope": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -81,6 +85,10 @@ def reference():
             "ref_row_bytes": (ctypes.c_uint64, [ctypes.c_uint64, _u32]),
             "ref_norm_rows": (_int, [_vp, _sz, _sz, _vp, ctypes.c_float, _int, _vp]),
             "ref_silu_gate": (None, [_vp, _vp, _sz, _vp]),
+            "ref_gelu": (None, [_vp, _sz, _int]),
+            "ref_bias": (None, [_vp, _sz, _sz, _vp]),
+            "ref_add": (None, [_vp, _vp, _sz]),
+            "ref_rope": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -162,6 +170,31 @@ def silu_gate(lib, prefix, gate, up):
     out = np.full_like(g, np.nan)
     getattr(lib, f"{prefix}_silu_gate")(ptr(g), ptr(u), g.size, ptr(out))
     return out
+
+
+def gelu(lib, prefix, x, approximate):
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    getattr(lib, f"{prefix}_gelu")(ptr(y), y.size, int(approximate))
+    return y
+
+
+def bias(lib, prefix, x, b):
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    getattr(lib, f"{prefix}_bias")(ptr(y), y.shape[0], y.shape[1], ptr(np.ascontiguousarray(b, dtype=np.float32)))
+    return y
+
+
+def add(lib, prefix, x, other):
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    getattr(lib, f"{prefix}_add")(ptr(y), ptr(np.ascontiguousarray(other, dtype=np.float32)), y.size)
+    return y
+
+
+def rope(lib, prefix, x, heads, cosine, sine, interleaved):
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    getattr(lib, f"{prefix}_rope")(ptr(y), y.shape[0], y.shape[1], heads, ptr(np.ascontiguousarray(cosine, dtype=np.float32)),
+                                   ptr(np.ascontiguousarray(sine, dtype=np.float32)), int(interleaved))
+    return y
 
 
 def decode(lib, w, wtype, count):

@@ -83,6 +83,8 @@ def test_entry_points_without_a_session(lib):
     assert lib.pixhip_quantize_q8_K(None, None, None, 1, 256) == state
     assert lib.pixhip_norm_quantize(None, 13, None, 1, 256, None, 1e-5, 0, None, None, None) == state
     assert lib.pixhip_silu_gate_quantize(None, 8, None, None, 1, 32, None, None) == state
+    assert lib.pixhip_pointwise(None, 2, None, None, 1, 4) == state
+    assert lib.pixhip_rope(None, None, 1, 8, 1, None, None, 0) == state
     assert lib.pixhip_synchronize(None) == state
     assert lib.pixhip_allocate(None, 16) is None
     lib.pixhip_free(None, None)  # no-op

@@ -8,7 +8,8 @@ import os
 import numpy as np
 import pytest
 
-from oracle_lib import (Q5_K, Q6_K, Q8_0, dot, norm_rows, oracle, quant_matmul, quantize, reference, silu_gate)
+from oracle_lib import (Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, norm_rows, oracle, quant_matmul, quantize, reference, rope,
+                        silu_gate)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 WTYPES = {"q8_0": Q8_0, "q5_K": Q5_K, "q6_K": Q6_K}
@@ -132,3 +133,25 @@ def test_silu_gate_matches_reference_vectors():
         gate = (rng.standard_normal(1 << 18) * 10).astype(np.float32)
         up = rng.standard_normal(gate.size).astype(np.float32)
         assert np.array_equal(bits(silu_gate(oracle(), "orc", gate, up)), bits(silu_gate(ref, "ref", gate, up)))
+
+
+def test_elementwise_ops_match_reference_vectors():
+    """tensor_gelu, tensor_bias, tensor_add, tensor_rope (src/tensor.cpp:211-240,
+    :321-332, :429-452), bit-exact."""
+    g = golden("g7_ops")
+    o, h = oracle(), int(g["heads"])
+    assert np.array_equal(bits(gelu(o, "orc", g["x"], 0)), bits(g["gelu_exact"]))
+    assert np.array_equal(bits(gelu(o, "orc", g["x"], 1)), bits(g["gelu_tanh"]))
+    assert np.array_equal(bits(bias(o, "orc", g["x"], g["b"])), bits(g["bias"]))
+    assert np.array_equal(bits(add(o, "orc", g["x"], g["y"])), bits(g["add"]))
+    assert np.array_equal(bits(rope(o, "orc", g["x"], h, g["cos"], g["sin"], 0)), bits(g["rope_split"]))
+    assert np.array_equal(bits(rope(o, "orc", g["x"], h, g["cos"], g["sin"], 1)), bits(g["rope_interleaved"]))
+    ref = reference()
+    if ref is not None:
+        rng = np.random.default_rng(11)
+        x = (rng.standard_normal((16, 512)) * 5).astype(np.float32)
+        for form in (0, 1):
+            assert np.array_equal(bits(gelu(o, "orc", x, form)), bits(gelu(ref, "ref", x, form)))
+        cs, sn = rng.standard_normal((2, 16, 64)).astype(np.float32)
+        for il in (0, 1):
+            assert np.array_equal(bits(rope(o, "orc", x, 4, cs, sn, il)), bits(rope(ref, "ref", x, 4, cs, sn, il)))

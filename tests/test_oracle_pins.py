@@ -9,8 +9,8 @@ import subprocess
 import numpy as np
 import pytest
 
-from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, dot, load_oracle, norm_rows, oracle, ptr, quant_matmul, quantize,
-                        silu_gate)
+from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, load_oracle, norm_rows, oracle, ptr,
+                        quant_matmul, quantize, rope, silu_gate)
 from pixelina_amd import synth
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -294,6 +294,45 @@ def test_silu_gate_properties():
     assert out[0] == 0 and out[1] == 104.0 and out[2] == 200.0 and out[3] == 0.0
 
 
+def test_elementwise_ops_properties():
+    """GELU against the float64 closed forms (the fp32 factor 1 + erf (or tanh)
+    carries an absolute error of about an ulp of 1, which for negative v cancels
+    towards zero: bound |0.5 v| * 3e-7 plus 3 ulps of the result), gelu(0) = 0 and
+    the exact large-|v| limits; RoPE with cos 1 / sin 0 is the identity, a
+    rotation by a quarter turn maps (a, b) to (-b, a) exactly, and it keeps
+    every pair's length to fp32 rounding; bias and add equal their fp32 sums."""
+    o = oracle()
+    rng = np.random.default_rng(47)
+    x = (rng.standard_normal((8, 256)) * 4.0).astype(np.float32)
+    xd = x.astype(np.float64)
+    from math import erf as _erf
+    exact = 0.5 * xd * (1.0 + np.vectorize(_erf)(xd / np.sqrt(2.0)))
+    approx = 0.5 * xd * (1.0 + np.tanh(0.7978845608028654 * (xd + 0.044715 * xd ** 3)))
+    for form, want in ((0, exact), (1, approx)):
+        got = gelu(o, "orc", x, form).astype(np.float64)
+        tol = 0.5 * np.abs(xd) * 3e-7 + 3 * np.spacing(np.abs(want).astype(np.float32)).astype(np.float64) + 1e-30
+        assert (np.abs(got - want) <= tol).all(), form
+        lim = gelu(o, "orc", np.array([[0.0, 20.0, -20.0]], np.float32), form)
+        assert lim[0, 0] == 0.0 and lim[0, 1] == 20.0 and lim[0, 2] == 0.0
+    heads, dim = 4, 64
+    ones, zeros = np.ones((8, dim // 2), np.float32), np.zeros((8, dim // 2), np.float32)
+    for il in (0, 1):
+        assert np.array_equal(rope(o, "orc", x, heads, ones, zeros, il), x)
+        q = rope(o, "orc", x, heads, zeros, ones, il).reshape(8, heads, -1)
+        xr = x.reshape(8, heads, -1)
+        first = np.arange(0, dim, 2) if il else np.arange(dim // 2)
+        second = first + 1 if il else first + dim // 2
+        assert np.array_equal(q[..., first], -xr[..., second]) and np.array_equal(q[..., second], xr[..., first])
+        th = rng.uniform(0, 6.3, (8, dim // 2))
+        r = rope(o, "orc", x, heads, np.cos(th).astype(np.float32), np.sin(th).astype(np.float32), il).reshape(8, heads, -1)
+        n0 = np.hypot(xr[..., first].astype(np.float64), xr[..., second])
+        n1 = np.hypot(r[..., first].astype(np.float64), r[..., second])
+        assert np.allclose(n0, n1, rtol=1e-6, atol=1e-6)
+    b = rng.standard_normal(256).astype(np.float32)
+    y = rng.standard_normal((8, 256)).astype(np.float32)
+    assert np.array_equal(bias(o, "orc", x, b), x + b) and np.array_equal(add(o, "orc", x, y), x + y)
+
+
 # ---- planted mistakes ----
 
 MUTANTS = {
@@ -307,6 +346,8 @@ MUTANTS = {
     8: "norm multiplying by the weight before the inverse",
     9: "centered norm subtracting the mean in fp32",
     10: "SiLU as a reciprocal times v",
+    11: "RoPE with the sine's sign flipped",
+    12: "tanh GELU with v*v instead of v*v*v",
 }
 
 
@@ -336,6 +377,13 @@ def golden_mismatches(lib):
     g6 = np.load(os.path.join(GOLDEN, "g6_silu_gate.npz"))
     y = silu_gate(lib, "orc", g6["gate"], g6["up"])
     bad += int(not np.array_equal(y.view(np.uint32), g6["y"].view(np.uint32)))
+    g7 = np.load(os.path.join(GOLDEN, "g7_ops.npz"))
+    h = int(g7["heads"])
+    for got, want in ((gelu(lib, "orc", g7["x"], 0), g7["gelu_exact"]), (gelu(lib, "orc", g7["x"], 1), g7["gelu_tanh"]),
+                      (bias(lib, "orc", g7["x"], g7["b"]), g7["bias"]), (add(lib, "orc", g7["x"], g7["y"]), g7["add"]),
+                      (rope(lib, "orc", g7["x"], h, g7["cos"], g7["sin"], 0), g7["rope_split"]),
+                      (rope(lib, "orc", g7["x"], h, g7["cos"], g7["sin"], 1), g7["rope_interleaved"])):
+        bad += int(not np.array_equal(got.view(np.uint32), want.view(np.uint32)))
     return bad
 
 
