@@ -118,7 +118,8 @@ def bench_fused(sess, synth, _lib, Q5_K, Q8_0, reps):
       norm    RMS norm + weight + modulation of X[4608, 3840] -> Q8_K (QKV / FFN-in)
       gate    SiLU(G) * U of [4608, 10240] -> Q8_0 (FFN-down input)
     Algorithmic bytes: fp32 inputs read once, planar activations written once
-    (Q8_K 1 + 1/64 + 1/8 B per value, Q8_0 1 + 1/8)."""
+    (Q8_K 1 + 1/64 + 1/8 B per value, Q8_0 1 + 1/8).  Also two of the
+    elementwise ops around the linears, in place: RoPE and the residual add."""
     m = 4608
     out = {}
 
@@ -162,8 +163,24 @@ def bench_fused(sess, synth, _lib, Q5_K, Q8_0, reps):
                              "unfused_us": round(sep_ms * 1e3, 2), "bytes": int(alg)}
     for b in (gb, ub, yb):
         b.free()
+
+    # Elementwise ops at the DiT block's attention shapes: RoPE on Q [4608, 3840]
+    # (30 heads of 128) and the residual add [4608, 3840]; bytes = read + write.
+    k = 3840
+    qb = sess.to_device(synth.normal(synth.SEED_ACTIVATIONS, (m, k)))
+    rb = sess.to_device(synth.normal(synth.SEED_WEIGHTS, (m, k)))
+    th = (synth.normal(synth.SEED_OUTLIERS, (m, 64)) * 3.0).astype(np.float64)
+    cb, sb = sess.to_device(np.cos(th).astype(np.float32)), sess.to_device(np.sin(th).astype(np.float32))
+    rope_ms = timed(lambda: _lib.check(sess.rope(qb.ptr, m, k, 30, cb.ptr, sb.ptr, 0), "rope"))
+    add_ms = timed(lambda: _lib.check(sess.pointwise(4, qb.ptr, rb.ptr, m, k), "add"))
+    for name, ms, nbytes, what in (("rope", rope_ms, m * k * 8 + m * 64 * 8, f"RoPE, Q[{m},{k}], 30 heads of 128"),
+                                   ("add", add_ms, m * k * 12, f"residual add [{m},{k}]")):
+        out[name] = {"workload": what, "us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": int(nbytes)}
+    for b in (qb, rb, cb, sb):
+        b.free()
     for name, v in out.items():
-        log(f"fused {name}: {v['us']} us ({v['gbs']} GB/s); unfused {v['unfused_us']} us")
+        log(f"{name}: {v['us']} us ({v['gbs']} GB/s)" + (f"; unfused {v['unfused_us']} us" if "unfused_us" in v else ""))
     return out
 
 

@@ -169,6 +169,18 @@ bool hip_silu_gate_multiply(uint32_t type, pixhip_weight* down, const float* gat
     return multiply_into(s,down,rows,n,output);
 }
 
+bool hip_pointwise(unsigned operation, float* destination, const float* second, size_t rows, size_t channels)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_pointwise(s,operation,destination,second,rows,channels) == PIXHIP_OK;
+}
+
+bool hip_rope(float* tensor, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, bool interleaved)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_rope(s,tensor,rows,channels,heads,cosine,sine,interleaved? 1 : 0) == PIXHIP_OK;
+}
+
 bool hip_available(std::string &description)
 {
     HipSession session;

@@ -137,6 +137,13 @@ bool hip_norm_multiply(uint32_t type, pixhip_weight* const* weights, float* cons
 bool hip_silu_gate_multiply(uint32_t type, pixhip_weight* down, const float* gate, const float* up, size_t rows, size_t channels,
                             float* output, float* gated);
 
+// vulkan_pointwise(operation, destination, second, nullptr) and vulkan_bias
+// (src/backend_vulkan.h:142, :150) for PIXHIP_OP_SILU / GATE / ADD / BIAS /
+// GELU_EXACT / GELU_TANH, and vulkan_rope (:145), on the active session's
+// stream: in place on `destination` [rows][channels].
+bool hip_pointwise(unsigned operation, float* destination, const float* second, size_t rows, size_t channels);
+bool hip_rope(float* tensor, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, bool interleaved);
+
 bool hip_available(std::string &description);
 
 #endif /* PIXELINA_BACKEND_HIP_H */

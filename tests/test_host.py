@@ -56,7 +56,7 @@ def test_cpp_shim_is_linked(lib):
     assert os.path.exists(shim_check), "the shim driver is built with the library"
     out = subprocess.run(["nm", "-DC", "--defined-only", _lib.LIBRARY], capture_output=True, text=True, check=True).stdout
     for sym in ("HipSession::initialize(int)", "hip_active_state()", "hip_synchronize()", "hip_matmul_weight(",
-                "hip_allocate(", "hip_free(", "hip_norm_multiply(", "hip_silu_gate_multiply("):
+                "hip_allocate(", "hip_free(", "hip_norm_multiply(", "hip_silu_gate_multiply(", "hip_pointwise(", "hip_rope("):
         assert sym in out, sym
 
 
