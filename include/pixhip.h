@@ -174,7 +174,8 @@ int pixhip_quantize_q8_K(pixhip_session* session, const float* input, void* bloc
  * and quantizes y for them as pixhip_matmul would (Q8_0 for 8, Q8_K else) into
  * the session's activations: follow with pixhip_matmul_stage(...,
  * PIXHIP_STAGE_MULTIPLY) for each consumer of that type and inner size.
- * type 0 only normalizes.  Optional outputs (NULL to skip): `normalized` fp32
+ * type 0 only normalizes (then `inner` need only be a multiple of 4; else of
+ * the block size, 256 or 32).  Optional outputs (NULL to skip): `normalized` fp32
  * [rows][inner] (the tensor the reference returns), `blocks` the reference's
  * block layout (block_q8_0 / block_q8_K, as pixhip_quantize_q8_0 / _q8_K).
  * Device pointers; input, norm_weight, modulation and normalized 16-byte

@@ -813,7 +813,8 @@ int fused_setup(pixhip_session* s, uint32_t type, size_t rows, size_t inner, flo
 {
     if (type && !supported_type(type)) return fail(PIXHIP_ERR_UNSUPPORTED,"unsupported weight type " + std::to_string(type));
     *kind = !type? 0 : (type == PIX_Q8_0? 2 : 1);
-    const size_t block = *kind == 1? PIX_QK : PIX_QK8;
+    // quantized: whole blocks; fp32 only: whole float4 loads
+    const size_t block = *kind == 1? PIX_QK : (*kind == 2? PIX_QK8 : 4);
     if (!rows || !inner || inner % block || inner > INT32_MAX || rows > INT32_MAX)
         return fail(PIXHIP_ERR_ARGUMENT,"rows must be positive and inner a positive multiple of " + std::to_string(block));
     if (!*kind && !result) return fail(PIXHIP_ERR_ARGUMENT,"nothing to write: no type and no fp32 output");

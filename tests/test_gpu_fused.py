@@ -136,14 +136,17 @@ def test_norm_quantize_multiply_vs_oracle(sess, wtype, rows, k, centered, weight
     assert err <= TOL
 
 
-def test_norm_type0_normalizes_only(sess):
-    rng = np.random.default_rng(3)
-    x = rng.standard_normal((4, 512)).astype(np.float32)
-    y, blocks = run_norm(sess, 0, x)
+@pytest.mark.parametrize("k,centered", [(512, 0), (100, 1), (4100, 0)])
+def test_norm_type0_normalizes_only(sess, k, centered):
+    """tensor_norm alone (vulkan_norm), any width that is a multiple of 4."""
+    rng = np.random.default_rng(3 + k)
+    x = (rng.standard_normal((5, k)) + centered).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    y, blocks = run_norm(sess, 0, x, w, 1e-6, centered)
     assert blocks is None
-    assert np.array_equal(bits(y), bits(norm_rows(oracle(), "orc", x, None, 1e-5, 0)))
+    assert np.array_equal(bits(y), bits(norm_rows(oracle(), "orc", x, w, 1e-6, centered)))
     xb = sess.to_device(x)
-    assert sess.norm_quantize(0, xb.ptr, 4, 512) == _lib.ERR_ARGUMENT  # nothing to write
+    assert sess.norm_quantize(0, xb.ptr, 5, k) == _lib.ERR_ARGUMENT  # nothing to write
 
 
 def test_multiply_after_norm_checks_the_activation_kind(sess):
