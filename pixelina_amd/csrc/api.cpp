@@ -67,9 +67,9 @@ struct pixhip_weight {
     std::string key;
     uint32_t type = 0;
     uint64_t inner = 0, rows = 0, gguf_bytes = 0;
-    void* raw = nullptr;        // GGUF bytes (Q5_K matvec input; source of the other forms)
-    void* planes = nullptr;     // Q5_K / Q6_K GEMM planes
-    void* planar = nullptr;     // Q8_0 planar (GEMM + matvec) or Q5_K / Q6_K planar (matvec)
+    void* raw = nullptr;        // GGUF bytes (the source of the other forms)
+    void* planes = nullptr;     // GEMM form (built on first GEMM use)
+    void* planar = nullptr;     // matvec form (built on first matvec use)
     pixhip::PlanesQ5K q5{};
     pixhip::PlanesQ6K q6{};
     pixhip::PlanarQ80 q80{};

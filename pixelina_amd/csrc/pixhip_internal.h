@@ -23,9 +23,11 @@
 //     dm   fp32   [K/256][Npad]     super-block dmin
 //     mn   fp16   [K/256][Npad][8]  the eight six-bit sub-block minima
 //   weights Q6_K for the GEMM: hi/lo of scale*(q-32) = 64*hi + lo, d fp32 [K/256][Npad]
-//   weights Q8_0 ("planar", GEMM and matvec), rows of Kp with a zero pad block:
-//     qs int8 [Npad][Kp], d fp16 [N][Kp/32], and for the GEMM the same scales
-//     widened and transposed, dT fp32 [Kp/32][Npad]
+//   weights Q8_0 for the GEMM, rows of Kp with a zero pad block: qs int8
+//     [Npad][Kp], and the scales widened and transposed, dT fp32 [Kp/32][Npad]
+//   weights Q8_0 for the matvec: qs_mv int8 [N][4][Kp/64][16] (each row
+//     piece-major: 16-byte piece p of 64-value unit u at (p*Kp/64 + u)*16),
+//     d fp16 [N][Kp/32]
 //   weights Q5_K for the matvec ("q5 planar"): per row, the GGUF nibble bytes of
 //     unit u (64 values, u = 4b + j covers sub-blocks 2j, 2j+1 of super-block b)
 //     split into two half planes, qs u8 [N][2][K/64][16] (half 0: the unit's
@@ -35,9 +37,11 @@
 //                    4w..4w+3, ((qh >> 2j) & 0x03030303) << 2*(qword & 3)
 //       bytes 8..11  scale_2j, scale_2j+1, min_2j, min_2j+1 (six-bit values as bytes)
 //       bytes 12..15 d, dmin (fp16 bits, as in the block)
-//   weights Q6_K for the matvec ("q6 planar"): ql u8 [N][K/2], qh u8 [N][K/4],
-//     sc int8 [N][K/16], d fp16 [N][K/256] -- same bytes as GGUF, re-sliced so every
-//     plane is 16-B aligned (210-B blocks are only 2-B aligned).
+//   weights Q6_K for the matvec ("q6 planar"): ql u8 [N][2][K/64][16] (each
+//     64-value unit's first and second 16-byte piece of GGUF ql bytes, in two
+//     unit-major planes), qh u8 [N][K/4], sc int8 [N][K/16], d fp16 [N][K/256]
+//     -- the GGUF bytes re-sliced so every plane is 16-B aligned (210-B blocks
+//     are only 2-B aligned) and every matvec load is lane-contiguous.
 #pragma once
 
 #include <hip/hip_runtime.h>

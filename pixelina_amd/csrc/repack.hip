@@ -127,9 +127,10 @@ __global__ __launch_bounds__(256) void repack_q6_K_planar_kernel(const uint8_t* 
     if (lane == 0) d[row * nb + b] = __builtin_bit_cast(_Float16,(uint16_t)(src[208] | (src[209] << 8)));
 }
 
-// Q8_0: 34-byte blocks (2-byte aligned) -> int8 plane + fp16 scale plane with
-// row stride kpad (the caller zero-fills the padding once at allocation).
-// One 8-lane group per block, 4 values per lane.
+// Q8_0: 34-byte blocks (2-byte aligned) -> the GEMM form (int8 plane, fp32
+// transposed scales) and/or the matvec form (piece-major int8 rows, fp16
+// scales), both with row stride kpad (the caller zero-fills the padding once
+// at allocation).  One 8-lane group per block, 4 values per lane.
 // Block b of a row holds values 32b..32b+31: unit b/2, 16-byte pieces
 // 2(b%2) and 2(b%2)+1 of it.  The matvec form stores piece p of unit u at
 // (p*units + u)*16 in the row, so that a load of piece p by 64 lanes reading
