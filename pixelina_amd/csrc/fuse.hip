@@ -26,8 +26,8 @@ constexpr int kNormWaves = 4;
 constexpr size_t kStageMaxK = 4096;  // norm vectors staged in LDS up to this row length (32 KB)
 constexpr int kGateWaves = 8;
 // Rows per workgroup in the SiLU * gate producer.  On [4608, 10240] -> Q8_0:
-// 92 us with 16 or 32 rows, 99 with one row's 8 chunks per workgroup, 186
-// with 64 (two waves per SIMD for the 16 loads per lane).
+// 92 us with 16 or 32 rows, 99 with 8 rows or with one row's 8 chunks per
+// workgroup, 186 with 64 (two waves per SIMD for the 16 loads per lane).
 constexpr int kGateRows = 16;
 
 struct FuseArgs {

@@ -20,8 +20,8 @@ constexpr int kQuantWaves = 8;  // waves per workgroup: 8 measured ~12% faster t
 // kQuantRows consecutive rows (wave w: rows w, w + kQuantWaves, ...), so each
 // block's transposed scales dT[b * mpad + row] leave it as 64-byte runs rather
 // than as 4-byte pieces from workgroups spread over the XCDs.  On [4608, 10240]:
-// 38.4 us with 16 rows, 39.5 with 32, 38.5 with 64, 45.7 with one row's 8
-// consecutive chunks per workgroup.
+// 38.4 us with 16 rows, 40.5 with 8, 39.5 with 32, 38.5 with 64, 45.7 with one
+// row's 8 consecutive chunks per workgroup.
 constexpr int kQuantRows = 16;
 constexpr int kQuantPer = kQuantRows / kQuantWaves;  // rows per wave
 // Q8_K writes one scale per 256 values, so a long grid matters more than its
