@@ -18,6 +18,7 @@ SOURCES = [
     "csrc/quantize.hip",
     "csrc/repack.hip",
     "csrc/gemm.hip",
+    "csrc/gemm_kq.hip",
     "csrc/matvec.hip",
     "csrc/fuse.hip",
     "csrc/ops.hip",
@@ -60,10 +61,43 @@ def _compile(src):
     return obj
 
 
+# Kernels whose s_waitcnt vmcnt accounting counts only their own DMAs: a
+# register spill would add scratch traffic to that counter and break it, so the
+# build fails if the compiler spills any (the integer-sum debug variants drain
+# the counter completely and are exempt).
+NO_SPILL = {"csrc/gemm_kq.hip": ("gemm_kq_kernelILb1ELb0E", "gemm_kq_kernelILb0ELb0E")}
+
+
+def _check_no_spill(src, kernels):
+    path = os.path.join(HERE, src)
+    out = os.path.join(OBJDIR, os.path.basename(src) + ".s")
+    cmd = [_hipcc(), *FLAGS, "--cuda-device-only", "-S", path, "-o", out]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src}:\n{proc.stderr}")
+    name, spills = None, {}
+    with open(out) as f:
+        for line in f:
+            line = line.strip()
+            if line.startswith(".name:"):
+                name = line.split()[-1]
+            elif line.startswith(".vgpr_spill_count:") and name:
+                spills[name] = int(line.split()[-1])
+    for k in kernels:
+        hits = [v for n, v in spills.items() if k in n]
+        if not hits:
+            raise RuntimeError(f"{src}: kernel {k} not found in the device assembly")
+        if max(hits) > 0:
+            raise RuntimeError(f"{src}: kernel {k} spills {max(hits)} VGPRs (its vmcnt waits assume no scratch traffic)")
+
+
 def build(verbose=False):
     os.makedirs(OBJDIR, exist_ok=True)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as pool:
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(len(SOURCES) + len(NO_SPILL), os.cpu_count() or 4)) as pool:
+        checks = [pool.submit(_check_no_spill, src, ks) for src, ks in NO_SPILL.items() if src in SOURCES]
         objs = list(pool.map(_compile, SOURCES))
+        for c in checks:
+            c.result()
     tmp = LIBRARY + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)

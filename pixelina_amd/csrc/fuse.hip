@@ -75,10 +75,10 @@ __device__ __forceinline__ void store_chunk(const FuseArgs& a, size_t row, int c
         quantize_q8_K_wave(v,lane,packed,d,gsum);
         const size_t nb = K / PIX_QK;
         if (a.qs) {
-            reinterpret_cast<uint32_t*>(a.qs + row * K + (size_t)c * PIX_QK)[lane] = packed;
+            *reinterpret_cast<uint32_t*>(a.qs + tiled_offset(row,(size_t)c * PIX_QK + 4 * lane,K)) = packed;
             if (lane == 0) a.d[(size_t)c * a.mpad + row] = d;
             const int t = lane >> 2;  // 16-value group, stored even groups first
-            if ((lane & 3) == 0) a.bs[row * (K / 16) + (size_t)c * 16 + (t & 1) * 8 + (t >> 1)] = (_Float16)(float)gsum;
+            if ((lane & 3) == 0) a.bs[tiled_bs_index(row,(size_t)c,(t & 1) * 8 + (t >> 1),K)] = (_Float16)(float)gsum;
         }
         if (a.blocks) {
             uint8_t* blk = a.blocks + (row * nb + c) * PIX_Q8_K_BYTES;

@@ -632,7 +632,7 @@ static int device_cus()
 // CUs/tiles-in-the-round pieces, run by separate workgroups.  Returns the
 // number of pieces (1: no split) and sets the whole tiles and the piece
 // length in stages.
-static int split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_chunks)
+int gemm_split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_chunks)
 {
     const size_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
     const int chunks = (int)(K / kKC), groups = chunks / kSBC;
@@ -652,7 +652,7 @@ static int split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_
 size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages)
 {
     int full, chunks;
-    const int splits = split_plan(M,N,K_stages,full,chunks);
+    const int splits = gemm_split_plan(M,N,K_stages,full,chunks);
     const size_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
     return splits > 1? (size_t)splits * (tiles - full) * (kBM * kBN) * sizeof(float) : 0;
 }
@@ -672,7 +672,7 @@ static hipError_t launch(GemmArgs g, size_t mpad, size_t npad, hipStream_t s)
     g.Npad = (int)npad;
     const int ntiles = g.tiles_m * g.tiles_n;
     if (!ntiles) return hipSuccess;
-    g.splits = SUMS? 1 : split_plan((size_t)g.M,(size_t)g.N,(size_t)g.K,g.full_tiles,g.split_chunks);
+    g.splits = SUMS? 1 : gemm_split_plan((size_t)g.M,(size_t)g.N,(size_t)g.K,g.full_tiles,g.split_chunks);
     if (g.splits == 1 || !g.part) {  // unsplit (or no workspace)
         g.splits = 1;
         g.full_tiles = ntiles;
@@ -696,28 +696,6 @@ static GemmArgs base_args(size_t M, size_t N, size_t K)
     return g;
 }
 
-hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
-                            hipStream_t s)
-{
-    GemmArgs g = base_args(M,N,K);
-    g.part = part;
-    g.xq = a.qs; g.xdT = a.d; g.xbs = a.bs;
-    g.whi = w.hi; g.wlo = w.lo; g.wdT = w.d; g.wdm = w.dm; g.wmn = w.mn;
-    g.y = out.y; g.bias = out.bias; g.ldy = out.ldy; g.yoff = out.offset;
-    return launch<KIND_Q5K,false>(g,a.mpad,w.npad,s);
-}
-
-hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
-                            hipStream_t s)
-{
-    GemmArgs g = base_args(M,N,K);
-    g.part = part;
-    g.xq = a.qs; g.xdT = a.d;
-    g.whi = w.hi; g.wlo = w.lo; g.wdT = w.d;
-    g.y = out.y; g.bias = out.bias; g.ldy = out.ldy; g.yoff = out.offset;
-    return launch<KIND_Q6K,false>(g,a.mpad,w.npad,s);
-}
-
 hipError_t launch_gemm_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, const Output& out, float* part,
                             hipStream_t s)
 {
@@ -727,25 +705,6 @@ hipError_t launch_gemm_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t
     g.whi = w.qs; g.wdT = w.dT;
     g.y = out.y; g.bias = out.bias; g.ldy = out.ldy; g.yoff = out.offset;
     return launch<KIND_Q80,false>(g,a.mpad,round_up(N,kBN),s);
-}
-
-hipError_t launch_sums_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, int32_t* scaled, int32_t* mins,
-                            hipStream_t s)
-{
-    GemmArgs g = base_args(M,N,K);
-    g.xq = a.qs; g.xdT = a.d; g.xbs = a.bs;
-    g.whi = w.hi; g.wlo = w.lo; g.wdT = w.d; g.wdm = w.dm; g.wmn = w.mn;
-    g.sums = scaled; g.mins = mins;
-    return launch<KIND_Q5K,true>(g,a.mpad,w.npad,s);
-}
-
-hipError_t launch_sums_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s)
-{
-    GemmArgs g = base_args(M,N,K);
-    g.xq = a.qs; g.xdT = a.d;
-    g.whi = w.hi; g.wlo = w.lo; g.wdT = w.d;
-    g.sums = sums;
-    return launch<KIND_Q6K,true>(g,a.mpad,w.npad,s);
 }
 
 hipError_t launch_sums_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s)

@@ -6,23 +6,25 @@
 // the cache is internal to the backend (src/backend_vulkan.cpp:742-758).
 //
 //   activations, Q8_K ("act8k"), M rows of K values:
-//     qs   int8   [M][K]          quantized values
+//     qs   int8   tiled [Mpad/16][K/64][16][64]: value (m, k) at tiled_offset(m, k, K),
+//                 so the 16 rows x 64 values of one GEMM stage are one contiguous 1 KB
 //     d    fp32   [K/256][Mpad]   block scale, super-block-major
-//     bs   fp16   [M][K/16]       sums of 16 quantized values (exact, |s| <= 2032),
-//                                 within each super-block in the order 0,2,..,14,1,3,..,15
-//                                 (even groups, then odd: the min-term MFMA operand order)
+//     bs   fp16   tiled [Mpad/32][K/256][32][16]: the sums of 16 quantized values
+//                 (exact, |s| <= 2032) of 32 rows and one super-block are one 1 KB
+//                 block; within a row the order is 0,2,..,14,1,3,..,15 (even groups,
+//                 then odd: the min-term MFMA operand order)
 //   activations, Q8_0 ("act80"), rows of Kp = K rounded up to 64 (a zero pad block):
 //     qs   int8   [M][Kp]
 //     d    fp32   [Kp/32][Mpad]   fp16-rounded block scale widened to fp32
 //   Activations are allocated with Mpad rows (multiple of PIX_GEMM_MTILE) and
 //   GEMM weight forms with Npad rows (multiple of PIX_GEMM_NTILE).
 //   weights Q5_K for the GEMM ("planes"), N rows padded to Npad:
-//     hi   int8   [Npad][K]         (scale_s * q) >> 6
-//     lo   int8   [Npad][K]         (scale_s * q) & 63
+//     hi   int8   tiled [Npad/16][K/64][16][64]   (scale_s * q) >> 6
+//     lo   int8   tiled, as hi                    (scale_s * q) & 63
 //     d    fp32   [K/256][Npad]     super-block scale d
 //     dm   fp32   [K/256][Npad]     super-block dmin
 //     mn   fp16   [K/256][Npad][8]  the eight six-bit sub-block minima
-//   weights Q6_K for the GEMM: hi/lo of scale*(q-32) = 64*hi + lo, d fp32 [K/256][Npad]
+//   weights Q6_K for the GEMM: hi/lo of scale*(q-32) = 64*hi + lo (tiled as Q5_K), d fp32 [K/256][Npad]
 //   weights Q8_0 for the GEMM, rows of Kp with a zero pad block: qs int8
 //     [Npad][Kp], and the scales widened and transposed, dT fp32 [Kp/32][Npad]
 //   weights Q8_0 for the matvec: qs_mv int8 [N][4][Kp/64][16] (each row
@@ -62,10 +64,26 @@
 
 namespace pixhip {
 
+// Byte offset of value (row, k) in a tiled plane of K values per row: rows in
+// groups of 16, each group's K bytes cut into 64-byte pieces, and the piece of
+// a group for values 64s..64s+63 is one contiguous 1 KB block (16 rows x 64).
+// The GEMM fetches one such block per DMA instruction: whole 128-byte lines,
+// where a row-major plane would give it 16 half lines.
+__host__ __device__ inline size_t tiled_offset(size_t row, size_t k, size_t K)
+{
+    return ((row >> 4) * (K >> 6) + (k >> 6)) * 1024 + (row & 15) * 64 + (k & 63);
+}
+// Element index of the 16-value sum j (0..15, even groups first) of super-block
+// b of row `row` in the tiled bs plane.
+__host__ __device__ inline size_t tiled_bs_index(size_t row, size_t b, int j, size_t K)
+{
+    return (((row >> 5) * (K >> 8) + b) * 32 + (row & 31)) * 16 + (size_t)j;
+}
+
 struct Act8K {
-    int8_t* qs;       // [mpad][K]
+    int8_t* qs;       // tiled [mpad/16][K/64][16][64]
     float* d;         // [K/256][mpad]
-    _Float16* bs;     // [mpad][K/16]
+    _Float16* bs;     // tiled [mpad/32][K/256][32][16]
     size_t mpad;      // rows allocated (multiple of the GEMM tile)
 };
 
@@ -162,6 +180,9 @@ hipError_t launch_repack_q8_0(const uint8_t* raw, size_t rows, size_t inner, siz
 // to 64: the stage length) uses; 0 when it runs unsplit.  The launchers take
 // a workspace of at least that size, or null to run unsplit.
 size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages);
+// The split of a GEMM grid: number of K pieces of the last round's tiles (1:
+// none), the whole tiles before them and the piece length in 64-value stages.
+int gemm_split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_chunks);
 hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
                             hipStream_t s);
 hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, float* part,

@@ -52,11 +52,11 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_K_kernel(const f
         int gsum;
         quantize_q8_K_wave(v[i],lane,packed,d,gsum);
         if (qs) {
-            reinterpret_cast<uint32_t*>(qs + row * inner + (size_t)b * PIX_QK)[lane] = packed;
+            *reinterpret_cast<uint32_t*>(qs + tiled_offset(row,(size_t)b * PIX_QK + 4 * lane,inner)) = packed;
             if (lane == 0) dT[(size_t)b * mpad + row] = d;
             // group t = lane/4 stored at (t&1)*8 + t/2: even groups first, then odd
             const int t = lane >> 2;
-            if ((lane & 3) == 0) bs[row * (inner / 16) + (size_t)b * 16 + (t & 1) * 8 + (t >> 1)] = (_Float16)(float)gsum;
+            if ((lane & 3) == 0) bs[tiled_bs_index(row,b,(t & 1) * 8 + (t >> 1),inner)] = (_Float16)(float)gsum;
         }
         if (blocks) {
             uint8_t* blk = blocks + (row * nb + b) * PIX_Q8_K_BYTES;

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void repack_q5_K_kernel(const uint8_t* __restr
         h[k] = p >> 6;
         l[k] = p & 63;
     }
-    const size_t off = row * inner + b * PIX_QK + 4 * lane;
+    const size_t off = tiled_offset(row,b * PIX_QK + 4 * lane,inner);
     *reinterpret_cast<uint32_t*>(hi + off) = pack_bytes(h[0],h[1],h[2],h[3]);
     *reinterpret_cast<uint32_t*>(lo + off) = pack_bytes(l[0],l[1],l[2],l[3]);
     if (lane == 0) {
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void repack_q6_K_planes_kernel(const uint8_t* 
         h[k] = p >> 6;
         l[k] = p & 63;
     }
-    const size_t off = row * inner + b * PIX_QK + 4 * lane;
+    const size_t off = tiled_offset(row,b * PIX_QK + 4 * lane,inner);
     *reinterpret_cast<uint32_t*>(hi + off) = pack_bytes(h[0],h[1],h[2],h[3]);
     *reinterpret_cast<uint32_t*>(lo + off) = pack_bytes(l[0],l[1],l[2],l[3]);
     if (lane == 0) d[b * npad + row] = half_bits_to_float((uint16_t)(src[208] | (src[209] << 8)));
