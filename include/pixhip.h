@@ -31,7 +31,7 @@ extern "C" {
 #define PIXHIP_ERR_UNSUPPORTED (-2) /* weight type other than Q8_0 / Q5_K / Q6_K */
 #define PIXHIP_ERR_MEMORY (-3)      /* device allocation failed or exceeds the budget (src/backend_vulkan.cpp:689, :718-720) */
 #define PIXHIP_ERR_DEVICE (-4)      /* HIP runtime failure: no device, launch or synchronisation error */
-#define PIXHIP_ERR_STATE (-5)       /* missing session */
+#define PIXHIP_ERR_STATE (-5)       /* missing session, MULTIPLY without matching activations, or an evicted weight without host bytes */
 
 #define PIXHIP_TYPE_Q8_0 8
 #define PIXHIP_TYPE_Q5_K 13
@@ -101,14 +101,25 @@ int pixhip_copy_device(pixhip_session* session, void* device_dst, const void* de
 
 /* Looks `key` up in the session's LRU weight cache (the reference keys it
  * "file:name:offset:bytes"); on a miss copies `bytes` host bytes of GGUF
- * blocks [rows][inner] of `type` to the device and converts them into the
- * resident layouts the kernels read.  The handle stays valid until the entry
- * is evicted (pixhip_prepare_stage, budget pressure) or the session ends. */
+ * blocks [rows][inner] of `type` to the device.  On first use by the GEMM
+ * (columns > 1) or the matvec (columns == 1) the kernel's resident layout is
+ * built from them and the device copy of the GGUF bytes is released.  The
+ * handle stays valid until the session ends: eviction (budget pressure,
+ * pixhip_prepare_stage) frees only the device memory, and the next call that
+ * needs a layout rebuilds it from `host_bytes`.  So `host_bytes` must stay
+ * readable while the handle is used, as the model file's mapping stays for
+ * the reference's cache (src/backend_vulkan.cpp:742-758); a later call with
+ * the same key may pass a new address of the same bytes. */
 int pixhip_weight_get(pixhip_session* session, const char* key, const void* host_bytes, uint64_t bytes, uint32_t type,
                       uint64_t inner, uint64_t rows, pixhip_weight** out);
 
-/* Number of cached weights and their resident bytes. */
+/* Number of cached weights with device memory and their resident bytes. */
 int pixhip_weight_cache_info(pixhip_session* session, uint64_t* entries, uint64_t* bytes);
+
+/* No Vulkan counterpart (residency report): the GGUF bytes of the weights
+ * that hold device memory and the device bytes they hold (the Q5_K GEMM
+ * layout is about 3.05x its GGUF bytes, the matvec layout 1.09x). */
+int pixhip_weight_residency(pixhip_session* session, uint64_t* gguf_bytes, uint64_t* resident_bytes);
 
 /* The type and shape a handle was created with (PixWeight::type and shape
  * {inner, rows}, src/model.h:33-39). */
@@ -144,9 +155,10 @@ int pixhip_matmul_stage(pixhip_session* session, const pixhip_weight* weight, co
                         const float* bias, size_t ldy, size_t y_offset, unsigned stages);
 
 /* cpu_quant_matmul (src/kernels_quant.cpp:369-412) with the same argument
- * meaning: host GGUF weight bytes (cached on the device keyed by their
- * address, size, type and shape), input [columns][inner], output
- * [columns][rows].  Same failures: unsupported type, a zero size,
+ * meaning: host GGUF weight bytes, input [columns][inner], output
+ * [columns][rows].  Stateless like the reference: the weight is uploaded and
+ * converted for this call only (nothing is cached) and the call completes
+ * before returning.  Same failures: unsupported type, a zero size,
  * inner % block != 0 or inner > INT32_MAX give an error and touch nothing. */
 int pixhip_quant_matmul(pixhip_session* session, const unsigned char* weights, uint32_t type, const float* input, float* output,
                         size_t rows, size_t columns, size_t inner);
@@ -208,7 +220,10 @@ int pixhip_silu_gate_quantize(pixhip_session* session, uint32_t type, const floa
  * fp32 arithmetic of the CPU op named above, in its order.  `second` is
  * [rows][channels] for GATE and ADD, [channels] for BIAS, unused (NULL) for
  * SILU and GELU.  expf / erff / tanhf are correctly rounded here (glibc's are
- * within about an ulp).  Device pointers, 4-byte aligned. */
+ * within about an ulp).  `destination` is device memory or pinned host
+ * memory (HipAllocator, PixTensorVals); `second` may also be pageable host
+ * memory (a std::vector, as tensor_bias passes), which is staged to the device
+ * first.  4-byte aligned. */
 int pixhip_pointwise(pixhip_session* session, unsigned operation, float* destination, const float* second, size_t rows,
                      size_t channels);
 
@@ -216,7 +231,9 @@ int pixhip_pointwise(pixhip_session* session, unsigned operation, float* destina
  * in place on `tensor` [rows][heads * dim]; for each head and pair i < dim/2,
  * (first, second) = (2i, 2i+1) when `interleaved`, else (i, i + dim/2), and
  * (a, b) -> (a*c - b*s, a*s + b*c) with c, s = cosine, sine [rows][dim/2][i],
- * in fp32 without contraction (bit-exact).  Device pointers. */
+ * in fp32 without contraction (bit-exact).  `tensor` is device memory or
+ * pinned host memory; `cosine` and `sine` may also be pageable host memory
+ * (tensor_rope's std::vector tables), staged to the device first. */
 int pixhip_rope(pixhip_session* session, float* tensor, size_t rows, size_t channels, size_t heads, const float* cosine,
                 const float* sine, int interleaved);
 

@@ -34,6 +34,8 @@
  *  10 SiLU as v * (1 / (1 + e)) instead of a division
  *  11 RoPE with the sine's sign flipped
  *  12 tanh GELU with v*v instead of v*v*v
+ *  13 modulation as x + x*scale instead of x*(1 + scale)
+ *  14 modulation by scale instead of 1 + scale
  */
 #ifndef ORC_MUTANT
 #define ORC_MUTANT 0
@@ -521,7 +523,16 @@ void orc_norm_rows(const float* x, size_t rows, size_t channels, const float* we
 void orc_modulate_rows(float* x, size_t rows, size_t channels, const float* scale)
 {
     for (size_t r = 0; r < rows; r++)
-        for (size_t c = 0; c < channels; c++) x[r * channels + c] = x[r * channels + c] * (1.0f + scale[c]);
+        for (size_t c = 0; c < channels; c++) {
+            const float v = x[r * channels + c];
+#if ORC_MUTANT == 13
+            x[r * channels + c] = v + v * scale[c];
+#elif ORC_MUTANT == 14
+            x[r * channels + c] = v * scale[c];
+#else
+            x[r * channels + c] = v * (1.0f + scale[c]);
+#endif
+        }
 }
 
 /* tensor_silu, src/tensor.cpp:199-209 (value /= 1.0f + expf(-value)), then

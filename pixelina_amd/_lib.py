@@ -49,6 +49,7 @@ SIGNATURES = {
     "pixhip_copy_device": (_int, [_vp, _vp, _vp, _sz]),
     "pixhip_weight_get": (_int, [_vp, ctypes.c_char_p, _vp, _u64, _u32, _u64, _u64, ctypes.POINTER(_vp)]),
     "pixhip_weight_cache_info": (_int, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "pixhip_weight_residency": (_int, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "pixhip_weight_shape": (_int, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "pixhip_matmul": (_int, [_vp, _vp, _vp, _sz, _vp]),
     "pixhip_matmul_ex": (_int, [_vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz]),

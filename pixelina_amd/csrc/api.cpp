@@ -63,11 +63,16 @@ struct Carver {
 
 }  // namespace
 
+// One cached weight.  The record lives until the session ends, so a handle
+// never dangles: eviction frees only its device memory, and the next use
+// rebuilds what it needs from the host bytes (as VulkanState::weight re-reads
+// the model file's mapping, src/backend_vulkan.cpp:742-758).
 struct pixhip_weight {
     std::string key;
     uint32_t type = 0;
     uint64_t inner = 0, rows = 0, gguf_bytes = 0;
-    void* raw = nullptr;        // GGUF bytes (the source of the other forms)
+    const void* host = nullptr; // the caller's GGUF bytes (re-read to rebuild a form)
+    void* raw = nullptr;        // device copy of the GGUF bytes, only while a form is built from it
     void* planes = nullptr;     // GEMM form (built on first GEMM use)
     void* planar = nullptr;     // matvec form (built on first matvec use)
     pixhip::PlanesQ5K q5{};
@@ -120,28 +125,35 @@ int use_device(pixhip_session* s)
     return PIXHIP_OK;
 }
 
-void release_weight(pixhip_session* s, pixhip_weight* w)
+// Frees a weight's device memory (the record and its handle stay valid).
+// Callers synchronise the stream first when queued work may still read it.
+void release_forms(pixhip_session* s, pixhip_weight* w)
 {
     if (w->raw) (void)hipFree(w->raw);
     if (w->planes) (void)hipFree(w->planes);
     if (w->planar) (void)hipFree(w->planar);
+    w->raw = w->planes = w->planar = nullptr;
+    w->q5 = {};
+    w->q6 = {};
+    w->q80 = {};
+    w->q5p = {};
+    w->q6p = {};
     s->cache_bytes -= w->resident;
-    delete w;
+    w->resident = 0;
 }
 
 // VulkanState::evict (src/backend_vulkan.cpp:671-681): least recently used first.
 bool evict_one(pixhip_session* s, const pixhip_weight* keep)
 {
-    auto victim = s->weights.end();
-    for (auto it = s->weights.begin(); it != s->weights.end(); ++it) {
-        if (it->second == keep) continue;
-        if (victim == s->weights.end() || it->second->used < victim->second->used) victim = it;
+    pixhip_weight* victim = nullptr;
+    for (auto& e : s->weights) {
+        pixhip_weight* w = e.second;
+        if (w == keep || !w->resident) continue;
+        if (!victim || w->used < victim->used) victim = w;
     }
-    if (victim == s->weights.end()) return false;
+    if (!victim) return false;
     (void)hipStreamSynchronize(s->stream);
-    pixhip_weight* w = victim->second;
-    s->weights.erase(victim);
-    release_weight(s,w);
+    release_forms(s,victim);
     return true;
 }
 
@@ -197,9 +209,40 @@ int grow(pixhip_session* s, void** buffer, size_t* have, size_t need)
     return PIXHIP_OK;
 }
 
-// GEMM forms, built on first use from the resident GGUF bytes.
+// A device copy of the GGUF bytes, for building a form.
+int ensure_raw(pixhip_session* s, pixhip_weight* w)
+{
+    if (w->raw) return PIXHIP_OK;
+    if (!w->host) return fail(PIXHIP_ERR_STATE,"weight " + w->key + " was evicted and has no host bytes to rebuild from");
+    int rc = weight_alloc(s,w,round_up(w->gguf_bytes,kAlign),&w->raw);
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync(w->raw,w->host,w->gguf_bytes,hipMemcpyHostToDevice,s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e,"weight upload");
+    return PIXHIP_OK;
+}
+
+// The device GGUF copy is released once a form has been built from it (the
+// forms are all the kernels read); another form needed later re-reads the host
+// bytes.
+int release_raw(pixhip_session* s, pixhip_weight* w)
+{
+    if (!w->raw) return PIXHIP_OK;
+    PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");  // the repack kernels read it
+    (void)hipFree(w->raw);
+    w->raw = nullptr;
+    const size_t bytes = round_up(w->gguf_bytes,kAlign);
+    w->resident -= bytes;
+    s->cache_bytes -= bytes;
+    return PIXHIP_OK;
+}
+
+// GEMM forms, built on first use from the GGUF bytes.
 int ensure_gemm_form(pixhip_session* s, pixhip_weight* w)
 {
+    if (w->planes) return PIXHIP_OK;
+    int rc0 = ensure_raw(s,w);
+    if (rc0) return rc0;
     const size_t N = w->rows, K = w->inner, npad = round_up(N,kTileN), nb = K / PIX_QK;
     if (w->type == PIX_Q5_K && !w->planes) {
         Carver c;
@@ -242,12 +285,22 @@ int ensure_gemm_form(pixhip_session* s, pixhip_weight* w)
                                                   const_cast<int8_t*>(w->q6.lo),const_cast<float*>(w->q6.d),s->stream),
                 "repack Q6_K planes");
     }
-    return PIXHIP_OK;
+    return release_raw(s,w);
 }
+
+int build_matvec_form(pixhip_session* s, pixhip_weight* w);
 
 int ensure_matvec_form(pixhip_session* s, pixhip_weight* w)
 {
     if (w->planar) return PIXHIP_OK;
+    int rc = ensure_raw(s,w);
+    if (!rc) rc = build_matvec_form(s,w);
+    if (!rc) rc = release_raw(s,w);
+    return rc;
+}
+
+int build_matvec_form(pixhip_session* s, pixhip_weight* w)
+{
     const size_t N = w->rows, K = w->inner, nb = K / PIX_QK;
     if (w->type == PIX_Q8_0) {
         const size_t kp = round_up(K,64);
@@ -323,6 +376,51 @@ bool device_visible(pixhip_session* s, const void* p, const void** dev)
         return true;
     }
     return false;
+}
+
+// A read-only operand of an elementwise op: device memory (ours, HIP device or
+// managed) and mapped pinned host memory are passed to the kernel as they
+// are; pageable host memory, which a kernel must not dereference, is copied to
+// a device block first (returned in *staged, freed by the caller after the
+// launch: the pool reuses it only for work queued after this op).
+int read_operand(pixhip_session* s, const void* p, size_t bytes, const void** dev, void** staged)
+{
+    *staged = nullptr;
+    if (device_visible(s,p,dev)) return PIXHIP_OK;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr,p) == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer) {
+        *dev = attr.devicePointer;
+        return PIXHIP_OK;
+    }
+    (void)hipGetLastError();
+    void* block = pixhip_allocate(s,bytes);
+    if (!block) return fail(PIXHIP_ERR_MEMORY,"staging of a host operand failed");
+    hipError_t e = hipMemcpyAsync(block,p,bytes,hipMemcpyHostToDevice,s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);  // the host buffer may change after return
+    if (e != hipSuccess) {
+        pixhip_free(s,block);
+        return hip_fail(e,"staging of a host operand");
+    }
+    *dev = block;
+    *staged = block;
+    return PIXHIP_OK;
+}
+
+// The in-place tensor of an elementwise op: device or mapped pinned memory only.
+int write_operand(pixhip_session* s, void* p, void** dev)
+{
+    const void* d = nullptr;
+    if (device_visible(s,p,&d)) {
+        *dev = const_cast<void*>(d);
+        return PIXHIP_OK;
+    }
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr,p) == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer) {
+        *dev = attr.devicePointer;
+        return PIXHIP_OK;
+    }
+    (void)hipGetLastError();
+    return fail(PIXHIP_ERR_ARGUMENT,"the tensor is pageable host memory: pass device memory (pixhip_allocate) or pinned host memory");
 }
 
 // Sizes the session's activation scratch for `columns` rows of K values of
@@ -536,7 +634,10 @@ void pixhip_session_destroy(pixhip_session* s)
     if (!s) return;
     (void)hipSetDevice(s->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
-    for (auto& e : s->weights) release_weight(s,e.second);
+    for (auto& e : s->weights) {
+        release_forms(s,e.second);
+        delete e.second;
+    }
     s->weights.clear();
     trim_pool(s);
     for (auto& e : s->live) (void)hipFree(reinterpret_cast<void*>(e.first));
@@ -587,8 +688,7 @@ int pixhip_prepare_stage(pixhip_session* s, uint64_t activation_bytes, uint64_t 
     if (activation_bytes > s->heap_limit || scratch_bytes > s->heap_limit - activation_bytes)
         return fail(PIXHIP_ERR_MEMORY,"stage does not fit the device heap");
     PIX_HIP(hipStreamSynchronize(s->stream),"hipStreamSynchronize");
-    for (auto& e : s->weights) release_weight(s,e.second);
-    s->weights.clear();
+    for (auto& e : s->weights) release_forms(s,e.second);  // handles stay valid; their forms are rebuilt on use
     trim_pool(s);
     size_t held = s->scratch_bytes + s->stage_bytes;
     for (auto& e : s->live) held += e.second;
@@ -700,6 +800,10 @@ int pixhip_weight_get(pixhip_session* s, const char* key, const void* host_bytes
     if (it != s->weights.end()) {
         pixhip_weight* w = it->second;
         if (w->type != type || w->inner != inner || w->rows != rows) return fail(PIXHIP_ERR_ARGUMENT,"cached key with another shape");
+        if (host_bytes) {
+            if (bytes < expect) return fail(PIXHIP_ERR_ARGUMENT,"weight bytes shorter than rows*row_bytes");
+            w->host = host_bytes;  // the caller's current mapping of the same bytes
+        }
         w->used = ++s->uses;
         *out = w;
         return PIXHIP_OK;
@@ -712,15 +816,13 @@ int pixhip_weight_get(pixhip_session* s, const char* key, const void* host_bytes
     w->inner = inner;
     w->rows = rows;
     w->gguf_bytes = expect;
+    w->host = host_bytes;
     w->used = ++s->uses;
-    rc = weight_alloc(s,w,round_up(expect,kAlign),&w->raw);
-    if (!rc) {
-        hipError_t e = hipMemcpyAsync(w->raw,host_bytes,expect,hipMemcpyHostToDevice,s->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-        if (e != hipSuccess) rc = hip_fail(e,"weight upload");
-    }
-    if (rc) {
-        release_weight(s,w);
+    // Upload now (the reference uploads on first use too): the forms are built
+    // from this copy on their first use, then it is released.
+    if ((rc = ensure_raw(s,w))) {
+        release_forms(s,w);
+        delete w;
         return rc;
     }
     s->weights.emplace(w->key,w);
@@ -731,8 +833,24 @@ int pixhip_weight_get(pixhip_session* s, const char* key, const void* host_bytes
 int pixhip_weight_cache_info(pixhip_session* s, uint64_t* entries, uint64_t* bytes)
 {
     if (!s) return fail(PIXHIP_ERR_STATE,"no session");
-    if (entries) *entries = s->weights.size();
+    uint64_t n = 0;
+    for (auto& e : s->weights) n += e.second->resident? 1 : 0;
+    if (entries) *entries = n;
     if (bytes) *bytes = s->cache_bytes;
+    return PIXHIP_OK;
+}
+
+int pixhip_weight_residency(pixhip_session* s, uint64_t* gguf_bytes, uint64_t* resident_bytes)
+{
+    if (!s) return fail(PIXHIP_ERR_STATE,"no session");
+    uint64_t g = 0, r = 0;
+    for (auto& e : s->weights) {
+        if (!e.second->resident) continue;
+        g += e.second->gguf_bytes;
+        r += e.second->resident;
+    }
+    if (gguf_bytes) *gguf_bytes = g;
+    if (resident_bytes) *resident_bytes = r;
     return PIXHIP_OK;
 }
 
@@ -769,12 +887,22 @@ int pixhip_quant_matmul(pixhip_session* s, const unsigned char* weights, uint32_
     int rc = check_shape(type,inner,rows);
     if (rc) return rc;
     if (!columns || !weights || !input || !output) return fail(PIXHIP_ERR_ARGUMENT,"null pointer or zero columns");
-    const uint64_t bytes = rows * (inner / block_values(type)) * block_bytes(type);
-    const std::string key = "host:" + std::to_string(reinterpret_cast<uintptr_t>(weights)) + ":" + std::to_string(bytes) + ":" +
-                            std::to_string(type) + ":" + std::to_string(rows) + ":" + std::to_string(inner);
-    pixhip_weight* w = nullptr;
-    if ((rc = pixhip_weight_get(s,key.c_str(),weights,bytes,type,inner,rows,&w))) return rc;
-    return pixhip_matmul(s,w,input,columns,output);
+    if ((rc = use_device(s))) return rc;
+    // Stateless, as cpu_quant_matmul is: a temporary weight outside the cache,
+    // released (after the work completes) before returning.
+    pixhip_weight w;
+    w.key = "quant_matmul";
+    w.type = type;
+    w.inner = inner;
+    w.rows = rows;
+    w.gguf_bytes = rows * (inner / block_values(type)) * block_bytes(type);
+    w.host = weights;
+    w.used = ++s->uses;
+    rc = pixhip_matmul(s,&w,input,columns,output);
+    hipError_t e = hipStreamSynchronize(s->stream);
+    release_forms(s,&w);
+    if (!rc && e != hipSuccess) rc = hip_fail(e,"hipStreamSynchronize");
+    return rc;
 }
 
 int pixhip_quantize_q8_0(pixhip_session* s, const float* input, void* blocks, size_t rows, size_t inner)
@@ -880,7 +1008,17 @@ int pixhip_pointwise(pixhip_session* s, unsigned operation, float* destination, 
         return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
     if ((reinterpret_cast<uintptr_t>(destination) | reinterpret_cast<uintptr_t>(second)) % 4)
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
-    PIX_HIP(pixhip::launch_pointwise((int)operation,destination,second,rows,channels,s->stream),"pointwise");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    const void* other = nullptr;
+    void* staged = nullptr;
+    if (needs_second) {
+        const size_t count = operation == PIXHIP_OP_BIAS? channels : rows * channels;
+        if ((rc = read_operand(s,second,count * sizeof(float),&other,&staged))) return rc;
+    }
+    hipError_t e = pixhip::launch_pointwise((int)operation,static_cast<float*>(dst),static_cast<const float*>(other),rows,channels,s->stream);
+    if (staged) pixhip_free(s,staged);
+    PIX_HIP(e,"pointwise");
     return PIXHIP_OK;
 }
 
@@ -893,7 +1031,21 @@ int pixhip_rope(pixhip_session* s, float* tensor, size_t rows, size_t channels, 
         return fail(PIXHIP_ERR_ARGUMENT,"null pointer, or channels not heads x an even head size");
     if ((reinterpret_cast<uintptr_t>(tensor) | reinterpret_cast<uintptr_t>(cosine) | reinterpret_cast<uintptr_t>(sine)) % 4)
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
-    PIX_HIP(pixhip::launch_rope(tensor,rows,channels,heads,cosine,sine,interleaved != 0,s->stream),"rope");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,tensor,&dst))) return rc;
+    const size_t table = rows * (channels / heads / 2) * sizeof(float);
+    const void *cd = nullptr, *sd = nullptr;
+    void *cs = nullptr, *ss = nullptr;
+    if ((rc = read_operand(s,cosine,table,&cd,&cs))) return rc;
+    if ((rc = read_operand(s,sine,table,&sd,&ss))) {
+        if (cs) pixhip_free(s,cs);
+        return rc;
+    }
+    hipError_t e = pixhip::launch_rope(static_cast<float*>(dst),rows,channels,heads,static_cast<const float*>(cd),static_cast<const float*>(sd),
+                                       interleaved != 0,s->stream);
+    if (cs) pixhip_free(s,cs);
+    if (ss) pixhip_free(s,ss);
+    PIX_HIP(e,"rope");
     return PIXHIP_OK;
 }
 

@@ -3,10 +3,57 @@
 
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <utility>
+#include <vector>
+
+// Pinned host blocks handed to HipAllocator vectors.  A freed block may still
+// be read or written by queued work, so hip_free does not wait: it records an
+// event on the session stream and parks the block; once the event has
+// completed the block returns to a pool that later allocations reuse (as the
+// reference defers a release to the last submission that used the buffer,
+// src/backend_vulkan.cpp:525-531).  The pool is trimmed past kPoolLimit.
 struct HipState {
+    static constexpr size_t kPoolLimit = size_t(1) << 30;
     pixhip_session* session = nullptr;
+    std::vector<std::pair<hipEvent_t,std::pair<void*,size_t>>> pending;  // freed, maybe still in use
+    std::multimap<size_t,void*> pool;                                     // free and idle
+    std::map<void*,size_t> sizes;                                         // every live or pooled block
+    size_t pooled = 0;
+
+    // Moves the blocks whose last use has completed into the pool.
+    void reap()
+    {
+        size_t keep = 0;
+        for (size_t i = 0; i < pending.size(); i++) {
+            hipError_t e = hipEventQuery(pending[i].first);
+            if (e == hipErrorNotReady) {
+                pending[keep++] = pending[i];
+                continue;
+            }
+            (void)hipGetLastError();
+            (void)hipEventDestroy(pending[i].first);
+            pool.emplace(pending[i].second.second,pending[i].second.first);
+            pooled += pending[i].second.second;
+        }
+        pending.resize(keep);
+        while (pooled > kPoolLimit && !pool.empty()) {
+            auto largest = std::prev(pool.end());
+            pooled -= largest->first;
+            sizes.erase(largest->second);
+            (void)hipHostFree(largest->second);
+            pool.erase(largest);
+        }
+    }
+
     ~HipState()
     {
+        if (session) (void)pixhip_synchronize(session);
+        for (auto& p : pending) {
+            (void)hipEventDestroy(p.first);
+            (void)hipHostFree(p.second.first);
+        }
+        for (auto& p : pool) (void)hipHostFree(p.second);
         if (session) pixhip_session_destroy(session);
     }
 };
@@ -29,27 +76,50 @@ void* hip_allocate(const std::shared_ptr<HipState> &state, size_t bytes)
 {
     if (!state) return nullptr;
     if (!bytes) bytes = 4;
+    state->reap();
+    auto hit = state->pool.lower_bound(bytes);
+    if (hit != state->pool.end() && hit->first <= 2 * bytes) {  // reuse up to twice the request
+        void* p = hit->second;
+        state->pooled -= hit->first;
+        state->pool.erase(hit);
+        return p;
+    }
     void* p = nullptr;
     hipError_t e = hipHostMalloc(&p,bytes,hipHostMallocDefault);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;
     }
+    state->sizes[p] = bytes;
     return p;
 }
 
 void hip_free(const std::shared_ptr<HipState> &state, void* pointer)
 {
     if (!state || !pointer) return;
-    // Queued work may still read the buffer (release is deferred in the
-    // reference, src/backend_vulkan.cpp:525-531).
-    (void)pixhip_synchronize(state->session);
-    (void)hipHostFree(pointer);
+    auto it = state->sizes.find(pointer);
+    if (it == state->sizes.end()) return;  // not ours
+    hipEvent_t done = nullptr;
+    if (hipEventCreateWithFlags(&done,hipEventDisableTiming) != hipSuccess ||
+        hipEventRecord(done,static_cast<hipStream_t>(pixhip_session_stream(state->session))) != hipSuccess) {
+        // No event: wait for the queued work instead.
+        (void)hipGetLastError();
+        if (done) (void)hipEventDestroy(done);
+        (void)pixhip_synchronize(state->session);
+        state->pool.emplace(it->second,pointer);
+        state->pooled += it->second;
+    } else {
+        state->pending.push_back({done,{pointer,it->second}});
+    }
+    state->reap();
 }
 
 bool hip_synchronize()
 {
-    return !active_state || pixhip_synchronize(active_state->session) == PIXHIP_OK;
+    if (!active_state) return true;
+    const bool ok = pixhip_synchronize(active_state->session) == PIXHIP_OK;
+    active_state->reap();
+    return ok;
 }
 
 bool HipSession::initialize(int device)

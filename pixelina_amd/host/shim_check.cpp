@@ -11,11 +11,14 @@
 // <in> (little-endian): uint32 type, down_type; uint64 M, K, N, F (FFN width);
 // then W1 [N][K] (type), W2 [N][K] (type), Wdown [K][F] (down_type) as GGUF
 // block bytes, each preceded by its uint64 byte count; X [M][K], norm weight
-// [K], modulation [K], G [M][F], U [M][F] as float32.
+// [K], modulation [K], G [M][F], U [M][F], cos, sin [M][32] and bias [N] as
+// float32 (the vectors in pageable std::vector memory, as tensor_norm,
+// tensor_rope and tensor_bias hold them).
 // <out>: float32 Y = X W1^T [M][N] (hip_matmul); Y1, Y2 = norm(X) W1^T,
 // norm(X) W2^T (hip_norm_multiply, with the weight and the modulation); the
 // normalized X [M][K]; D = (silu(G) * U) Wdown^T [M][K] (hip_silu_gate_multiply);
-// the gated product [M][F].
+// the gated product [M][F]; RoPE of X with K/64 heads of 64 (hip_rope, split
+// halves) [M][K]; Y + bias (hip_pointwise BIAS) [M][N].
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -92,9 +95,10 @@ int main(int argc, char** argv)
     {
         // HipAllocator vectors allocate through the active session (pinned host memory).
         Vals<float> x, gate, up;
-        std::vector<float> norm_weight, modulation;
+        std::vector<float> norm_weight, modulation, cosine, sine, bias;
         if (!read_floats(in,x,M * K) || !read_floats(in,norm_weight,K) || !read_floats(in,modulation,K) ||
-            !read_floats(in,gate,M * F) || !read_floats(in,up,M * F))
+            !read_floats(in,gate,M * F) || !read_floats(in,up,M * F) || !read_floats(in,cosine,M * 32) ||
+            !read_floats(in,sine,M * 32) || !read_floats(in,bias,N))
             return fail("short activations");
         std::fclose(in);
 
@@ -111,12 +115,18 @@ int main(int argc, char** argv)
         pixhip_weight* down = hip_weight_of(file,wd);
         if (!down || !hip_silu_gate_multiply(wd.type,down,gate.data(),up.data(),M,F,d.data(),gated.data()))
             return fail("hip_silu_gate_multiply");
+        // tensor_rope / tensor_bias hand their std::vector tables straight in
+        Vals<float> roped(x.begin(),x.end()), biased(M * N);
+        if (!hip_synchronize()) return fail("hip_synchronize");
+        for (size_t i = 0; i < biased.size(); i++) biased[i] = y[i];
+        if (!hip_rope(roped.data(),M,K,K / 64,cosine.data(),sine.data(),false)) return fail("hip_rope");
+        if (!hip_pointwise(PIXHIP_OP_BIAS,biased.data(),bias.data(),M,N)) return fail("hip_pointwise(BIAS)");
         if (!hip_synchronize()) return fail("hip_synchronize");
 
         FILE* out = std::fopen(argv[2],"wb");
         if (!out) return fail("cannot open output");
         const bool ok = write_floats(out,y) && write_floats(out,y1) && write_floats(out,y2) && write_floats(out,normalized) &&
-                        write_floats(out,d) && write_floats(out,gated);
+                        write_floats(out,d) && write_floats(out,gated) && write_floats(out,roped) && write_floats(out,biased);
         std::fclose(out);
         if (!ok) return fail("short write");
     }

@@ -46,11 +46,16 @@ class Session:
         h = ctypes.c_void_p()
         check(self.lib.pixhip_session_create(device, ctypes.byref(h)), "pixhip_session_create")
         self.handle = h.value
+        # The library re-reads a weight's host bytes when it rebuilds a form
+        # (after eviction, or for the other kernel family): keep them alive for
+        # the session, as a model file's mapping is.
+        self._host_weights = {}
 
     def close(self):
         if self.handle:
             self.lib.pixhip_session_destroy(self.handle)
             self.handle = None
+            self._host_weights = {}
 
     def __enter__(self):
         return self
@@ -83,6 +88,7 @@ class Session:
         h = ctypes.c_void_p()
         check(self.lib.pixhip_weight_get(self.handle, key.encode(), b.ctypes.data, b.nbytes, wtype, inner, rows,
                                          ctypes.byref(h)), "pixhip_weight_get")
+        self._host_weights[key] = b
         return h.value
 
     def weight_shape(self, weight):
@@ -94,6 +100,18 @@ class Session:
         n, b = ctypes.c_uint64(), ctypes.c_uint64()
         check(self.lib.pixhip_weight_cache_info(self.handle, ctypes.byref(n), ctypes.byref(b)), "pixhip_weight_cache_info")
         return n.value, b.value
+
+    def residency(self):
+        """(GGUF bytes, resident device bytes) of the weights with device forms."""
+        g, r = ctypes.c_uint64(), ctypes.c_uint64()
+        check(self.lib.pixhip_weight_residency(self.handle, ctypes.byref(g), ctypes.byref(r)), "pixhip_weight_residency")
+        return g.value, r.value
+
+    def set_weight_budget(self, nbytes):
+        check(self.lib.pixhip_set_weight_budget(self.handle, nbytes), "pixhip_set_weight_budget")
+
+    def prepare_stage(self, activation_bytes, scratch_bytes):
+        return self.lib.pixhip_prepare_stage(self.handle, activation_bytes, scratch_bytes)
 
     # the op
     def matmul(self, weight, x_ptr, columns, y_ptr):

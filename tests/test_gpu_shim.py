@@ -3,8 +3,10 @@ reference's model code drives its Vulkan backend, by pixelina_amd/shim_check
 (built with the library): a HipSession made current on the thread, activations
 in HipAllocator vectors (pinned host memory), weights reached through a
 model-file / weight pair shaped like PixModelFile / PixWeight, and the calls of
-tensor_linear (hip_matmul) and of the DiT block's FFN (hip_norm_multiply for
-the gate and up linears, hip_silu_gate_multiply for the down linear).
+tensor_linear (hip_matmul), of the DiT block's FFN (hip_norm_multiply for
+the gate and up linears, hip_silu_gate_multiply for the down linear), and of
+tensor_rope / tensor_bias (hip_rope, hip_pointwise) with their tables in
+pageable std::vector memory, which the library stages to the device.
 
 Against the oracle: the normalized input bit-exact; the SiLU product within 4
 ulps (the reference's glibc expf is not correctly rounded; this one is); every
@@ -17,7 +19,7 @@ import numpy as np
 import pytest
 
 from gpu_helpers import TOL, row_rel_error
-from oracle_lib import Q5_K, Q8_0, modulate_rows, norm_rows, oracle, quant_matmul, quantize, silu_gate
+from oracle_lib import Q5_K, Q8_0, bias, modulate_rows, norm_rows, oracle, quant_matmul, quantize, rope, silu_gate
 from pixelina_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -38,6 +40,9 @@ def test_shim_matmul_norm_and_gate(tmp_path):
     mod = (0.2 * rng.standard_normal(k)).astype(np.float32)
     g = (rng.standard_normal((m, f)) * 3.0).astype(np.float32)
     u = rng.standard_normal((m, f)).astype(np.float32)
+    th = rng.standard_normal((m, 32)) * 3.0
+    cos, sin = np.cos(th).astype(np.float32), np.sin(th).astype(np.float32)
+    bvec = rng.standard_normal(n).astype(np.float32)
     src, dst = tmp_path / "in.bin", tmp_path / "out.bin"
     with open(src, "wb") as fh:
         fh.write(np.array([Q5_K, Q8_0], np.uint32).tobytes())
@@ -45,15 +50,20 @@ def test_shim_matmul_norm_and_gate(tmp_path):
         for wb in (w1, w2, wd):
             fh.write(np.array([wb.nbytes], np.uint64).tobytes())
             fh.write(np.ascontiguousarray(wb).tobytes())
-        for a in (x, nw, mod, g, u):
+        for a in (x, nw, mod, g, u, cos, sin, bvec):
             fh.write(np.ascontiguousarray(a, np.float32).tobytes())
     print("running shim_check", flush=True)
     proc = subprocess.run([SHIM_CHECK, str(src), str(dst)], capture_output=True, text=True, timeout=120)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     out = np.fromfile(dst, np.float32)
-    sizes = [m * n, m * n, m * n, m * k, m * k, m * f]
+    sizes = [m * n, m * n, m * n, m * k, m * k, m * f, m * k, m * n]
     assert out.size == sum(sizes)
-    y, y1, y2, normalized, d, gated = np.split(out, np.cumsum(sizes)[:-1])
+    y, y1, y2, normalized, d, gated, roped, biased = np.split(out, np.cumsum(sizes)[:-1])
+
+    # hip_rope / hip_pointwise(BIAS) were handed pageable std::vector tables:
+    # bit-exact against the oracle's tensor_rope / tensor_bias
+    assert np.array_equal(roped.reshape(m, k).view(np.uint32), rope(o, "orc", x, k // 64, cos, sin, 0).view(np.uint32))
+    assert np.array_equal(biased.reshape(m, n).view(np.uint32), bias(o, "orc", y.reshape(m, n), bvec).view(np.uint32))
 
     ref_norm = modulate_rows(o, norm_rows(o, "orc", x, nw, 1e-5, 0), mod)
     assert np.array_equal(normalized.view(np.uint32), ref_norm.reshape(-1).view(np.uint32))

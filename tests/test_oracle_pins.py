@@ -9,7 +9,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, load_oracle, norm_rows, oracle, ptr,
+from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, load_oracle, modulate_rows, norm_rows, oracle, ptr,
                         quant_matmul, quantize, rope, silu_gate)
 from pixelina_amd import synth
 
@@ -348,6 +348,8 @@ MUTANTS = {
     10: "SiLU as a reciprocal times v",
     11: "RoPE with the sine's sign flipped",
     12: "tanh GELU with v*v instead of v*v*v",
+    13: "modulation as x + x*scale",
+    14: "modulation by scale instead of 1 + scale",
 }
 
 
@@ -387,8 +389,39 @@ def golden_mismatches(lib):
     return bad
 
 
+def modulation_mismatches(lib):
+    """orc_modulate_rows (z_modulate, src/inference.cpp:263-277:
+    x * (1.0f + scale[c]) in fp32) against what fixes it without the reference,
+    which cannot be linked here (z_modulate is static in inference.cpp):
+      scale 0 is the identity, bit for bit;  scale -1 gives x * 0 (signed zeros);
+      scale 1 doubles exactly;  scale 2^-24 rounds 1 + scale to 1, so 1.5 stays
+      1.5 (x + x*scale would give 1.5 + 2^-23);  and on random values the single
+      rounding of the product of x and the rounded 1 + scale, computed in float64
+      and rounded once (exact: both factors have 24-bit significands)."""
+    bad = 0
+    rng = np.random.default_rng(23)
+    x = (rng.standard_normal((6, 64)) * 10.0 ** rng.integers(-3, 4, (6, 1))).astype(np.float32)
+    x[0, :4] = [1.5, -1.5, 3.0, -0.0]
+    for s_val, want in ((0.0, x), (-1.0, x * np.float32(0.0)), (1.0, x * np.float32(2.0))):
+        got = modulate_rows(lib, x, np.full(64, s_val, np.float32))
+        bad += int(not np.array_equal(got.view(np.uint32), np.asarray(want, np.float32).view(np.uint32)))
+    s = np.zeros(64, np.float32)
+    s[:4] = 2.0 ** -24
+    got = modulate_rows(lib, x[:1], s)
+    bad += int(not np.array_equal(got[0, :4].view(np.uint32), x[0, :4].view(np.uint32)))
+    s = (rng.standard_normal(64) * 0.3).astype(np.float32)
+    one_plus = (1.0 + s.astype(np.float64)).astype(np.float32)  # the fp32 sum: one rounding of an exact double sum
+    want = (x.astype(np.float64) * one_plus.astype(np.float64)).astype(np.float32)
+    bad += int(not np.array_equal(modulate_rows(lib, x, s).view(np.uint32), want.view(np.uint32)))
+    return bad
+
+
 def test_unmutated_oracle_passes_every_golden_comparison():
     assert golden_mismatches(oracle()) == 0
+
+
+def test_modulation_closed_forms():
+    assert modulation_mismatches(oracle()) == 0
 
 
 @pytest.mark.parametrize("mutant", sorted(MUTANTS))
@@ -397,4 +430,5 @@ def test_golden_vectors_catch_planted_mistake(mutant, tmp_path):
     subprocess.run(["gcc", "-std=c11", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", "-pthread",
                     f"-DORC_MUTANT={mutant}", os.path.join(ORACLE_DIR, "pix_oracle.c"), "-o", str(so), "-lm"],
                    check=True, capture_output=True)
-    assert golden_mismatches(load_oracle(str(so))) > 0, MUTANTS[mutant]
+    lib = load_oracle(str(so))
+    assert golden_mismatches(lib) + modulation_mismatches(lib) > 0, MUTANTS[mutant]
