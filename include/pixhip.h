@@ -154,6 +154,24 @@ int pixhip_matmul_ex(pixhip_session* session, const pixhip_weight* weight, const
 int pixhip_matmul_stage(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t columns, float* output,
                         const float* bias, size_t ldy, size_t y_offset, unsigned stages);
 
+/* No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  pixhip_matmul_ex without any allocation: the quantized
+ * activations go to a fixed 32 MiB device array per GPU (held until the
+ * process ends) instead of session scratch, the GEMM runs without its split-K
+ * workspace, and nothing is staged, so `input` and `output` must be device
+ * memory.  The weight's layout must already be resident (run it once through
+ * pixhip_matmul_ex with the same kind of call: columns == 1 for the matvec,
+ * columns > 1 for the GEMM); otherwise PIXHIP_ERR_STATE.  Activations beyond
+ * the array (Mpad*K bytes plus scales: e.g. 4096 x 3840 Q8_K takes 17.9 MB)
+ * give PIXHIP_ERR_MEMORY.  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (several sessions or streams) race.  Results equal
+ * pixhip_matmul_ex's, bit for bit where that call runs unsplit, else within
+ * the fp32 rounding of the split sums.  Leaves no activations for
+ * PIXHIP_STAGE_MULTIPLY. */
+int pixhip_matmul_ex_noalloc(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t columns,
+                             float* output, const float* bias, size_t ldy, size_t y_offset);
+
 /* cpu_quant_matmul (src/kernels_quant.cpp:369-412) with the same argument
  * meaning: host GGUF weight bytes, input [columns][inner], output
  * [columns][rows].  Stateless like the reference: the weight is uploaded and

@@ -54,6 +54,7 @@ SIGNATURES = {
     "pixhip_matmul": (_int, [_vp, _vp, _vp, _sz, _vp]),
     "pixhip_matmul_ex": (_int, [_vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz]),
     "pixhip_matmul_stage": (_int, [_vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz, ctypes.c_uint]),
+    "pixhip_matmul_ex_noalloc": (_int, [_vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz]),
     "pixhip_quant_matmul": (_int, [_vp, _vp, _u32, _vp, _vp, _sz, _sz, _sz]),
     "pixhip_quantize_q8_0": (_int, [_vp, _vp, _vp, _sz, _sz]),
     "pixhip_quantize_q8_K": (_int, [_vp, _vp, _vp, _sz, _sz]),

@@ -11,6 +11,7 @@
 #include <cstdint>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <new>
 #include <string>
 #include <unordered_map>
@@ -60,6 +61,38 @@ struct Carver {
         return at;
     }
 };
+
+// The allocation-free GEMM entry point (pixhip_matmul_ex_noalloc) keeps the
+// quantized activations in this fixed device array instead of session
+// scratch.  Each device holds its own copy until the process ends; host code
+// reaches it only through the per-device address from hipGetSymbolAddress.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// Resolves, once per device (the device current), the address of that
+// device's copy of `scratch`.
+int scratch_setup(int device)
+{
+    if (device < 0 || device >= kMaxDevices) return fail(PIXHIP_ERR_ARGUMENT,"device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device]) return PIXHIP_OK;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p,HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return fail(PIXHIP_ERR_DEVICE,std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    }
+    g_scratch_ptr[device] = p;
+    return PIXHIP_OK;
+}
 
 }  // namespace
 
@@ -619,6 +652,10 @@ int pixhip_session_create(int device, pixhip_session** out)
         return rc;
     }
     s->stream = s->own_stream;
+    if (int rc = scratch_setup(device)) {
+        pixhip_session_destroy(s);
+        return rc;
+    }
     // hipDeviceProp_t::name can be empty (no marketing name in the driver's
     // table); fall back to the architecture name alone.
     s->name = prop.name[0]? std::string(prop.name) + " (" + prop.gcnArchName + ")" : std::string(prop.gcnArchName);
@@ -878,6 +915,67 @@ int pixhip_matmul_stage(pixhip_session* s, const pixhip_weight* w, const float* 
                         const float* bias, size_t ldy, size_t y_offset, unsigned stages)
 {
     return run(s,w,input,columns,output,bias,ldy,y_offset,stages,false);
+}
+
+int pixhip_matmul_ex_noalloc(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t columns, float* output,
+                             const float* bias, size_t ldy, size_t y_offset)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    pixhip_weight* w = const_cast<pixhip_weight*>(wc);
+    if (!w) return fail(PIXHIP_ERR_ARGUMENT,"null weight handle");
+    if (!columns || !input || !output) return fail(PIXHIP_ERR_ARGUMENT,"null pointer or zero columns");
+    if (!ldy) ldy = w->rows;
+    if (ldy < w->rows) return fail(PIXHIP_ERR_ARGUMENT,"output stride smaller than rows");
+    const void* xin = nullptr;
+    const void* yv = nullptr;
+    if (!device_visible(s,input,&xin) || !device_visible(s,output,&yv))
+        return fail(PIXHIP_ERR_ARGUMENT,"input and output must be device memory (nothing is staged here)");
+    if (reinterpret_cast<uintptr_t>(xin) % 16) return fail(PIXHIP_ERR_ARGUMENT,"input must be 16-byte aligned");
+    void* dev_scratch = g_scratch_ptr[s->device];
+    if (!dev_scratch) return fail(PIXHIP_ERR_STATE,"scratch not set up on this device");
+    const pixhip::Output out = {static_cast<float*>(const_cast<void*>(yv)),bias,ldy,y_offset};
+    const float* x = static_cast<const float*>(xin);
+    const size_t K = w->inner;
+    w->used = ++s->uses;
+    hipError_t e;
+    if (columns == 1 && matvec_ok(w)) {
+        // The matvec quantizes x in LDS: no scratch, but its layout must be resident.
+        if (!w->planar) return fail(PIXHIP_ERR_STATE,"matvec layout not resident: run the weight once through pixhip_matmul_ex");
+        if (w->type == PIX_Q5_K) e = pixhip::launch_matvec_q5_K(w->q5p,x,w->rows,K,out,s->stream);
+        else if (w->type == PIX_Q8_0) e = pixhip::launch_matvec_q8_0(w->q80,x,w->rows,K,out,s->stream);
+        else e = pixhip::launch_matvec_q6_K(w->q6p,x,w->rows,K,out,s->stream);
+        PIX_HIP(e,"matvec launch");
+        return PIXHIP_OK;
+    }
+    if (!w->planes) return fail(PIXHIP_ERR_STATE,"GEMM layout not resident: run the weight once through pixhip_matmul_ex");
+    // The quantized activations in `scratch`, carved as act_buffers carves the
+    // session scratch; the GEMM then runs unsplit (no split-K workspace).
+    const size_t mpad = round_up(columns,kTileM);
+    Carver c;
+    uint8_t* base = static_cast<uint8_t*>(dev_scratch);
+    if (w->type == PIX_Q8_0) {
+        const size_t kp = round_up(K,64);
+        const size_t qs = c.take(mpad * kp), d = c.take((kp / PIX_QK8) * mpad * 4);
+        if (c.offset > kNoAllocScratchBytes)
+            return fail(PIXHIP_ERR_MEMORY,"activations of " + std::to_string(columns) + " x " + std::to_string(K) + " need " +
+                                              std::to_string(c.offset) + " bytes, beyond the 32 MiB allocation-free scratch");
+        const pixhip::Act80 a = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<float*>(base + d),mpad};
+        PIX_HIP(pixhip::launch_quantize_q8_0(x,columns,K,kp,a,nullptr,s->stream),"quantize Q8_0");
+        e = pixhip::launch_gemm_q8_0(a,w->q80,columns,w->rows,K,out,nullptr,s->stream);
+    } else {
+        const size_t qs = c.take(mpad * K), d = c.take((K / PIX_QK) * mpad * 4), bs = c.take(mpad * (K / 16) * 2);
+        if (c.offset > kNoAllocScratchBytes)
+            return fail(PIXHIP_ERR_MEMORY,"activations of " + std::to_string(columns) + " x " + std::to_string(K) + " need " +
+                                              std::to_string(c.offset) + " bytes, beyond the 32 MiB allocation-free scratch");
+        const pixhip::Act8K a = {reinterpret_cast<int8_t*>(base + qs),reinterpret_cast<float*>(base + d),
+                                 reinterpret_cast<_Float16*>(base + bs),mpad};
+        PIX_HIP(pixhip::launch_quantize_q8_K(x,columns,K,a,nullptr,s->stream),"quantize Q8_K");
+        e = w->type == PIX_Q5_K? pixhip::launch_gemm_q5_K(a,w->q5,columns,w->rows,K,out,nullptr,s->stream)
+                               : pixhip::launch_gemm_q6_K(a,w->q6,columns,w->rows,K,out,nullptr,s->stream);
+    }
+    PIX_HIP(e,"GEMM launch");
+    return PIXHIP_OK;
 }
 
 int pixhip_quant_matmul(pixhip_session* s, const unsigned char* weights, uint32_t type, const float* input, float* output,

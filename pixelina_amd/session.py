@@ -120,6 +120,9 @@ class Session:
     def matmul_ex(self, weight, x_ptr, columns, y_ptr, bias_ptr=None, ldy=0, y_offset=0):
         return self.lib.pixhip_matmul_ex(self.handle, weight, x_ptr, columns, y_ptr, bias_ptr, ldy, y_offset)
 
+    def matmul_noalloc(self, weight, x_ptr, columns, y_ptr, bias_ptr=None, ldy=0, y_offset=0):
+        return self.lib.pixhip_matmul_ex_noalloc(self.handle, weight, x_ptr, columns, y_ptr, bias_ptr, ldy, y_offset)
+
     def matmul_stage(self, weight, x_ptr, columns, y_ptr, stages, bias_ptr=None, ldy=0, y_offset=0):
         return self.lib.pixhip_matmul_stage(self.handle, weight, x_ptr, columns, y_ptr, bias_ptr, ldy, y_offset, stages)
 
