@@ -10,14 +10,19 @@ Inputs are resident in HBM before timing starts.
 Also reported in the same JSON line: the GEMM kernel alone (the roofline
 object, against the int8 MFMA peak), the quantize pass alone, the M=1 decode
 matvec (Q5_K and Q8_0, W [18944, 3584], 100 repeats rotating >= 1 GiB of weight
-copies so the 256 MB Infinity Cache cannot serve them), and the reference CPU
-path (cpu_quant_matmul) timed on this host on the same inputs.
+copies so the 256 MB Infinity Cache cannot serve them), the other specified
+workloads (`workloads`: a single Q8_0 linear [256, 3840] x [3840, 3840], every
+linear of a Z-Image DiT block at M = 4608 and of a Qwen-Image edit block at
+M = 8448, each linear and the block back to back), the same step with host
+(pinned) operands staged over PCIe, and the reference CPU path
+(cpu_quant_matmul) timed on this host on the same inputs.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-blocks]
 
 Progress goes to stderr; stdout carries exactly one JSON line.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -36,29 +41,56 @@ COPY_BYTES = 1 << 29  # the plain copy that calibrates the HBM byte counters
 
 GEMM_M, GEMM_K, GEMM_N = 4096, 3840, 10240
 MV_K, MV_N = 3584, 18944
+WARMUP_FLOOR_MS = 50.0  # device time before the headline series
+SERIES_FLOOR_MS = 20.0  # device time per timed series of the other workloads
+
+# The other workloads: (name, tokens, activation row scales, [(linear, type, K, N)]).
+WORKLOADS = [
+    ("q8_0_linear", 256, None, [("linear", "Q8_0", 3840, 3840)]),
+    ("dit_block", 4096 + 512, None, [("qkv", "Q5_K", 3840, 11520), ("out", "Q5_K", 3840, 3840), ("w1", "Q5_K", 3840, 10240),
+                                     ("w3", "Q5_K", 3840, 10240), ("w2", "Q8_0", 10240, 3840)]),
+    ("qwen_edit_block", 4096 + 4096 + 256, (0.1, 10.0),
+     [("qkv", "Q5_K", 3072, 9216), ("out", "Q5_K", 3072, 3072), ("ff_up", "Q5_K", 3072, 12288), ("ff_down", "Q5_K", 12288, 3072)]),
+]
+WORKLOAD_TEXT = {
+    "q8_0_linear": "single Q8_0 linear, X[256,3840] W[3840,3840]",
+    "dit_block": "Z-Image DiT block linears, M=4608 (4096 image + 512 text), Q5_K except FFN-down Q8_0",
+    "qwen_edit_block": "Qwen-Image edit block linears, M=8448 (2x4096 image + 256 text), Q5_K, per-token scales log-uniform [0.1,10]",
+}
 
 
 def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_threads():
+def affinity_cores():
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        return os.cpu_count() or 1
 
 
-def cpu_model():
+def cpu_threads():
+    """Threads for the CPU reference: every core this process may run on, at
+    most 16 (the host-core share of one GPU on a shared multi-GPU node)."""
+    return max(1, min(affinity_cores(), 16))
+
+
+def cpu_info():
+    model, flags = "unknown", set()
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
     except OSError:
         pass
-    return "unknown"
+    # The reference's quantized kernels take their AVX2 path (target("avx2,fma,f16c"))
+    # when the CPU has these.
+    return {"cpu": model, "nproc": affinity_cores(), "os_cpu_count": os.cpu_count(),
+            "avx2": "avx2" in flags, "fma": "fma" in flags, "f16c": "f16c" in flags, "avx512f": "avx512f" in flags}
 
 
 def row_rel(y, r):
@@ -109,6 +141,156 @@ def gemm_workload(synth):
     wb = synth.pack_q5_K(w)
     del w
     return x, wb, ch
+
+
+def timed_series(sess, run_once, min_reps, floor_ms=SERIES_FLOOR_MS):
+    """Average device ms of run_once() (which enqueues one step) over a series of
+    at least min_reps steps and floor_ms of device time, after a warm-up of the
+    same length."""
+    sess.synchronize()
+    sess.timer_start()
+    run_once()
+    once = max(sess.timer_stop(), 1e-3)
+    reps = max(min_reps, int(np.ceil(floor_ms / once)))
+    for _ in range(reps):
+        run_once()
+    sess.timer_start()
+    for _ in range(reps):
+        run_once()
+    return sess.timer_stop() / reps, reps
+
+
+def workload_inputs(synth, name, m, row_scale, linears):
+    """Seeded inputs of one workload: one activation matrix per distinct K
+    (~N(0,1), times a per-token scale where given) and N(0, 0.02) weights, all
+    from numpy's PCG64 generator, the generator of the parity tests' block
+    workloads.  Q5_K weights are packed here; Q8_0 weights are returned as
+    float32 and quantized by the HIP quantizer (bit-exact quantize_row_q8_0_ref)."""
+    xs = {}
+    for i, k in enumerate(sorted({k for _, _, k, _ in linears})):
+        x = np.random.default_rng(500 + 7 * i + len(name)).standard_normal((m, k), dtype=np.float32)
+        if row_scale:
+            x *= synth.log_uniform(600 + k, m, *row_scale)[:, None]
+        xs[k] = x
+    ws = {}
+    for j, (lin, wtype, k, n) in enumerate(linears):
+        wf = np.random.default_rng(700 + 13 * j + len(name)).standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+        ws[lin] = synth.pack_q5_K(wf) if wtype == "Q5_K" else wf
+    return xs, ws
+
+
+def bench_workloads(sess, synth, _lib, types, steps):
+    """Every linear of each workload timed alone (quantize + GEMM per step, and
+    the GEMM alone), then the workload's linears back to back as one series.
+    Returns the JSON records and, per workload, what the CPU leg needs."""
+    out, keep = {}, {}
+    both = _lib.STAGE_QUANTIZE | _lib.STAGE_MULTIPLY
+    for name, m, row_scale, linears in WORKLOADS:
+        log(f"workload {name}: generating inputs")
+        xs, ws = workload_inputs(synth, name, m, row_scale, linears)
+        xbs = {k: sess.to_device(x) for k, x in xs.items()}
+        handles, ybs, recs, wbytes = [], [], {}, {}
+        for lin, wtype, k, n in linears:
+            if wtype == "Q8_0":  # quantize the float weights with the HIP quantizer
+                wdev, qdev = sess.to_device(ws[lin]), sess.alloc(n * k // 32 * 34)
+                _lib.check(sess.quantize_q8_0(wdev.ptr, qdev.ptr, n, k), "quantize weights")
+                ws[lin] = qdev.download(np.uint8, n * k // 32 * 34).reshape(n, -1)
+                wdev.free()
+                qdev.free()
+            wbytes[lin] = ws[lin]
+            h = sess.weight(f"bench:{name}:{lin}", ws[lin], types[wtype], k, n)
+            yb = sess.alloc(m * n * 4)
+            handles.append((h, xbs[k].ptr, yb.ptr))
+            ybs.append(yb)
+            ops = 2.0 * m * n * k
+            step_ms, reps = timed_series(sess, lambda: _lib.check(sess.matmul_stage(h, xbs[k].ptr, m, yb.ptr, both), lin), steps)
+            gemm_ms, _ = timed_series(sess, lambda: _lib.check(sess.matmul_stage(h, None, m, yb.ptr, _lib.STAGE_MULTIPLY), lin),
+                                      steps)
+            recs[lin] = {"M": m, "K": k, "N": n, "type": wtype, "us": round(step_ms * 1e3, 2),
+                         "tops": round(ops / (step_ms * 1e-3) / 1e12, 2),
+                         "frac": round(ops / (step_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+                         "gemm_us": round(gemm_ms * 1e3, 2), "gemm_tops": round(ops / (gemm_ms * 1e-3) / 1e12, 2),
+                         "gemm_frac": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4), "reps": reps}
+            log(f"  {lin} [{m},{k}]x[{n}] {wtype}: {step_ms * 1e3:.1f} us ({recs[lin]['frac'] * 100:.1f}%), "
+                f"GEMM {gemm_ms * 1e3:.1f} us ({recs[lin]['gemm_frac'] * 100:.1f}%)")
+
+        def block():
+            for h, xp, yp in handles:
+                _lib.check(sess.matmul(h, xp, m, yp), name)
+
+        block_ms, block_reps = timed_series(sess, block, max(3, steps // len(linears)))
+        ops = sum(2.0 * m * n * k for _, _, k, n in linears)
+        ys = {}
+        for (lin, _, _, n), yb in zip(linears, ybs):
+            ys[lin] = yb.download(np.float32, m * n).reshape(m, n)
+            yb.free()
+        for xb in xbs.values():
+            xb.free()
+        rec = {"workload": WORKLOAD_TEXT[name], "linears": recs}
+        if len(linears) > 1:
+            rec["total"] = {"us": round(block_ms * 1e3, 2), "tops": round(ops / (block_ms * 1e-3) / 1e12, 2),
+                            "frac": round(ops / (block_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+                            "sum_of_linears_us": round(sum(r["us"] for r in recs.values()), 2), "reps": block_reps,
+                            "ops": ops}
+            log(f"  {name} back to back: {block_ms * 1e3:.1f} us ({rec['total']['frac'] * 100:.1f}%)")
+        out[name] = rec
+        keep[name] = (xs, wbytes, ys, linears)
+    return out, keep
+
+
+def cpu_workloads(cpu, types, out, keep):
+    """The reference CPU path on the same inputs: every linear in full (a few
+    seconds on 16 threads); with the oracle restatement instead, 64 token rows
+    per linear and the time scaled to the full M."""
+    for name, (xs, wbytes, ys, linears) in keep.items():
+        total = 0.0
+        for lin, wtype, k, n in linears:
+            x = xs[k]
+            rows = x.shape[0] if cpu.kind == "reference" else min(64, x.shape[0])
+            cpu.matmul(wbytes[lin][:8], types[wtype], x[:4], 8)  # pool warm-up
+            t = time.perf_counter()
+            yc = cpu.matmul(wbytes[lin], types[wtype], x[:rows], n)
+            sec = (time.perf_counter() - t) * x.shape[0] / rows
+            err = row_rel(ys[lin][:rows], yc)
+            r = out[name]["linears"][lin]
+            r["cpu_us"] = round(sec * 1e6, 1)
+            r["cpu_tops"] = round(2.0 * x.shape[0] * n * k / sec / 1e12, 4)
+            r["cpu_rows_timed"] = rows
+            r["parity_max_row_rel_err_vs_cpu"] = err
+            total += sec
+            log(f"  CPU {name}.{lin}: {sec * 1e3:.1f} ms; GPU vs CPU rel err {err:.2e}")
+        if "total" in out[name]:
+            out[name]["total"]["cpu_us"] = round(total * 1e6, 1)
+            out[name]["total"]["cpu_tops"] = round(out[name]["total"]["ops"] / total / 1e12, 4)
+
+
+def bench_pcie(sess, _lib, w, x, reps=10):
+    """The headline step through pixhip_matmul with host operands in pinned
+    memory (what hip_matmul receives from HipAllocator vectors): X copied to
+    HBM, quantize + GEMM, Y copied back, synchronously, timed on the host clock."""
+    hip = sess.lib  # libpixhip.so resolves the HIP runtime it links
+    hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+    hip.hipHostFree.argtypes = [ctypes.c_void_p]
+    xp, yp = ctypes.c_void_p(), ctypes.c_void_p()
+    nx, ny = GEMM_M * GEMM_K * 4, GEMM_M * GEMM_N * 4
+    if hip.hipHostMalloc(ctypes.byref(xp), nx, 0) or hip.hipHostMalloc(ctypes.byref(yp), ny, 0):
+        raise RuntimeError("hipHostMalloc failed")
+    try:
+        ctypes.memmove(xp, x.ctypes.data, nx)
+        for _ in range(3):
+            _lib.check(sess.matmul(w, xp.value, GEMM_M, yp.value), "pixhip_matmul (host operands)")
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            _lib.check(sess.matmul(w, xp.value, GEMM_M, yp.value), "pixhip_matmul (host operands)")
+            ts.append(time.perf_counter() - t)
+    finally:
+        hip.hipHostFree(xp)
+        hip.hipHostFree(yp)
+    sec = float(np.median(ts))
+    return {"workload": "the headline step with X and Y in pinned host memory (pixhip_matmul stages them through HBM)",
+            "us": round(sec * 1e6, 1), "tops": round(2.0 * GEMM_M * GEMM_N * GEMM_K / sec / 1e12, 2),
+            "h2d_bytes": nx, "d2h_bytes": ny, "clock": f"host perf_counter, median of {reps} synchronous calls"}
 
 
 def bench_fused(sess, synth, _lib, Q5_K, Q8_0, reps):
@@ -196,13 +378,15 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # ~20 ms of untimed steps: the first 5-20 ms of work on an idle device run
-    # up to 30% slower (clock / power ramp) before the GEMM settles
+    # untimed steps, continued until >= 50 ms of device time: the first 5-50 ms
+    # of work on an idle device run up to 30% slower (clock / power ramp)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--matvec-reps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--no-fused", action="store_true", help="skip the fused norm / SiLU-gate producers")
+    ap.add_argument("--no-blocks", action="store_true", help="skip the single Q8_0 linear and the block workloads")
+    ap.add_argument("--no-pcie", action="store_true", help="skip the host-operand (PCIe-inclusive) step")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one plain 512 MiB device copy (the calibration kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -222,8 +406,13 @@ def main():
         xb = sess.to_device(x)
         yb = sess.alloc(GEMM_M * GEMM_N * 4)
         both = _lib.STAGE_QUANTIZE | _lib.STAGE_MULTIPLY
-        log(f"warmup {args.warmup} steps")
-        sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, both, max(1, args.warmup))
+        warm_steps = max(1, args.warmup)
+        warm_ms = sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, both, warm_steps)
+        while warm_ms < WARMUP_FLOOR_MS:
+            more = int((WARMUP_FLOOR_MS - warm_ms) / (warm_ms / warm_steps)) + 1
+            warm_ms += sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, both, more)
+            warm_steps += more
+        log(f"warmup {warm_steps} steps, {warm_ms:.1f} ms of device time")
         log(f"timing {args.steps} steps (quantize + GEMM)")
         ms_step = sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, both, args.steps) / args.steps
         ms_gemm = sess.bench_matmul([w], xb.ptr, GEMM_M, yb.ptr, _lib.STAGE_MULTIPLY, args.steps) / args.steps
@@ -233,6 +422,12 @@ def main():
         log(f"step {ms_step * 1e3:.1f} us, GEMM {ms_gemm * 1e3:.1f} us, quantize {ms_quant * 1e3:.1f} us")
         xb.free()
         yb.free()
+        pcie = None if args.no_pcie else bench_pcie(sess, _lib, w, x)
+        if pcie:
+            log(f"host operands (PCIe-inclusive): {pcie['us']:.0f} us per step")
+        types = {"Q5_K": Q5_K, "Q8_0": Q8_0}
+        workloads, keep = ({}, {}) if args.no_blocks else bench_workloads(sess, synth, _lib, types, args.steps)
+        gguf_bytes, resident_bytes = sess.residency()
 
         matvec = {}
         if not args.no_matvec:
@@ -283,6 +478,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_steps,
+        "warmup_ms": round(warm_ms, 2),
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -292,7 +489,7 @@ def main():
         "config": {"workload": "Q5_K GEMM M=4096 K=3840 N=10240 (Z-Image DiT FFN), quantize + GEMM per step",
                    "M": GEMM_M, "K": GEMM_K, "N": GEMM_N, "weight_type": "Q5_K", "activation_type": "Q8_K",
                    "outlier_channels": int(len(ch)), "device": device},
-        "roofline": {"kernel": "gemm_kernel<Q5_K>", "bound": "mfma", "achieved": round(tops_gemm, 2), "peak": PEAK_INT8_TOPS,
+        "roofline": {"kernel": "gemm_kq_kernel<Q5_K>", "bound": "mfma", "achieved": round(tops_gemm, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOP/s", "frac": round(tops_gemm / PEAK_INT8_TOPS, 4), "traffic": measured_traffic("gemm_q5_K"),
                      "work_per_launch": f"2*M*N*K = {ops:.4e} int8 ops", "avg_launch_us": round(ms_gemm * 1e3, 2)},
         "gemm_only": {"us": round(ms_gemm * 1e3, 2), "tops": round(tops_gemm, 2)},
@@ -310,11 +507,19 @@ def main():
 
     if fused:
         line["fused"] = fused
+    if workloads:
+        line["workloads"] = workloads
+    if pcie:
+        line["pcie_inclusive"] = pcie
+    line["residency"] = {"gguf_bytes": gguf_bytes, "resident_bytes": resident_bytes,
+                         "ratio": round(resident_bytes / max(gguf_bytes, 1), 3),
+                         "note": "device bytes per GGUF byte of the headline and workload weights (GEMM layouts)"}
 
     if not args.no_cpu:
         threads = cpu_threads()
         cpu = CpuBaseline(threads)
-        log(f"CPU baseline ({cpu.kind}, {threads} threads, {cpu_model()})")
+        host = cpu_info()
+        log(f"CPU baseline ({cpu.kind}, {threads} threads of {host['nproc']}, {host['cpu']})")
         if cpu.kind == "reference":
             xs, sample = x, f"full workload M={GEMM_M} N={GEMM_N} K={GEMM_K}, median of 3 after a pool warm-up"
             cpu.matmul(wb[:64], Q5_K, x[:16], 64)
@@ -334,7 +539,8 @@ def main():
         parity = row_rel(y_gpu[: xs.shape[0]], y_cpu)
         log(f"CPU {t_cpu:.2f} s -> {cpu_tops * 1e3:.1f} GOPS; GPU vs CPU max row rel err {parity:.2e}")
         line["cpu_baseline"] = {"value": round(cpu_tops, 5), "unit": "TOPS", "cores": threads, "kind": cpu.kind,
-                                "sample": sample, "seconds": round(t_cpu, 3), "cpu": cpu_model()}
+                                "sample": sample, "seconds": round(t_cpu, 3), **host,
+                                "threads_rule": "min(affinity cores, 16): one GPU's share of host cores"}
         line["parity"] = {"max_row_rel_err_vs_cpu": parity, "tolerance": 1e-4, "rows_checked": int(xs.shape[0])}
         for k, v in matvec.items():
             reps = args.matvec_reps
@@ -351,6 +557,8 @@ def main():
                                                  "us": round(tc * 1e6, 1)}
             line["matvec"][k]["parity_max_row_rel_err"] = err
             log(f"CPU matvec {k}: {tc * 1e6:.0f} us; GPU vs CPU rel err {err:.2e}")
+        if keep:
+            cpu_workloads(cpu, types, workloads, keep)
     print(json.dumps(line), flush=True)
 
 

@@ -7,8 +7,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-# PIXHIP_LIBRARY names another build of the same library (same ABI) to load instead.
-LIBRARY = os.environ.get("PIXHIP_LIBRARY") or os.path.join(HERE, "libpixhip.so")
+LIBRARY = os.path.join(HERE, "libpixhip.so")
 
 OK = 0
 ERR_ARGUMENT = -1

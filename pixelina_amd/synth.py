@@ -11,6 +11,9 @@ these encoders produce valid blocks of those layouts for synthetic weights.
 Q8_0 weights use the reference's own quantizer semantics instead (the HIP
 quantizer, bit-exact with quantize_row_q8_0_ref).
 """
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 SEED_ACTIVATIONS = 1337  # PIXELINA_DEFAULT_SEED, src/storage.h:37
@@ -33,12 +36,30 @@ def splitmix_uniform(seed, n, start=0):
     return ((z >> np.uint64(11)).astype(np.float64) + 0.5) * (2.0 ** -53)
 
 
-def normal(seed, shape, std=1.0, chunk=1 << 22):
+def _threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _parallel(fn, items):
+    """fn over items on a thread pool (numpy releases the GIL in its loops)."""
+    items = list(items)
+    if len(items) <= 1:
+        return [fn(i) for i in items]
+    with ThreadPoolExecutor(min(_threads(), len(items))) as ex:
+        return list(ex.map(fn, items))
+
+
+def normal(seed, shape, std=1.0, chunk=1 << 20):
     """float32 N(0, std^2) of the given shape, Box-Muller pairs in row-major order."""
     n = int(np.prod(shape))
     out = np.empty(n, dtype=np.float32)
     pairs = (n + 1) // 2
-    for p0 in range(0, pairs, chunk):
+
+    def fill(p0):
         p1 = min(pairs, p0 + chunk)
         u = splitmix_uniform(seed, 2 * (p1 - p0), start=2 * p0)
         r = np.sqrt(-2.0 * np.log(u[0::2]))
@@ -48,6 +69,8 @@ def normal(seed, shape, std=1.0, chunk=1 << 22):
         z[1::2] = r * np.sin(a)
         lo, hi = 2 * p0, min(n, 2 * p1)
         out[lo:hi] = (z[: hi - lo] * std).astype(np.float32)
+
+    _parallel(fill, range(0, pairs, chunk))
     return out.reshape(shape)
 
 
@@ -66,6 +89,15 @@ def _f16_bits(v):
     return np.asarray(v, dtype=np.float32).astype(np.float16).view(np.uint16)
 
 
+def _by_rows(pack, w, rows=256):
+    """pack() over row slices (each row's blocks depend on that row alone), on a
+    thread pool; slices small enough for the temporaries to stay in cache."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    if w.shape[0] <= rows:
+        return pack(w)
+    return np.concatenate(_parallel(lambda r: pack(w[r:r + rows]), range(0, w.shape[0], rows)))
+
+
 def pack_q5_K(w):
     """float32 [rows, K] (K % 256 == 0) -> uint8 [rows, K/256*176] Q5_K blocks.
 
@@ -75,7 +107,10 @@ def pack_q5_K(w):
     clipped to [0,31].  Layout per src/kernels_quant.cpp:18-23, decode
     src/backend_cpu.cpp:56-79.
     """
-    w = np.ascontiguousarray(w, dtype=np.float32)
+    return _by_rows(_pack_q5_K, w)
+
+
+def _pack_q5_K(w):
     rows, k = w.shape
     assert k % 256 == 0
     x = w.reshape(rows, k // 256, 8, 32).astype(np.float64)
@@ -112,7 +147,10 @@ def pack_q6_K(w):
     round(step/d); q = round(x/(d*scale)) + 32 clipped to [0,63].  Layout per
     src/kernels_quant.cpp:24-29, decode src/backend_cpu.cpp:80-96.
     """
-    w = np.ascontiguousarray(w, dtype=np.float32)
+    return _by_rows(_pack_q6_K, w)
+
+
+def _pack_q6_K(w):
     rows, k = w.shape
     assert k % 256 == 0
     x = w.reshape(rows, k // 256, 16, 16).astype(np.float64)
