@@ -12,39 +12,39 @@
 // so the fp32 result is exact).  Per super-block the fp32 epilogue is
 // y += yd * (wd * S - wdmin * Mn).
 //
-// Tiling: a workgroup of 8 waves (2 per SIMD) owns a 256 (tokens) x 128
-// (features) tile; wave w owns the 64 x 64 block at tokens 64*(w%4), features
-// 64*(w/4): two token tiles x two feature tiles of 32 x 32, each with hi, lo and
-// fp32 accumulators (192 registers).  A wave keeps the operands of one 32-value
-// sub-block in registers (two activation and four weight fragments) and reads
-// the next sub-block's fragments as soon as the MFMAs of the current one have
-// consumed each register, so its matrix-core work runs from registers while the
-// next reads are in flight.
+// Tiling: a workgroup of 8 waves (2 per SIMD: waves w and w+4 share one)
+// owns a 256 (tokens) x 128 (features) tile; wave w owns the 64 x 64 block at
+// tokens 64*(w%4), features 64*(w/4): two token tiles x two feature tiles of
+// 32 x 32, each with hi, lo and fp32 accumulators (192 registers).  A wave
+// keeps the operands of one 32-value sub-block in registers (two activation
+// fragments, double-buffered, and four weight fragments) and reads the next
+// sub-block's fragments as registers free up, each at least four MFMAs before
+// its use.
 //
-// Data movement: K advances in 64-value stages through a 4-slot LDS ring (per
-// slot 16 KB of activations, 16 KB of weight planes) filled by
-// buffer_load_dwordx4 ... lds (HBM/L2 -> LDS without registers).  The operand
-// planes are tiled in HBM so that one DMA instruction reads one contiguous
-// 1 KB block (16 rows x 64 values): whole 128-byte lines, which the memory
-// path delivers at twice the rate of the 16 half lines a row-major plane
-// gives.  In LDS, rows are four 16-byte pieces, piece c of row r at position
-// 4r + (c ^ ((r>>2)&3)), which
-// makes the ds_read_b128 operand reads (lane l: row l%32, piece 2s + l/32)
-// free of bank conflicts.  Per 256-value super-block the epilogue inputs (yd,
-// wd, 16-value sums, minima, wdmin) ride in a double-buffered LDS region.
+// Data movement: K advances in 64-value stages (16 KB of activations, 16 KB of
+// weight planes per stage) through LDS rings filled by buffer_load_dwordx4 ...
+// lds (L2 -> LDS without registers): five activation slots, four weight slots.
+// The operand planes are tiled in HBM so that one DMA instruction reads one
+// contiguous 1 KB block (16 rows x 64 values): whole 128-byte lines, which the
+// memory path delivers at twice the rate of the 16 half lines a row-major
+// plane gives.  In LDS, rows are four 16-byte pieces, piece c of row r at
+// position 4r + (c ^ ((r>>2)&3)), which makes the ds_read_b128 operand reads
+// (lane l: row l%32, piece 2s + l/32) free of bank conflicts.  The epilogue
+// inputs of one super-block (yd, wd, 16-value sums, minima, wdmin) sit in a
+// region after the rings.
 //
-// Synchronisation: one s_barrier per stage, placed after the first four MFMAs
-// of the stage's second sub-block (issued from registers, so the matrix core
-// stays busy while a wave waits).  By that barrier every wave has read all of
-// stage c, so its slot is refilled with stage c+4 right after it (prefetch
-// distance four stages); before it, each wave waits for its own DMAs of stage
-// c+1.  A wave's DMAs of a window are spread between its MFMAs.
+// Synchronisation: one s_barrier per interval of two stages; the two wave
+// groups run one stage apart so that their super-block epilogues fall at
+// different points of an interval (the schedule is described at wait_all).
+// A wave drains its own DMAs and LDS reads before each barrier.
 //
-// What bounds it (measured with cycle counters around each phase, Q5_K at
-// 4096 x 3840 x 10240): with the tiled planes the DMAs of a stage take
-// ~1240 cycles alone and MFMAs + DMAs ~1380 (1024 is the MFMA time); the
-// super-block epilogue, ~320 vector instructions per wave that both waves of a
-// SIMD run in the same window, adds the rest (~2700 cycles per stage).
+// What bounds it (Q5_K, 4096 x 3840 x 10240, ~320 us; variants that drop one
+// component each): the MFMAs with their LDS operand reads alone take ~210 us
+// (the int8 matrix-core time at the ~2.1 GHz this load runs at is ~145 us;
+// the tile prologues and output stores of five tiles per CU are part of the
+// difference), the super-block epilogue adds ~55 us and the L2 -> LDS
+// traffic (2.5 GB per launch, 78% L2 hits) ~45 us.  Hardware counters put the
+// matrix core at 49% busy.
 #include <type_traits>
 
 #include "pixhip_device.h"
@@ -57,14 +57,14 @@ namespace {
 
 constexpr int kBM = PIX_GEMM_MTILE, kBN = PIX_GEMM_NTILE, kKC = 64;
 constexpr int kWaves = 8, kThreads = 64 * kWaves;
-constexpr int kStages = 4;                  // ring slots
+constexpr int kASlots = 5;                  // activation ring slots
+constexpr int kWSlots = 4;                  // weight ring slots
 constexpr int kChunk = 1024;                // bytes written by one DMA instruction (64 lanes x 16 B)
 constexpr int kHalf = 16384;                // activation (or weight) bytes of one stage
-constexpr int kWRing = kStages * kHalf;     // weight ring after the activation ring
+constexpr int kWRing = kASlots * kHalf;     // weight ring after the activation ring
+constexpr int kScaleAt = kWRing + kWSlots * kHalf;  // one super-block's epilogue inputs after the rings
 constexpr int kPlane = 8192;                // lo plane after hi within a weight slot
 constexpr int kSBC = PIX_QK / kKC;          // stages per super-block
-constexpr int kStageDma = 4;                // DMAs per wave per stage (32 chunks / 8 waves)
-constexpr int kScaleDma = 2;                // DMAs per wave per super-block of scale data
 static_assert(kWaves * 64 == kThreads && kBM == 4 * 64 && kBN == 2 * 64, "wave grid covers the tile");
 
 // Scale region of one super-block (16-B slots; DMA chunk c fills slots 64c..64c+63):
@@ -144,15 +144,17 @@ __device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi
 struct Ctx {
     int m0, n0, wave, wm, wn, K;
     int c_begin, nchunks;   // this workgroup's stages c_begin .. nchunks-1 (c_begin starts a super-block)
+    bool lag;               // group 1 (waves 4-7): one stage behind group 0
     uint32_t oa0;           // per-lane LDS offset of the wave's activation fragments (sub-block 0 of a stage;
                             // sub-block 1 is oa0 ^ 32)
     uint32_t ow0;           // same for the weight fragments (absolute, includes the weight ring base)
     uint32_t vo_tile;       // per-lane DMA source offset within a 1 KB tile (16 rows x 64 B)
-    Rsrc rx, rxd, rxbs, rwh, rwl, rwd, rwdm, rwmn, rnull;
+    Rsrc rx, rxd, rxbs, rwh, rwl, rwd, rwdm, rwmn;
 };
 
 struct Opnd {
-    v4i a[2], h[2], l[2];
+    v4i a[2][2];     // [sub-block parity][token tile]: the next sub-block's activations load into the other half
+    v4i h[2], l[2];  // [feature tile] of the hi and lo planes
 };
 
 struct Acc {
@@ -160,18 +162,20 @@ struct Acc {
     v16f y[2][2];
 };
 
-// Fragments of sub-block s of the stage in ring slot P.
-template <int P, int S> __device__ __forceinline__ v4i frag_a(const uint8_t* lds, const Ctx& x, int i)
+// Byte offset of stage s's slot in the activation ring (runtime: five slots).
+__device__ __forceinline__ uint32_t a_off(const Ctx& x, int s) { return (uint32_t)((s - x.c_begin) % kASlots) * (uint32_t)kHalf; }
+
+// Fragments of sub-block S of a stage: activations at ring offset aoff, weights
+// in ring slot PW (the stage index mod 4).
+template <int S> __device__ __forceinline__ v4i frag_a(const uint8_t* lds, const Ctx& x, uint32_t aoff, int i)
 {
-    return *reinterpret_cast<const v4i*>(lds + (S? x.oa0 ^ 32u : x.oa0) + P * kHalf + i * 2048);
+    return *reinterpret_cast<const v4i*>(lds + (S? x.oa0 ^ 32u : x.oa0) + aoff + i * 2048);
 }
-template <int P, int S> __device__ __forceinline__ v4i frag_w(const uint8_t* lds, const Ctx& x, int j, int plane)
+template <int PW, int S> __device__ __forceinline__ v4i frag_w(const uint8_t* lds, const Ctx& x, int j, int plane)
 {
-    return *reinterpret_cast<const v4i*>(lds + (S? x.ow0 ^ 32u : x.ow0) + P * kHalf + j * 2048 + plane * kPlane);
+    return *reinterpret_cast<const v4i*>(lds + (S? x.ow0 ^ 32u : x.ow0) + PW * kHalf + j * 2048 + plane * kPlane);
 }
 
-// DMA of stage c into ring slot P: this wave's chunks are wave, wave+8 (16
-// activation rows each), wave+16 (16 rows of the hi plane) and wave+24 (lo).
 // Byte offset of the 1 KB tile of rows r0..r0+15 (r0 a multiple of 16) and
 // stage c in a tiled plane (pixhip_internal.h, tiled_offset).
 __device__ __forceinline__ uint32_t tile_at(const Ctx& x, int r0, int c)
@@ -179,21 +183,27 @@ __device__ __forceinline__ uint32_t tile_at(const Ctx& x, int r0, int c)
     return ((uint32_t)(r0 >> 4) * (uint32_t)(x.K >> 6) + (uint32_t)c) * 1024u;
 }
 
-template <int P> __device__ __forceinline__ void issue_stage(const Ctx& x, uint8_t* lds, int c)
+// DMAs of stage c: the wave's activation chunks are wave and wave+8 (16 token
+// rows each), into the activation ring; its weight chunks are the 16 rows of
+// features 16*wave .. of the hi and the lo plane, into weight slot c % 4 (the
+// waves of group 0 load its features 0-63, those of group 1 features 64-127).
+__device__ __forceinline__ void issue_act(const Ctx& x, uint8_t* lds, int c)
 {
     const int w = x.wave;
-    dma(x.rx,lds + P * kHalf + w * kChunk,x.vo_tile,tile_at(x,x.m0 + w * 16,c));
-    dma(x.rx,lds + P * kHalf + (w + 8) * kChunk,x.vo_tile,tile_at(x,x.m0 + (w + 8) * 16,c));
-    dma(x.rwh,lds + kWRing + P * kHalf + w * kChunk,x.vo_tile,tile_at(x,x.n0 + w * 16,c));
-    dma(x.rwl,lds + kWRing + P * kHalf + kPlane + w * kChunk,x.vo_tile,tile_at(x,x.n0 + w * 16,c));
+    uint8_t* slot = lds + a_off(x,c);
+    dma(x.rx,slot + w * kChunk,x.vo_tile,tile_at(x,x.m0 + w * 16,c));
+    dma(x.rx,slot + (w + 8) * kChunk,x.vo_tile,tile_at(x,x.m0 + (w + 8) * 16,c));
+}
+template <int PW> __device__ __forceinline__ void issue_w(const Ctx& x, uint8_t* lds, int c)
+{
+    const int w = x.wave;
+    dma(x.rwh,lds + kWRing + PW * kHalf + w * kChunk,x.vo_tile,tile_at(x,x.n0 + w * 16,c));
+    dma(x.rwl,lds + kWRing + PW * kHalf + kPlane + w * kChunk,x.vo_tile,tile_at(x,x.n0 + w * 16,c));
 }
 
 // DMA of super-block b's epilogue inputs into `sc`: chunk q of the 13 (2 for
-// Q6_K) is issued by wave q % 8 as its (q / 8)-th scale DMA; waves without a
-// chunk load nothing into the discard chunk, so that every wave issues the
-// same number of DMAs (the vmcnt waits count them).
-template <bool Q5> __device__ __forceinline__ void issue_scale_chunk(const Args& g, const Ctx& x, int b, int chunk, uint8_t* sc,
-                                                                    uint8_t* discard)
+// Q6_K) is issued by wave q % 8.
+template <bool Q5> __device__ __forceinline__ void issue_scale_chunk(const Args& g, const Ctx& x, int b, int chunk, uint8_t* sc)
 {
     const uint32_t lane = lane_id();
     if (chunk == 0) {
@@ -207,68 +217,78 @@ template <bool Q5> __device__ __forceinline__ void issue_scale_chunk(const Args&
         dma(x.rwmn,sc + chunk * kChunk,16u * lane,(uint32_t)(b * g.Npad + x.n0 + (chunk - 10) * 64) * 16u);
     } else if (Q5 && chunk == 12) {
         dma(x.rwdm,sc + chunk * kChunk,16u * (lane & 31),(uint32_t)(b * g.Npad + x.n0) * 4u);
-    } else {
-        dma(x.rnull,discard,0,0);
     }
 }
-template <bool Q5> __device__ __forceinline__ void issue_scales(const Args& g, const Ctx& x, int b, uint8_t* sc, uint8_t* discard)
+template <bool Q5> __device__ __forceinline__ void issue_scales(const Args& g, const Ctx& x, int b, uint8_t* sc)
 {
-    issue_scale_chunk<Q5>(g,x,b,x.wave,sc,discard);
-    issue_scale_chunk<Q5>(g,x,b,x.wave + 8 < scale_chunks<Q5>()? x.wave + 8 : 99,sc,discard);
+    if (x.wave < scale_chunks<Q5>()) issue_scale_chunk<Q5>(g,x,b,x.wave,sc);
+    if (x.wave + 8 < scale_chunks<Q5>()) issue_scale_chunk<Q5>(g,x,b,x.wave + 8,sc);
 }
 
-// MFMAs of one sub-block from R; when READ, the fragments of the next
-// sub-block (sub-block NS of the stage in slot NP) replace each register as
-// soon as the MFMAs that read it have been issued.  f0, f1 and f2 run after the
-// first four, the sixth and the eighth MFMA (the barrier and the DMAs of a
-// window go there, so that the wave has MFMAs queued while it waits).
+// MFMAs of sub-block S (0 or 1 within its stage) from R, in the order hi00,
+// hi10, lo00, lo10, hi01, hi11, lo01, lo11 (plane, token tile, feature tile):
+// each weight fragment is free after two MFMAs.  When READ, the fragments of
+// the next sub-block (sub-block 1-S of the stage at activation offset naoff and
+// weight slot NPW) load as registers free up: its activations into the other
+// half of R.a (at the start when EARLY, else after f0), each weight fragment
+// after its last use here, so every load has at least four MFMAs to land.
+// f0, f1 and f2 run after the fourth, sixth and eighth MFMA (a barrier and the
+// DMAs of an interval go there, with MFMAs queued while the wave waits; the
+// loads of a next stage follow f0).
 struct Nop {
     __device__ __forceinline__ void operator()() const {}
 };
-template <bool FRESH, bool READ, int NP, int NS, class F0 = Nop, class F1 = Nop, class F2 = Nop>
-__device__ __forceinline__ void sub_block(Acc& acc, Opnd& R, const uint8_t* lds, const Ctx& x, F0 f0 = {}, F1 f1 = {}, F2 f2 = {})
+template <bool FRESH, int S, bool READ, bool EARLY, int NPW, class F0 = Nop, class F1 = Nop, class F2 = Nop>
+__device__ __forceinline__ void sub_block(Acc& acc, Opnd& R, const uint8_t* lds, const Ctx& x, uint32_t naoff, F0 f0 = {}, F1 f1 = {},
+                                          F2 f2 = {})
 {
+    constexpr int NS = 1 - S;
     const v16i z = {};
-#define PIX_MF(i, j)                                                                                           \
-    acc.hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[i],R.h[j],FRESH? z : acc.hi[i][j],0,0,0);         \
-    acc.lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[i],R.l[j],FRESH? z : acc.lo[i][j],0,0,0)
-    PIX_MF(0,0);
-    PIX_MF(0,1);
+    if constexpr (READ && EARLY) {
+        R.a[NS][0] = frag_a<NS>(lds,x,naoff,0);
+        R.a[NS][1] = frag_a<NS>(lds,x,naoff,1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    acc.hi[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][0],R.h[0],FRESH? z : acc.hi[0][0],0,0,0);
+    acc.hi[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][1],R.h[0],FRESH? z : acc.hi[1][0],0,0,0);
+    acc.lo[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][0],R.l[0],FRESH? z : acc.lo[0][0],0,0,0);
+    acc.lo[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][1],R.l[0],FRESH? z : acc.lo[1][0],0,0,0);
     __builtin_amdgcn_sched_barrier(0);
     f0();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (READ) R.a[0] = frag_a<NP,NS>(lds,x,0);
+    if constexpr (READ) {
+        if constexpr (!EARLY) {
+            R.a[NS][0] = frag_a<NS>(lds,x,naoff,0);
+            R.a[NS][1] = frag_a<NS>(lds,x,naoff,1);
+        }
+        R.h[0] = frag_w<NPW,NS>(lds,x,0,0);
+        R.l[0] = frag_w<NPW,NS>(lds,x,0,1);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    PIX_MF(1,0);
+    acc.hi[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][0],R.h[1],FRESH? z : acc.hi[0][1],0,0,0);
+    acc.hi[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][1],R.h[1],FRESH? z : acc.hi[1][1],0,0,0);
     __builtin_amdgcn_sched_barrier(0);
     f1();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (READ) {
-        R.h[0] = frag_w<NP,NS>(lds,x,0,0);
-        R.l[0] = frag_w<NP,NS>(lds,x,0,1);
-    }
+    if constexpr (READ) R.h[1] = frag_w<NPW,NS>(lds,x,1,0);
     __builtin_amdgcn_sched_barrier(0);
-    PIX_MF(1,1);
+    acc.lo[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][0],R.l[1],FRESH? z : acc.lo[0][1],0,0,0);
+    acc.lo[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(R.a[S][1],R.l[1],FRESH? z : acc.lo[1][1],0,0,0);
     __builtin_amdgcn_sched_barrier(0);
     f2();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (READ) {
-        R.a[1] = frag_a<NP,NS>(lds,x,1);
-        R.h[1] = frag_w<NP,NS>(lds,x,1,0);
-        R.l[1] = frag_w<NP,NS>(lds,x,1,1);
-    }
+    if constexpr (READ) R.l[1] = frag_w<NPW,NS>(lds,x,1,1);
     __builtin_amdgcn_sched_barrier(0);
-#undef PIX_MF
 }
 
-template <int NP, int NS> __device__ __forceinline__ void read_all(Opnd& R, const uint8_t* lds, const Ctx& x)
+template <int NPW> __device__ __forceinline__ void read_all(Opnd& R, const uint8_t* lds, const Ctx& x, uint32_t naoff)
 {
     __asm__ volatile("" ::: "memory");  // not hoisted into a preceding epilogue
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        R.a[i] = frag_a<NP,NS>(lds,x,i);
-        R.h[i] = frag_w<NP,NS>(lds,x,i,0);
-        R.l[i] = frag_w<NP,NS>(lds,x,i,1);
+        R.a[0][i] = frag_a<0>(lds,x,naoff,i);
+        R.h[i] = frag_w<NPW,0>(lds,x,i,0);
+        R.l[i] = frag_w<NPW,0>(lds,x,i,1);
     }
 }
 
@@ -325,109 +345,208 @@ __device__ __forceinline__ void sb_epilogue(const Args& g, const Ctx& x, int b, 
     }
 }
 
+// The fp32 epilogue of super-block b for the wave's four tiles, arranged for
+// latency: every LDS read it needs is issued first; the integer sums of all
+// four tiles become t = S * wd (the hi/lo registers are free afterwards,
+// until the next super-block's first MFMAs); the four minimum-term MFMAs are
+// issued back to back; then y += yd * (t - wdm * Mn).
+template <bool Q5>
+__device__ __forceinline__ void epilogue_y(const Ctx& x, Acc& acc, const uint8_t* __restrict__ sc)
+{
+    __asm__ volatile("" ::: "memory");
+    const uint32_t ln = lane_id();
+    const int lg = (int)(ln >> 5), lr = (int)(ln & 31);
+    const float* syd = reinterpret_cast<const float*>(sc + 16 * kSlotYd);
+    float wd[2], nwm[2] = {0.0f,0.0f};
+    v8h mnB[2], bsA[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = x.wn * 64 + j * 32 + lr;
+        wd[j] = reinterpret_cast<const float*>(sc + 16 * kSlotWd)[col];
+        if constexpr (Q5) {
+            nwm[j] = -reinterpret_cast<const float*>(sc + 16 * kSlotWdm)[col];
+            mnB[j] = *reinterpret_cast<const v8h*>(sc + 16 * (kSlotMn + col));
+        }
+    }
+    if constexpr (Q5) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) bsA[i] = *reinterpret_cast<const v8h*>(sc + 16 * (kSlotBs + 2 * (x.wm * 64 + i * 32 + lr) + lg));
+    }
+    float4 yd[4];  // token rows row0 + 8q .. +3 of the first token tile
+    const int row0 = x.wm * 64 + 4 * lg;
+#pragma unroll
+    for (int q = 0; q < 4; q++) yd[q] = *reinterpret_cast<const float4*>(syd + row0 + 8 * q);
+    v16f t[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) t[i][j][r] = (float)(acc.hi[i][j][r] * 64 + acc.lo[i][j][r]) * wd[j];
+    const v16f fzero = {};
+    v16f mt[2];
+    if constexpr (Q5) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) mt[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsA[0],mnB[j],fzero,0,0,0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        if (i == 1) {
+            if constexpr (Q5) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) mt[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsA[1],mnB[j],fzero,0,0,0);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) yd[q] = *reinterpret_cast<const float4*>(syd + row0 + 32 + 8 * q);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float yq[4] = {yd[q].x,yd[q].y,yd[q].z,yd[q].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int r = 4 * q + e;
+                    acc.y[i][j][r] = __builtin_fmaf(yq[e],Q5? __builtin_fmaf(mt[j][r],nwm[j],t[i][j][r]) : t[i][j][r],acc.y[i][j][r]);
+                }
+            }
+            __asm__ volatile("" : "+v"(acc.y[i][j]));
+        }
+    }
+}
+
 template <bool Q5, bool SUMS>
 __device__ __forceinline__ void epilogue(const Args& g, const Ctx& x, int b, Acc& acc, const uint8_t* sc)
 {
-    // One tile at a time: the scheduler would otherwise hoist the LDS reads
-    // and minimum-term MFMAs of all four tiles and run out of registers.
-    sb_epilogue<Q5,SUMS,0,0>(g,x,b,acc,sc);
-    __builtin_amdgcn_sched_barrier(0);
-    sb_epilogue<Q5,SUMS,0,1>(g,x,b,acc,sc);
-    __builtin_amdgcn_sched_barrier(0);
-    sb_epilogue<Q5,SUMS,1,0>(g,x,b,acc,sc);
-    __builtin_amdgcn_sched_barrier(0);
-    sb_epilogue<Q5,SUMS,1,1>(g,x,b,acc,sc);
+    if constexpr (!SUMS) {
+        epilogue_y<Q5>(x,acc,sc);
+    } else {
+        // One tile at a time (the integer-sum variant is a test path).
+        sb_epilogue<Q5,SUMS,0,0>(g,x,b,acc,sc);
+        __builtin_amdgcn_sched_barrier(0);
+        sb_epilogue<Q5,SUMS,0,1>(g,x,b,acc,sc);
+        __builtin_amdgcn_sched_barrier(0);
+        sb_epilogue<Q5,SUMS,1,0>(g,x,b,acc,sc);
+        __builtin_amdgcn_sched_barrier(0);
+        sb_epilogue<Q5,SUMS,1,1>(g,x,b,acc,sc);
+    }
 }
 
-// DMAs a wave issues in the window after the barrier of stage c (phase P =
-// c % 4): the four of stage c+DIST, plus the scale data of the next
-// super-block in phase 1.
-template <int P> constexpr int issued_in() { return kStageDma + (P == 1? kScaleDma : 0); }
-
-// Before the barrier of stage c every wave's DMAs of stage c+1 have landed:
-// only those issued in the windows of stages c-DIST+2 .. c-1 may be pending
-// (none near the end of the K range; the integer-sum variant also stores
-// inside the loop, so it drains everything).
-template <bool SUMS, int P, int DIST> __device__ __forceinline__ void wait_stage(int c, int C)
+// The schedule.  K advances in 64-value stages; the waves synchronise once per
+// interval of two stages.  Group 0 (waves 0-3, features 0-63 of the tile)
+// works on stages C0+2k and C0+2k+1 in interval k; group 1 (waves 4-7,
+// features 64-127) runs one stage behind, on C0+2k-1 and C0+2k.  So the two
+// waves of a SIMD (one of each group) finish a super-block at different points
+// of an interval: group 0's super-block epilogue (vector ALU) runs at the start
+// of the interval while group 1 issues MFMAs, group 1's in its middle while
+// group 0 does.
+//
+// Between barriers k-1 and k the activation ring holds stages C0+2k-1 ..
+// C0+2k+1 (read in interval k) and C0+2k+2, C0+2k+3 (landed by barrier k-1);
+// each group's weight slots hold its two stages of interval k and two of
+// interval k+1.  After barrier k every wave issues its share of interval k+2:
+// activations C0+2k+4, C0+2k+5 into the slots of C0+2k-1 and C0+2k (read for
+// the last time in interval k) and its weight rows of the same stages (group
+// 0) or C0+2k+3, C0+2k+4 (group 1), into the slots of the group's stages of
+// interval k.  Everything a wave issues in an interval has landed before the
+// barrier that ends it.  The epilogue inputs of super-block b are read in
+// interval 2b+2 (relative to C0) and those of b+1 loaded in interval 2b+3.
+//
+// Group 0's barriers sit in its stages C0+2k+1, group 1's in C0+2k; in a
+// wave's barrier stage s the interval's DMAs are activations s+3, s+4 (group
+// 0) or s+4, s+5 (group 1) and weights s+3, s+4.
+template <bool SUMS> __device__ __forceinline__ void wait_all()
 {
-    if (!SUMS && c + DIST - 1 < C) {
-        if constexpr (DIST == 3) wait_vmcnt<issued_in<(P + 3) % 4>()>();
-        else wait_vmcnt<issued_in<(P + 3) % 4>() + issued_in<(P + 2) % 4>()>();
-    } else {
-        wait_vmcnt<0>();
-    }
+    wait_vmcnt<0>();
     wait_lgkm0();
 }
 
-// Part PART (0..2) of the window's DMAs: 0 the two activation chunks of stage
-// c+DIST, 1 its hi-plane chunk (and the first scale chunk in phase 1), 2 its
-// lo-plane chunk (and the second).  Stage c+DIST goes into the slot whose stage
-// no wave reads any more after this barrier.
-template <bool Q5, int P, int DIST, int PART>
-__device__ __forceinline__ void window_dma(const Args& g, const Ctx& x, uint8_t* lds, int c, uint8_t* scale_base, uint8_t* discard)
+// Part PART (0..2) of the DMAs after the barrier in stage s (weight slot PW =
+// s % 4): 0 the activations of the interval's first stage, 1 those of the
+// second and the weights of the first, 2 the weights of the second and, in
+// the interval that loads them, the next super-block's epilogue inputs.
+template <bool Q5, int PW, int PART>
+__device__ __forceinline__ void window_dma(const Args& g, const Ctx& x, uint8_t* lds, int s, uint8_t* sc)
 {
-    constexpr int slot = (P + DIST) % 4;
-    const int st = c + DIST;
-    if (st < x.nchunks) {
-        const int w = x.wave;
-        if constexpr (PART == 0) {
-            dma(x.rx,lds + slot * kHalf + w * kChunk,x.vo_tile,tile_at(x,x.m0 + w * 16,st));
-            dma(x.rx,lds + slot * kHalf + (w + 8) * kChunk,x.vo_tile,tile_at(x,x.m0 + (w + 8) * 16,st));
-        } else if constexpr (PART == 1) {
-            dma(x.rwh,lds + kWRing + slot * kHalf + w * kChunk,x.vo_tile,tile_at(x,x.n0 + w * 16,st));
-        } else {
-            dma(x.rwl,lds + kWRing + slot * kHalf + kPlane + w * kChunk,x.vo_tile,tile_at(x,x.n0 + w * 16,st));
-        }
-    }
-    if constexpr (P == 1 && PART > 0) {
-        constexpr int kScale = scale_bytes<Q5>();
-        const int b = c / kSBC + 1;
-        if (b * kSBC < x.nchunks) {
-            const int chunk = PART == 1? x.wave : (x.wave + 8 < scale_chunks<Q5>()? x.wave + 8 : 99);
-            issue_scale_chunk<Q5>(g,x,b,chunk,scale_base + (b & 1) * kScale,discard);
-        }
+    const int a0 = s + 3 + (x.lag? 1 : 0), w0 = s + 3;
+    if constexpr (PART == 0) {
+        if (a0 < x.nchunks) issue_act(x,lds,a0);
+    } else if constexpr (PART == 1) {
+        if (a0 + 1 < x.nchunks) issue_act(x,lds,a0 + 1);
+        if (w0 < x.nchunks) issue_w<(PW + 3) % 4>(x,lds,w0);
+    } else {
+        if (w0 + 1 < x.nchunks) issue_w<PW>(x,lds,w0 + 1);
+        // Super-block s / 4 (the one stage s belongs to) is loaded in the
+        // interval after barrier 2b+2 relative to C0: group 0's barrier stage
+        // C0+4b+5, group 1's C0+4b+4; the first super-block comes with the
+        // prologue.
+        if (PW == (x.lag? 0 : 1) && s - PW > x.c_begin) issue_scales<Q5>(g,x,s / kSBC,sc);
     }
 }
 
-// One stage per wave: [MFMAs c.0, read c.1] [4 MFMAs of c.1, barrier c, the
-// rest of c.1 with the window's DMAs, read c+1.0] [epilogue at the end of a
-// super-block].  The barrier sits after MFMAs a wave can issue from
-// registers, so the matrix core has work queued while the wave waits.
-template <bool Q5, bool SUMS, int P, int DIST>
-__device__ __forceinline__ void wave_iter(const Args& g, const Ctx& x, Acc& acc, Opnd& R, uint8_t* lds, int c, uint8_t* scale_base,
-                                          uint8_t* discard)
+// One stage s of a wave: sub-block 0 from registers (reading sub-block 1),
+// then sub-block 1 (reading sub-block 0 of stage s+1 when READ_NEXT) with the
+// hooks f0, f1, f2.
+template <bool FRESH, bool READ_NEXT, bool BARRIER, int PW, class F0 = Nop, class F1 = Nop, class F2 = Nop>
+__device__ __forceinline__ void stage(Acc& acc, Opnd& R, const uint8_t* lds, const Ctx& x, int s, F0 f0 = {}, F1 f1 = {}, F2 f2 = {})
 {
-    constexpr int kScale = scale_bytes<Q5>();
-    sub_block<P == 0,true,P,1>(acc,R,lds,x);
+    sub_block<FRESH,0,true,true,PW>(acc,R,lds,x,a_off(x,s));
+    sub_block<false,1,READ_NEXT,!BARRIER,(PW + 1) % 4>(acc,R,lds,x,READ_NEXT? a_off(x,s + 1) : 0u,f0,f1,f2);
+}
+
+// Stage s of a super-block (PW = s % 4); group 0 has its barrier in stages 1
+// and 3 of a super-block, group 1 in stages 0 and 2.  The barrier comes after
+// the first four MFMAs of sub-block 1 (issued from registers, so the matrix
+// core has work queued while the wave waits), the interval's DMAs spread over
+// the rest of the sub-block.
+template <bool Q5, bool SUMS, bool FRESH, bool READ_NEXT, int PW>
+__device__ __forceinline__ void sb_stage(const Args& g, Acc& acc, Opnd& R, uint8_t* lds, const Ctx& x, int s, uint8_t* sc)
+{
+    const bool here = x.lag == ((PW & 1) == 0);  // (wave-uniform)
     auto f0 = [&]() {
-        wait_stage<SUMS,P,DIST>(c,x.nchunks);
-        __builtin_amdgcn_s_barrier();
-        window_dma<Q5,P,DIST,0>(g,x,lds,c,scale_base,discard);
+        if (here) {
+            wait_all<SUMS>();
+            __builtin_amdgcn_s_barrier();
+            window_dma<Q5,PW,0>(g,x,lds,s,sc);
+        }
     };
-    auto f1 = [&]() { window_dma<Q5,P,DIST,1>(g,x,lds,c,scale_base,discard); };
-    auto f2 = [&]() { window_dma<Q5,P,DIST,2>(g,x,lds,c,scale_base,discard); };
-    // (K ranges are whole super-blocks, so stage c+1 exists unless P == 3.)
-    if constexpr (P != kSBC - 1) {
-        sub_block<false,true,(P + 1) % 4,0>(acc,R,lds,x,f0,f1,f2);
-    } else {
-        sub_block<false,false,0,0>(acc,R,lds,x,f0,f1,f2);
-        const int b = c / kSBC;
-        epilogue<Q5,SUMS>(g,x,b,acc,scale_base + (b & 1) * kScale);
-        __builtin_amdgcn_sched_barrier(0);
-        // Unconditional (after the last stage it reads a stale slot, unused):
-        // a conditional read would keep the consumed fragments live through
-        // the epilogue.
-        read_all<0,0>(R,lds,x);
-    }
+    auto f1 = [&]() {
+        if (here) window_dma<Q5,PW,1>(g,x,lds,s,sc);
+    };
+    auto f2 = [&]() {
+        if (here) window_dma<Q5,PW,2>(g,x,lds,s,sc);
+    };
+    // (whether this wave's barrier is in this stage is only known at run time:
+    // the next stage's activations load after f0 in either case)
+    stage<FRESH,READ_NEXT,true,PW>(acc,R,lds,x,s,f0,f1,f2);
+}
+
+// One super-block at stage s0 (R holds sub-block 0 of s0): stages s0 .. s0+3,
+// the epilogue (group 0: at the start of the interval its barrier in s0+3
+// opens; group 1: in the middle of the interval its barrier in s0+2 opened),
+// then the first fragments of the next super-block (both groups: in the same
+// interval as the epilogue).
+template <bool Q5, bool SUMS>
+__device__ __forceinline__ void super_block(const Args& g, Acc& acc, Opnd& R, uint8_t* lds, const Ctx& x, int s0, uint8_t* sc)
+{
+    sb_stage<Q5,SUMS,true,true,0>(g,acc,R,lds,x,s0,sc);
+    sb_stage<Q5,SUMS,false,true,1>(g,acc,R,lds,x,s0 + 1,sc);
+    sb_stage<Q5,SUMS,false,true,2>(g,acc,R,lds,x,s0 + 2,sc);
+    sb_stage<Q5,SUMS,false,false,3>(g,acc,R,lds,x,s0 + 3,sc);
+    epilogue<Q5,SUMS>(g,x,s0 / kSBC,acc,sc);
+    __builtin_amdgcn_sched_barrier(0);
+    // Unconditional (after the last super-block it reads a stale slot,
+    // unused): a conditional read would keep the consumed fragments live
+    // through the epilogue.
+    read_all<0>(R,lds,x,a_off(x,s0 + 4));
 }
 
 template <bool Q5, bool SUMS>
 __global__ __launch_bounds__(kThreads,1) void gemm_kq_kernel(Args g)
 {
     constexpr int kScale = scale_bytes<Q5>();
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kWRing + 2 * kScale + kChunk];
-    uint8_t* const scale_base = lds + 2 * kWRing;
-    uint8_t* const discard = scale_base + 2 * kScale;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kScaleAt + kScale];
+    uint8_t* const sc = lds + kScaleAt;
 
     // Whole tiles first (XCD-remapped), then the split tiles' pieces in launch
     // order (consecutive pieces land on different XCDs).
@@ -447,6 +566,7 @@ __global__ __launch_bounds__(kThreads,1) void gemm_kq_kernel(Args g)
     x.wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     x.wm = x.wave % 4;
     x.wn = x.wave / 4;
+    x.lag = x.wn != 0;
     x.K = g.K;
     {
         // lane l reads row l%32, piece (l/32) ^ ((l%32 >> 2) & 3) of sub-block 0; sub-block 1 is that ^ 2
@@ -471,7 +591,6 @@ __global__ __launch_bounds__(kThreads,1) void gemm_kq_kernel(Args g)
         x.rxbs = make_rsrc(Q5? (const void*)g.xbs : (const void*)g.xq,Q5? mp * (K / 16) * 2 : 0);
         x.rwmn = make_rsrc(Q5? (const void*)g.wmn : (const void*)g.xq,Q5? nblk * np * 16 : 0);
         x.rwdm = make_rsrc(Q5? (const void*)g.wdm : (const void*)g.xq,Q5? nblk * np * 4 : 0);
-        x.rnull = make_rsrc(g.xq,0);
     }
 
     // (hi and lo are written fresh by the first MFMAs of every super-block.)
@@ -482,25 +601,28 @@ __global__ __launch_bounds__(kThreads,1) void gemm_kq_kernel(Args g)
         for (int j = 0; j < 2; j++) acc.y[i][j] = v16f{};
 
     const int C0 = x.c_begin, C = x.nchunks;  // C0 is a multiple of kSBC; C - C0 >= kSBC
-    constexpr int DIST = 4;                     // prefetch distance in stages
-    // Prologue: stages C0 .. C0+DIST-1 and the first super-block's scales;
-    // stage C0 is read before the first barrier of the loop.
-    issue_stage<0>(x,lds,C0);
-    issue_scales<Q5>(g,x,C0 / kSBC,scale_base + ((C0 / kSBC) & 1) * kScale,discard);
-    issue_stage<1>(x,lds,C0 + 1);
-    issue_stage<2>(x,lds,C0 + 2);
-    issue_stage<3>(x,lds,C0 + 3);
-    wait_vmcnt<(DIST - 1) * kStageDma>();
+    // Prologue: intervals 0 and 1 (activations C0 .. C0+3; weights C0 ..
+    // C0+3 for group 0, C0 .. C0+2 for group 1) and the first super-block's
+    // epilogue inputs.  Interval 0's chunks are issued first: before the
+    // prologue barrier they have landed (at most the 8 DMAs of interval 1
+    // pending), interval 1's land before barrier 0.
+    const bool lag = x.lag;
+    issue_act(x,lds,C0);
+    issue_act(x,lds,C0 + 1);
+    issue_w<0>(x,lds,C0);
+    if (!lag) issue_w<1>(x,lds,C0 + 1);
+    issue_scales<Q5>(g,x,C0 / kSBC,sc);
+    issue_act(x,lds,C0 + 2);
+    issue_act(x,lds,C0 + 3);
+    if (lag) issue_w<1>(x,lds,C0 + 1);
+    issue_w<2>(x,lds,C0 + 2);
+    if (!lag) issue_w<3>(x,lds,C0 + 3);
+    if constexpr (SUMS) wait_vmcnt<0>();  // (spill traffic would join the count)
+    else wait_vmcnt<8>();
     __builtin_amdgcn_s_barrier();
     Opnd R;
-    read_all<0,0>(R,lds,x);
-
-    for (int c = C0; c < C; c += kSBC) {
-        wave_iter<Q5,SUMS,0,DIST>(g,x,acc,R,lds,c,scale_base,discard);
-        wave_iter<Q5,SUMS,1,DIST>(g,x,acc,R,lds,c + 1,scale_base,discard);
-        wave_iter<Q5,SUMS,2,DIST>(g,x,acc,R,lds,c + 2,scale_base,discard);
-        wave_iter<Q5,SUMS,3,DIST>(g,x,acc,R,lds,c + 3,scale_base,discard);
-    }
+    read_all<0>(R,lds,x,a_off(x,C0));
+    for (int s0 = C0; s0 < C; s0 += kSBC) super_block<Q5,SUMS>(g,acc,R,lds,x,s0,sc);
 
     if constexpr (!SUMS) {
         const uint32_t ln = lane_id();
