@@ -352,13 +352,13 @@ int build_matvec_form(pixhip_session* s, pixhip_weight* w)
     }
     if (w->type == PIX_Q5_K) {
         Carver c;
-        size_t qs = c.take(N * K / 2), meta = c.take(N * (K / 64) * 16);
+        size_t qs = c.take(N * K / 2), rec = c.take(N * (K / 64) * 12);
         int rc = weight_alloc(s,w,c.offset,&w->planar);
         if (rc) return rc;
         uint8_t* base = static_cast<uint8_t*>(w->planar);
-        w->q5p = {base + qs,reinterpret_cast<const uint4*>(base + meta)};
+        w->q5p = {base + qs,reinterpret_cast<const uint32_t*>(base + rec)};
         PIX_HIP(pixhip::launch_repack_q5_K_planar(static_cast<const uint8_t*>(w->raw),N,K,const_cast<uint8_t*>(w->q5p.qs),
-                                                  const_cast<uint4*>(w->q5p.meta),s->stream),
+                                                  const_cast<uint32_t*>(w->q5p.rec),s->stream),
                 "repack Q5_K planar");
         return PIXHIP_OK;
     }

@@ -241,12 +241,25 @@ template <int UPL> constexpr int mv_rows() { return UPL <= 4? kMvRows : 1; }
 // ---------------------------------------------------------------- Q5_K (planar)
 // Weight registers of R rows: unit u = lane + 64k of a row covers two
 // 32-value sub-blocks (2j, 2j+1 of super-block u/4): its 32 nibble bytes (from
-// the row's two half planes) and its 16-byte record (high bits, scales and
-// minima, d and dmin).
+// the row's two half planes) and its 12-byte record (high bits, six-bit scales
+// and minima, and one byte of the super-block's d and dmin; the four units of
+// a super-block sit in one lane quad, which gathers the four bytes with DPP).
+// A row streams its GGUF byte count.
 template <int UPL, int ROWS> struct Q5Rows {
     static constexpr int R = ROWS;
-    uint4 qs0[R][UPL], qs1[R][UPL], meta[R][UPL];
+    uint4 qs0[R][UPL], qs1[R][UPL];
+    uint3 rec[R][UPL];
 };
+
+// The 32-bit word made of byte 3 of v in lanes 0..3 of the caller's quad.
+__device__ __forceinline__ uint32_t quad_gather_top_bytes(uint32_t v)
+{
+    const uint32_t b0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v,0x00,0xf,0xf,false);
+    const uint32_t b1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v,0x55,0xf,0xf,false);
+    const uint32_t b2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v,0xaa,0xf,0xf,false);
+    const uint32_t b3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)v,0xff,0xf,0xf,false);
+    return (b0 >> 24) | ((b1 >> 16) & 0xff00u) | ((b2 >> 8) & 0xff0000u) | (b3 & 0xff000000u);
+}
 
 template <int UPL, int R>
 __device__ __forceinline__ void q5_load(Q5Rows<UPL,R>& f, const PlanarQ5K& w, int K, int r0, int last, int lane, int units)
@@ -260,7 +273,7 @@ __device__ __forceinline__ void q5_load(Q5Rows<UPL,R>& f, const PlanarQ5K& w, in
             const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2));
             f.qs0[rr][k] = load_stream(q + u);
             f.qs1[rr][k] = load_stream(q + units + u);
-            f.meta[rr][k] = load_stream(w.meta + (size_t)row * units + u);
+            f.rec[rr][k] = *reinterpret_cast<const uint3*>(w.rec + ((size_t)row * units + u) * 3);
         }
     }
 }
@@ -285,7 +298,8 @@ __device__ __forceinline__ void q5_compute(const Q5Rows<UPL,R>& f, float part[R]
         const int bs1 = sB[b * 16 + 4 * j + 2] + sB[b * 16 + 4 * j + 3];
 #pragma unroll
         for (int rr = 0; rr < R; rr++) {
-            const uint4 m = f.meta[rr][k];
+            const uint3 m = f.rec[rr][k];
+            const uint32_t dd = quad_gather_top_bytes(m.z);
             const uint32_t qsw[8] = {f.qs0[rr][k].x,f.qs0[rr][k].y,f.qs0[rr][k].z,f.qs0[rr][k].w,
                                      f.qs1[rr][k].x,f.qs1[rr][k].y,f.qs1[rr][k].z,f.qs1[rr][k].w};
             int dot0 = 0, dot1 = 0;
@@ -297,12 +311,12 @@ __device__ __forceinline__ void q5_compute(const Q5Rows<UPL,R>& f, float part[R]
                 dot0 = sdot4(lo,xa[q],dot0);
                 dot1 = sdot4(hi,xb[q],dot1);
             }
-            const int sc0 = (int)(m.z & 255u), sc1 = (int)((m.z >> 8) & 255u);
-            const int mn0 = (int)((m.z >> 16) & 255u), mn1 = (int)(m.z >> 24);
+            const int sc0 = (int)(m.z & 63u), sc1 = (int)((m.z >> 6) & 63u);
+            const int mn0 = (int)((m.z >> 12) & 63u), mn1 = (int)((m.z >> 18) & 63u);
             const int S = sc0 * dot0 + sc1 * dot1;
             const int Mn = mn0 * bs0 + mn1 * bs1;
-            const float wd = half_bits_to_float((uint16_t)(m.w & 0xffffu));
-            const float wm = half_bits_to_float((uint16_t)(m.w >> 16));
+            const float wd = half_bits_to_float((uint16_t)(dd & 0xffffu));
+            const float wm = half_bits_to_float((uint16_t)(dd >> 16));
             part[rr] = __builtin_fmaf(yd,__builtin_fmaf(-wm,(float)Mn,wd * (float)S),part[rr]);
         }
     }

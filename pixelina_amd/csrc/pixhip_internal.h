@@ -33,12 +33,14 @@
 //   weights Q5_K for the matvec ("q5 planar"): per row, the GGUF nibble bytes of
 //     unit u (64 values, u = 4b + j covers sub-blocks 2j, 2j+1 of super-block b)
 //     split into two half planes, qs u8 [N][2][K/64][16] (half 0: the unit's
-//     bytes 0..15, half 1: bytes 16..31), and one 16-B record per unit,
-//     meta [N][K/64][16]:
-//       bytes 0..7   the unit's 64 high bits: word w = 0, 1 holds, for qh words
-//                    4w..4w+3, ((qh >> 2j) & 0x03030303) << 2*(qword & 3)
-//       bytes 8..11  scale_2j, scale_2j+1, min_2j, min_2j+1 (six-bit values as bytes)
-//       bytes 12..15 d, dmin (fp16 bits, as in the block)
+//     bytes 0..15, half 1: bytes 16..31), and one 12-B record per unit,
+//     rec u32 [N][K/64][3] -- 44 bytes per 64 values, as the GGUF blocks:
+//       words 0, 1  the unit's 64 high bits: word w holds, for qh words
+//                   4w..4w+3, ((qh >> 2j) & 0x03030303) << 2*(qword & 3)
+//       word 2      bits 0..23: scale_2j, scale_2j+1, min_2j, min_2j+1 (six
+//                   bits each); bits 24..31: byte j of the super-block's
+//                   d | dmin << 16 (fp16 bits), which the four units of a
+//                   super-block carry between them
 //   weights Q6_K for the matvec ("q6 planar"): ql u8 [N][2][K/64][16] (each
 //     64-value unit's first and second 16-byte piece of GGUF ql bytes, in two
 //     unit-major planes), qh u8 [N][K/4], sc int8 [N][K/16], d fp16 [N][K/256]
@@ -118,7 +120,7 @@ struct PlanarQ80 {
 
 struct PlanarQ5K {
     const uint8_t* qs;    // [N][K/2]
-    const uint4* meta;    // [N][K/64]
+    const uint32_t* rec;  // [N][K/64][3]
 };
 
 struct PlanarQ6K {
@@ -167,7 +169,7 @@ hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, siz
                               float* dm, _Float16* mn, hipStream_t s);
 hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
                                      hipStream_t s);
-hipError_t launch_repack_q5_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* qs, uint4* meta, hipStream_t s);
+hipError_t launch_repack_q5_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* qs, uint32_t* rec, hipStream_t s);
 hipError_t launch_repack_q6_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* ql, uint8_t* qh, int8_t* sc,
                                      _Float16* d, hipStream_t s);
 // Q8_0 forms: the GEMM's (qs, dT: pass null to skip) and the matvec's

@@ -181,9 +181,9 @@ hipError_t launch_repack_q6_K_planes(const uint8_t* raw, size_t rows, size_t inn
 }
 
 // Q5_K matvec form: one thread per 64-value unit (the nibbles are copied, the
-// rest re-sliced into the unit's 16-byte record).
+// rest re-sliced into the unit's 12-byte record).
 __global__ __launch_bounds__(256) void repack_q5_K_planar_kernel(const uint8_t* __restrict__ raw, size_t rows, size_t inner,
-                                                                 uint8_t* __restrict__ qs, uint4* __restrict__ meta)
+                                                                 uint8_t* __restrict__ qs, uint32_t* __restrict__ rec)
 {
     const size_t units = inner / 64;
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -208,15 +208,18 @@ __global__ __launch_bounds__(256) void repack_q5_K_planar_kernel(const uint8_t* 
     int sc0, mn0, sc1, mn1;
     q5_scale_min(w0,w1,w2,2 * j,sc0,mn0);
     q5_scale_min(w0,w1,w2,2 * j + 1,sc1,mn1);
-    meta[row * units + u] = make_uint4(h[0],h[1],(uint32_t)sc0 | ((uint32_t)sc1 << 8) | ((uint32_t)mn0 << 16) | ((uint32_t)mn1 << 24),
-                                       load_u32_aligned(src));
+    uint32_t* r = rec + (row * units + u) * 3;
+    r[0] = h[0];
+    r[1] = h[1];
+    r[2] = (uint32_t)sc0 | ((uint32_t)sc1 << 6) | ((uint32_t)mn0 << 12) | ((uint32_t)mn1 << 18) |
+           (((load_u32_aligned(src) >> (8 * j)) & 255u) << 24);
 }
 
-hipError_t launch_repack_q5_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* qs, uint4* meta, hipStream_t s)
+hipError_t launch_repack_q5_K_planar(const uint8_t* raw, size_t rows, size_t inner, uint8_t* qs, uint32_t* rec, hipStream_t s)
 {
     const size_t n = rows * (inner / 64);
     if (!n) return hipSuccess;
-    repack_q5_K_planar_kernel<<<dim3((unsigned)((n + 255) / 256)),256,0,s>>>(raw,rows,inner,qs,meta);
+    repack_q5_K_planar_kernel<<<dim3((unsigned)((n + 255) / 256)),256,0,s>>>(raw,rows,inner,qs,rec);
     return hipGetLastError();
 }
 
