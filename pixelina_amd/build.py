@@ -65,7 +65,10 @@ def _compile(src):
 # register spill would add scratch traffic to that counter and break it, so the
 # build fails if the compiler spills any (the integer-sum debug variants drain
 # the counter completely and are exempt).
-NO_SPILL = {"csrc/gemm_kq.hip": ("gemm_kq_kernelILb1ELb0E", "gemm_kq_kernelILb0ELb0E")}
+NO_SPILL = {
+    "csrc/gemm_kq.hip": ("gemm_kq_kernelILb1ELb0E", "gemm_kq_kernelILb0ELb0E"),
+    "csrc/gemm.hip": ("gemm_kernelILb0E",),
+}
 
 
 def _check_no_spill(src, kernels):
