@@ -67,7 +67,7 @@ def _compile(src):
 # the counter completely and are exempt).
 NO_SPILL = {
     "csrc/gemm_kq.hip": ("gemm_kq_kernelILb1ELb0E", "gemm_kq_kernelILb0ELb0E"),
-    "csrc/gemm.hip": ("gemm_kernelILb0E",),
+    "csrc/gemm.hip": ("gemm_kernelILb0E", "gemm_small_kernel"),
 }
 
 

@@ -510,7 +510,9 @@ int multiply_stage(pixhip_session* s, pixhip_weight* w, size_t columns, const pi
         return fail(PIXHIP_ERR_STATE,"no quantized activations of this shape: run the QUANTIZE stage first");
     int rc = ensure_gemm_form(s,w);
     if (rc) return rc;
-    const size_t part_bytes = pixhip::gemm_split_bytes(columns,w->rows,round_up(w->inner,64));
+    const size_t part_bytes = kind == 2 && pixhip::gemm_q8_0_grouped(columns,w->rows)
+                                  ? 0
+                                  : pixhip::gemm_split_bytes(columns,w->rows,round_up(w->inner,64));
     if (part_bytes) {
         rc = grow(s,&s->partial,&s->partial_bytes,part_bytes);
         if (rc) return rc;

@@ -397,6 +397,175 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// K-grouped form for grids too small to fill the device (the 256-token
+// linear has thirty 256 x 128 tiles for 256 CUs).  A workgroup owns a 64 x 64
+// tile and splits its K range over four K-groups of four waves: group g runs
+// stages [g*Cg, (g+1)*Cg) with its own 3-slot ring, each of its waves owns a
+// 32 x 32 quarter of the tile, and at the end groups 1..3 hand their
+// accumulators to group 0 through LDS, which adds them in group order and
+// stores.  No fp32 partial tiles go through memory and the sum order is fixed.
+// A stage slot holds the 64 activation rows (4 chunks), the 64 weight rows
+// (4 chunks), the activation scales of the stage's two blocks (one chunk: 64
+// floats per block, from lanes 0..31; lanes 32..63 repeat them) and the weight
+// scales likewise.  Per stage each wave of a group issues three DMAs of the
+// twelve chunk ids (ten loads, two empty).
+constexpr int kSBM = 64, kSBN = 64, kSGroups = 4, kSWaves = 16, kSThreads = 64 * kSWaves;
+constexpr int kSSlots = 3, kSDist = kSSlots - 1;
+constexpr int kSChunks = 10, kSSlotBytes = kSChunks * kChunk, kSGroupBytes = kSSlots * kSSlotBytes;
+constexpr int kSPerWave = 3;
+constexpr int kSRedBytes = (kSGroups - 1) * 4 * 32 * 32 * 4;  // groups 1..3: four 32 x 32 fp32 blocks each
+static_assert(kSGroups * 4 == kSWaves && kSPerWave * 4 >= kSChunks, "K-grouped shape");
+static_assert(kSRedBytes <= kSGroups * kSGroupBytes, "the reduction reuses the rings");
+
+struct SmallCtx {
+    int m0, n0, q, wm, wn, K, Mpad, Npad;
+    int begin, end;  // this group's stages
+    Rsrc rx, rxd, rwq, rwd, rnull;
+};
+
+__device__ __forceinline__ void small_issue(const SmallCtx& x, int c, uint8_t* slot, uint8_t* discard)
+{
+    const uint32_t k0 = (uint32_t)c * kKC;
+#pragma unroll
+    for (int i = 0; i < kSPerWave; i++) {
+        const int chunk = x.q + 4 * i;  // wave-uniform
+        const uint32_t lane = lane_now();
+        if (chunk < 8) {
+            const uint32_t vo = (lane >> 2) * (uint32_t)x.K + 16u * ((lane & 3) ^ ((lane >> 4) & 3));
+            if (chunk < 4) dma(x.rx,slot + chunk * kChunk,vo,(uint32_t)(x.m0 + chunk * 16) * x.K + k0);
+            else dma(x.rwq,slot + chunk * kChunk,vo,(uint32_t)(x.n0 + (chunk - 4) * 16) * x.K + k0);
+        } else if (chunk == 8) {
+            const uint32_t vo = 16u * (lane & 15) + ((lane >> 4) & 1) * 4u * (uint32_t)x.Mpad;
+            dma(x.rxd,slot + 8 * kChunk,vo,(uint32_t)(2 * c * x.Mpad + x.m0) * 4u);
+        } else if (chunk == 9) {
+            const uint32_t vo = 16u * (lane & 15) + ((lane >> 4) & 1) * 4u * (uint32_t)x.Npad;
+            dma(x.rwd,slot + 9 * kChunk,vo,(uint32_t)(2 * c * x.Npad + x.n0) * 4u);
+        } else {
+            dma(x.rnull,discard,0,0);
+        }
+    }
+}
+
+// One stage from `slot`: two blocks, each an i8 MFMA and the fp16 scale outer
+// product, then y += cs * P; the DMA of stage c + kSDist goes out after the
+// MFMAs.
+__device__ __forceinline__ void small_stage(const SmallCtx& x, int c, v16f& acc, const uint8_t* __restrict__ slot,
+                                            uint8_t* __restrict__ dma_slot, uint8_t* __restrict__ discard)
+{
+    const v16i izero = {};
+    const v16f fzero = {};
+    const uint32_t ln = lane_now(), lr = ln & 31;
+    const bool k0 = ln < 32;
+    const _Float16 z = (_Float16)0.0f;
+    const float* sxd = reinterpret_cast<const float*>(slot + 8 * kChunk);
+    const float* swd = reinterpret_cast<const float*>(slot + 9 * kChunk);
+    v4i a[2], w[2];
+    v4h xa[2], wb[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const uint32_t piece = 16 * ((2 * s + (ln >> 5)) ^ ((lr >> 2) & 3));
+        a[s] = *reinterpret_cast<const v4i*>(slot + (x.wm * 32 + lr) * 64 + piece);
+        w[s] = *reinterpret_cast<const v4i*>(slot + 4 * kChunk + (x.wn * 32 + lr) * 64 + piece);
+        const float xv = sxd[s * kSBM + x.wm * 32 + lr], wv = swd[s * kSBN + x.wn * 32 + lr];
+        xa[s] = v4h{(_Float16)(k0? xv : 0.0f),z,z,z};
+        wb[s] = v4h{(_Float16)(k0? wv : 0.0f),z,z,z};
+    }
+    v16i p[2];
+    v16f cs[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        p[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s],w[s],izero,0,0,0);
+        cs[s] = __builtin_amdgcn_mfma_f32_32x32x8f16(xa[s],wb[s],fzero,0,0,0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + kSDist < x.end) small_issue(x,c + kSDist,dma_slot,discard);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = __builtin_fmaf(cs[s][r],(float)p[s][r],acc[r]);
+    pin(acc);
+}
+
+__global__ __launch_bounds__(kSThreads, 1) void gemm_small_kernel(GemmArgs g)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kSGroups * kSGroupBytes + kChunk];
+    uint8_t* const discard = lds + kSGroups * kSGroupBytes;
+    const int ntiles = g.tiles_m * g.tiles_n;
+    const int lid = xcd_remap((int)blockIdx.x,ntiles);
+    SmallCtx x;
+    x.m0 = (lid % g.tiles_m) * kSBM;  // consecutive tiles share a weight tile
+    x.n0 = (lid / g.tiles_m) * kSBN;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int grp = wave / 4;
+    x.q = wave % 4;
+    x.wm = x.q % 2;
+    x.wn = x.q / 2;
+    x.K = g.K;
+    x.Mpad = g.Mpad;
+    x.Npad = g.Npad;
+    const int C = g.K / kKC, Cg = (C + kSGroups - 1) / kSGroups;
+    x.begin = min(grp * Cg,C);
+    x.end = min(x.begin + Cg,C);
+    {
+        const size_t mp = (size_t)g.Mpad, np = (size_t)g.Npad, K = (size_t)g.K;
+        const size_t nblk = K / PIX_QK8;
+        x.rx = make_rsrc(g.xq,mp * K);
+        x.rxd = make_rsrc(g.xdT,nblk * mp * 4);
+        x.rwq = make_rsrc(g.wq,np * K);
+        x.rwd = make_rsrc(g.wdT,nblk * np * 4);
+        x.rnull = make_rsrc(g.xq,0);
+    }
+    uint8_t* const ring = lds + grp * kSGroupBytes;
+
+    v16f acc = {};
+    for (int j = 0; j < kSDist; j++)
+        if (x.begin + j < x.end) small_issue(x,x.begin + j,ring + j * kSSlotBytes,discard);
+    // Every wave runs Cg iterations (one barrier each); a group past its
+    // range idles through them.  Stage c has landed once at most the DMAs of
+    // stage c+1 are in flight.
+    for (int i = 0; i < Cg; i++) {
+        const int c = x.begin + i;
+        if (c + kSDist - 1 < x.end) wait_vmcnt<(kSDist - 1) * kSPerWave>();
+        else wait_vmcnt<0>();
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+        if (c < x.end) small_stage(x,c,acc,ring + (i % kSSlots) * kSSlotBytes,ring + ((i + kSDist) % kSSlots) * kSSlotBytes,discard);
+    }
+    wait_vmcnt<0>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    // Groups 1..3 hand over their 32 x 32 blocks ([group-1][quarter][r][lane]
+    // fp32, conflict-free), group 0 adds them in group order.
+    const uint32_t ln = lane_now();
+    float* red = reinterpret_cast<float*>(lds);
+    if (grp > 0) {
+        float* dst = red + ((grp - 1) * 4 + x.q) * 1024 + ln;
+#pragma unroll
+        for (int r = 0; r < 16; r++) dst[r * 64] = acc[r];
+    }
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    if (grp != 0) return;
+#pragma unroll
+    for (int g2 = 1; g2 < kSGroups; g2++) {
+        const float* src = red + ((g2 - 1) * 4 + x.q) * 1024 + ln;
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] += src[r * 64];
+    }
+    const int lr = (int)(ln & 31), lg = (int)(ln >> 5);
+    const int n = x.n0 + x.wn * 32 + lr;
+    const float bv = g.bias? g.bias[min(n,g.N - 1)] : 0.0f;
+    float* col = g.y + g.yoff + n;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = x.m0 + x.wm * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (m < g.M && n < g.N) __builtin_nontemporal_store(acc[r] + bv,col + (size_t)m * g.ldy);
+    }
+}
+
 static size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
 // For the split tiles: y[yoff + m*ldy + n] = sum over the splits, in order, of
@@ -463,6 +632,14 @@ int gemm_split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_ch
     return (chunks + split_chunks - 1) / split_chunks;
 }
 
+// The Q8_0 GEMM runs the K-grouped 64 x 64 form when its 256 x 128 tiles
+// would fill at most half of the device.
+bool gemm_q8_0_grouped(size_t M, size_t N)
+{
+    const size_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    return tiles * 2 <= (size_t)device_cus();
+}
+
 size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages)
 {
     int full, chunks;
@@ -485,6 +662,12 @@ static hipError_t launch(GemmArgs g, size_t mpad, size_t npad, hipStream_t s)
     g.Npad = (int)npad;
     const int ntiles = g.tiles_m * g.tiles_n;
     if (!ntiles) return hipSuccess;
+    if (!SUMS && gemm_q8_0_grouped((size_t)g.M,(size_t)g.N)) {
+        g.tiles_m = (int)((g.M + kSBM - 1) / kSBM);
+        g.tiles_n = (int)((g.N + kSBN - 1) / kSBN);
+        gemm_small_kernel<<<dim3(g.tiles_m * g.tiles_n),dim3(kSThreads),0,s>>>(g);
+        return hipGetLastError();
+    }
     g.splits = SUMS? 1 : gemm_split_plan((size_t)g.M,(size_t)g.N,(size_t)g.K,g.full_tiles,g.split_chunks);
     if (g.splits == 1 || !g.part) {  // unsplit (or no workspace)
         g.splits = 1;

@@ -185,6 +185,9 @@ size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages);
 // The split of a GEMM grid: number of K pieces of the last round's tiles (1:
 // none), the whole tiles before them and the piece length in 64-value stages.
 int gemm_split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_chunks);
+// True when the Q8_0 GEMM of M x N runs its K-grouped small-tile form, which
+// needs no split-K workspace.
+bool gemm_q8_0_grouped(size_t M, size_t N);
 hipError_t launch_gemm_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t N, size_t K, const Output& out, float* part,
                             hipStream_t s);
 hipError_t launch_gemm_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, const Output& out, float* part,

@@ -139,7 +139,9 @@ def test_block_sums_exact(sess, wtype):
 @pytest.mark.parametrize("wtype,m,n,k", [
     (Q5_K, 2, 1, 256), (Q5_K, 129, 130, 768), (Q5_K, 37, 300, 3840),
     (Q6_K, 3, 257, 512), (Q6_K, 200, 64, 1024),
-    (Q8_0, 2, 7, 32), (Q8_0, 131, 129, 96), (Q8_0, 64, 256, 3840),
+    (Q8_0, 2, 7, 32), (Q8_0, 131, 129, 96), (Q8_0, 64, 256, 3840), (Q8_0, 200, 300, 4000),
+    # enough 256 x 128 tiles (9 x 16) for the Q8_0 GEMM's whole-tile form; the shapes above run its K-grouped form
+    (Q8_0, 2100, 2000, 512),
 ])
 def test_gemm_ragged_vs_oracle(sess, wtype, m, n, k):
     rng = np.random.default_rng(m * 1000 + n)
