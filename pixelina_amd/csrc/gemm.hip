@@ -131,6 +131,13 @@ __device__ __forceinline__ void dma(Rsrc r, uint8_t* lds_uniform, uint32_t voff,
 // later uses rise above) this point.
 template <class T> __device__ __forceinline__ void pin(T& v) { __asm__ volatile("" : "+v"(v)); }
 
+// One dword per lane: lane l lands at LDS base + 4*l.
+__device__ __forceinline__ void dma4(Rsrc r, uint8_t* lds_uniform, uint32_t voff, uint32_t soff)
+{
+    __builtin_assume(lds_uniform != nullptr);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r,PIX_LDS(lds_uniform),4,(int)voff,(int)soff,0,0);
+}
+
 // The lane index, recomputed where it is used (volatile, so the compiler
 // cannot keep derived per-lane offsets live across the loop).
 __device__ __forceinline__ uint32_t lane_now()
@@ -406,26 +413,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
 // 32 x 32 quarter of the tile, and at the end groups 1..3 hand their
 // accumulators to group 0 through LDS, which adds them in group order and
 // stores.  No fp32 partial tiles go through memory and the sum order is fixed.
-// A stage slot holds the 64 activation rows (4 chunks), the 64 weight rows
-// (4 chunks), the activation scales of the stage's two blocks (one chunk: 64
-// floats per block, from lanes 0..31; lanes 32..63 repeat them) and the weight
-// scales likewise.  Per stage each wave of a group issues three DMAs of the
-// twelve chunk ids (ten loads, two empty).
+// A stage slot (9 KB) holds the 64 activation rows (4 KB, four 16-row
+// DMAs), the 64 weight rows (4 KB) and the activation and weight scales of the
+// stage's two blocks (4 x 256 B, one dword DMA each).  Per stage each wave of a
+// group issues three of the twelve DMAs.
 constexpr int kSBM = 64, kSBN = 64, kSGroups = 4, kSWaves = 16, kSThreads = 64 * kSWaves;
-constexpr int kSSlots = 3, kSDist = kSSlots - 1;
-constexpr int kSChunks = 10, kSSlotBytes = kSChunks * kChunk, kSGroupBytes = kSSlots * kSSlotBytes;
+constexpr int kSSlots = 4, kSDist = kSSlots - 1;
+constexpr int kSXd = 8 * kChunk, kSWd = kSXd + 2 * 256, kSSlotBytes = kSWd + 2 * 256;
+constexpr int kSChunks = 12, kSGroupBytes = kSSlots * kSSlotBytes;
 constexpr int kSPerWave = 3;
 constexpr int kSRedBytes = (kSGroups - 1) * 4 * 32 * 32 * 4;  // groups 1..3: four 32 x 32 fp32 blocks each
-static_assert(kSGroups * 4 == kSWaves && kSPerWave * 4 >= kSChunks, "K-grouped shape");
+static_assert(kSGroups * 4 == kSWaves && kSPerWave * 4 == kSChunks, "K-grouped shape");
 static_assert(kSRedBytes <= kSGroups * kSGroupBytes, "the reduction reuses the rings");
 
 struct SmallCtx {
     int m0, n0, q, wm, wn, K, Mpad, Npad;
     int begin, end;  // this group's stages
-    Rsrc rx, rxd, rwq, rwd, rnull;
+    Rsrc rx, rxd, rwq, rwd;
 };
 
-__device__ __forceinline__ void small_issue(const SmallCtx& x, int c, uint8_t* slot, uint8_t* discard)
+__device__ __forceinline__ void small_issue(const SmallCtx& x, int c, uint8_t* slot)
 {
     const uint32_t k0 = (uint32_t)c * kKC;
 #pragma unroll
@@ -436,14 +443,12 @@ __device__ __forceinline__ void small_issue(const SmallCtx& x, int c, uint8_t* s
             const uint32_t vo = (lane >> 2) * (uint32_t)x.K + 16u * ((lane & 3) ^ ((lane >> 4) & 3));
             if (chunk < 4) dma(x.rx,slot + chunk * kChunk,vo,(uint32_t)(x.m0 + chunk * 16) * x.K + k0);
             else dma(x.rwq,slot + chunk * kChunk,vo,(uint32_t)(x.n0 + (chunk - 4) * 16) * x.K + k0);
-        } else if (chunk == 8) {
-            const uint32_t vo = 16u * (lane & 15) + ((lane >> 4) & 1) * 4u * (uint32_t)x.Mpad;
-            dma(x.rxd,slot + 8 * kChunk,vo,(uint32_t)(2 * c * x.Mpad + x.m0) * 4u);
-        } else if (chunk == 9) {
-            const uint32_t vo = 16u * (lane & 15) + ((lane >> 4) & 1) * 4u * (uint32_t)x.Npad;
-            dma(x.rwd,slot + 9 * kChunk,vo,(uint32_t)(2 * c * x.Npad + x.n0) * 4u);
+        } else if (chunk < 10) {
+            const int b = chunk - 8;
+            dma4(x.rxd,slot + kSXd + 256 * b,4u * lane,(uint32_t)((2 * c + b) * x.Mpad + x.m0) * 4u);
         } else {
-            dma(x.rnull,discard,0,0);
+            const int b = chunk - 10;
+            dma4(x.rwd,slot + kSWd + 256 * b,4u * lane,(uint32_t)((2 * c + b) * x.Npad + x.n0) * 4u);
         }
     }
 }
@@ -452,15 +457,15 @@ __device__ __forceinline__ void small_issue(const SmallCtx& x, int c, uint8_t* s
 // product, then y += cs * P; the DMA of stage c + kSDist goes out after the
 // MFMAs.
 __device__ __forceinline__ void small_stage(const SmallCtx& x, int c, v16f& acc, const uint8_t* __restrict__ slot,
-                                            uint8_t* __restrict__ dma_slot, uint8_t* __restrict__ discard)
+                                            uint8_t* __restrict__ dma_slot)
 {
     const v16i izero = {};
     const v16f fzero = {};
     const uint32_t ln = lane_now(), lr = ln & 31;
     const bool k0 = ln < 32;
     const _Float16 z = (_Float16)0.0f;
-    const float* sxd = reinterpret_cast<const float*>(slot + 8 * kChunk);
-    const float* swd = reinterpret_cast<const float*>(slot + 9 * kChunk);
+    const float* sxd = reinterpret_cast<const float*>(slot + kSXd);
+    const float* swd = reinterpret_cast<const float*>(slot + kSWd);
     v4i a[2], w[2];
     v4h xa[2], wb[2];
 #pragma unroll
@@ -480,7 +485,7 @@ __device__ __forceinline__ void small_stage(const SmallCtx& x, int c, v16f& acc,
         cs[s] = __builtin_amdgcn_mfma_f32_32x32x8f16(xa[s],wb[s],fzero,0,0,0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (c + kSDist < x.end) small_issue(x,c + kSDist,dma_slot,discard);
+    if (c + kSDist < x.end) small_issue(x,c + kSDist,dma_slot);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < 2; s++)
@@ -491,8 +496,7 @@ __device__ __forceinline__ void small_stage(const SmallCtx& x, int c, v16f& acc,
 
 __global__ __launch_bounds__(kSThreads, 1) void gemm_small_kernel(GemmArgs g)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[kSGroups * kSGroupBytes + kChunk];
-    uint8_t* const discard = lds + kSGroups * kSGroupBytes;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kSGroups * kSGroupBytes];
     const int ntiles = g.tiles_m * g.tiles_n;
     const int lid = xcd_remap((int)blockIdx.x,ntiles);
     SmallCtx x;
@@ -516,13 +520,12 @@ __global__ __launch_bounds__(kSThreads, 1) void gemm_small_kernel(GemmArgs g)
         x.rxd = make_rsrc(g.xdT,nblk * mp * 4);
         x.rwq = make_rsrc(g.wq,np * K);
         x.rwd = make_rsrc(g.wdT,nblk * np * 4);
-        x.rnull = make_rsrc(g.xq,0);
     }
     uint8_t* const ring = lds + grp * kSGroupBytes;
 
     v16f acc = {};
     for (int j = 0; j < kSDist; j++)
-        if (x.begin + j < x.end) small_issue(x,x.begin + j,ring + j * kSSlotBytes,discard);
+        if (x.begin + j < x.end) small_issue(x,x.begin + j,ring + j * kSSlotBytes);
     // Every wave runs Cg iterations (one barrier each); a group past its
     // range idles through them.  Stage c has landed once at most the DMAs of
     // stage c+1 are in flight.
@@ -532,7 +535,7 @@ __global__ __launch_bounds__(kSThreads, 1) void gemm_small_kernel(GemmArgs g)
         else wait_vmcnt<0>();
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
-        if (c < x.end) small_stage(x,c,acc,ring + (i % kSSlots) * kSSlotBytes,ring + ((i + kSDist) % kSSlots) * kSSlotBytes,discard);
+        if (c < x.end) small_stage(x,c,acc,ring + (i % kSSlots) * kSSlotBytes,ring + ((i + kSDist) % kSSlots) * kSSlotBytes);
     }
     wait_vmcnt<0>();
     wait_lgkm0();
