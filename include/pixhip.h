@@ -28,7 +28,7 @@ extern "C" {
 
 #define PIXHIP_OK 0
 #define PIXHIP_ERR_ARGUMENT (-1)    /* bad pointer, size or shape (cpu_quant_matmul's `return false`, src/kernels_quant.cpp:373-377) */
-#define PIXHIP_ERR_UNSUPPORTED (-2) /* weight type other than Q8_0 / Q5_K / Q6_K */
+#define PIXHIP_ERR_UNSUPPORTED (-2) /* weight type other than Q8_0 / Q5_K / Q6_K; attention head size above 128 */
 #define PIXHIP_ERR_MEMORY (-3)      /* device allocation failed or exceeds the budget (src/backend_vulkan.cpp:689, :718-720) */
 #define PIXHIP_ERR_DEVICE (-4)      /* HIP runtime failure: no device, launch or synchronisation error */
 #define PIXHIP_ERR_STATE (-5)       /* missing session, MULTIPLY without matching activations, or an evicted weight without host bytes */
@@ -254,6 +254,40 @@ int pixhip_pointwise(pixhip_session* session, unsigned operation, float* destina
  * (tensor_rope's std::vector tables), staged to the device first. */
 int pixhip_rope(pixhip_session* session, float* tensor, size_t rows, size_t channels, size_t heads, const float* cosine,
                 const float* sine, int interleaved);
+
+/* ---- attention ---- */
+
+/* One PixAttentionRange (src/tensor.h:58-63): query rows [query_begin,
+ * query_end) see keys [0, key_end), and, when `causal`, only keys up to their
+ * absolute row query_offset + row. */
+typedef struct pixhip_attention_range {
+    size_t query_begin, query_end, key_end;
+    int causal;
+} pixhip_attention_range;
+
+/* tensor_attention(q, k, v, heads, kv_heads, causal) (src/tensor.cpp:347-382;
+ * vulkan_attention, src/backend_vulkan.h:143): `output` [rows][channels] for
+ * q [rows][channels] and k, v [keys][channels / heads * kv_heads], head h
+ * reading kv head h / (heads / kv_heads), scale 1/sqrt(channels / heads);
+ * causal rows see keys 0..row.  Head sizes 1..128 (PIXHIP_ERR_UNSUPPORTED
+ * beyond; the reference's Vulkan path takes up to 1280).  Rejects
+ * (PIXHIP_ERR_ARGUMENT) heads not a multiple of kv_heads, channels not a
+ * multiple of heads, and causal with rows > keys (where the reference reads
+ * past k).  Within 1e-4 of the fp32
+ * reference per row (bf16 three-term products, fp32 softmax).  Tensors are
+ * device memory or pinned host memory (q, k, v may be pageable, staged to the
+ * device first), 16-byte aligned. */
+int pixhip_attention(pixhip_session* session, const float* q, size_t rows, const float* k, const float* v, size_t keys,
+                     size_t heads, size_t kv_heads, size_t channels, int causal, float* output);
+
+/* tensor_attention(q, k, v, heads, kv_heads, ranges, query_offset)
+ * (src/tensor.cpp:384-427; vulkan_attention, src/backend_vulkan.h:144,
+ * :1318-1340): as above with per-range key limits; `ranges` must tile the
+ * query rows in order with 0 < key_end <= keys (the reference's checks,
+ * src/tensor.cpp:386-394, PIXHIP_ERR_ARGUMENT otherwise). */
+int pixhip_attention_ranges(pixhip_session* session, const float* q, size_t rows, const float* k, const float* v, size_t keys,
+                            size_t heads, size_t kv_heads, size_t channels, const pixhip_attention_range* ranges, size_t count,
+                            size_t query_offset, float* output);
 
 /* ---- integer parity gate ---- */
 

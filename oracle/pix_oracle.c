@@ -600,3 +600,86 @@ void orc_rope(float* x, size_t rows, size_t channels, size_t heads, const float*
             }
         }
 }
+
+/* dot_avx, src/tensor.cpp:117-132 (cpu_dot's path on an AVX2+FMA host, :135-143):
+ * two 8-lane fused multiply-add accumulators over 16-value steps, added lane
+ * by lane, the 8 partials summed in order, then the tail as a product and a
+ * sum (no contraction). */
+static float dot_avx_lanes(const float* a, const float* b, size_t count)
+{
+    float s0[8] = {0}, s1[8] = {0};
+    size_t i = 0;
+    for (; i + 16 <= count; i += 16)
+        for (int l = 0; l < 8; l++) {
+            s0[l] = fmaf(a[i + l],b[i + l],s0[l]);
+            s1[l] = fmaf(a[i + 8 + l],b[i + 8 + l],s1[l]);
+        }
+    float result = 0;
+    for (int l = 0; l < 8; l++) result += s0[l] + s1[l];
+    for (; i < count; i++) result += a[i] * b[i];
+    return result;
+}
+
+/* tensor_attention with ranges, src/tensor.cpp:384-427 (the causal form,
+ * :347-382, is the one range {0, rows, keys, causal} at query_offset 0 where
+ * token + 1 <= keys).  q [rows][channels], k and v [keys][channels / heads *
+ * kv_heads], out [rows][channels]; ranges [n][4] = query_begin, query_end,
+ * key_end, causal (PixAttentionRange, src/tensor.h:58-63), contiguous from row
+ * 0.  Per (token, head): scores = dot(q, k_j) * (1/sqrt(dim)) in fp32, the
+ * maximum, exp(score - max) in fp32 summed in double, then out += float(p /
+ * sum) * v_j in fp32, key by key.  Returns 0 on the arguments the reference
+ * rejects (:386-394), 1 otherwise. */
+int orc_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                  size_t channels, const uint64_t* ranges, size_t nranges, size_t query_offset, float* out)
+{
+    if (!heads || !kv_heads || heads % kv_heads || channels % heads || !rows || !keys) return 0;
+    const size_t dim = channels / heads, kv_channels = dim * kv_heads;
+    size_t covered = 0;
+    for (size_t r = 0; r < nranges; r++) {
+        const uint64_t* g = ranges + 4 * r;
+        if (g[0] != covered || g[1] <= g[0] || g[1] > rows || !g[2] || g[2] > keys) return 0;
+        covered = (size_t)g[1];
+    }
+    if (covered != rows) return 0;
+    const float scale = 1.0f / sqrtf((float)dim);
+    float* scores = (float*)malloc(keys * sizeof(float));
+    if (!scores) return 0;
+    memset(out,0,rows * channels * sizeof(float));
+    size_t range = 0;
+    for (size_t token = 0; token < rows; token++) {
+        while (token >= ranges[4 * range + 1]) range++;
+        const uint64_t* g = ranges + 4 * range;
+        size_t tokens = (size_t)g[2];
+#if ORC_MUTANT == 16
+        if (g[3] && query_offset + token < tokens) tokens = query_offset + token;
+#else
+        if (g[3] && query_offset + token + 1 < tokens) tokens = query_offset + token + 1;
+#endif
+        for (size_t head = 0; head < heads; head++) {
+#if ORC_MUTANT == 15
+            const size_t kv_head = head % kv_heads;
+#else
+            const size_t kv_head = head / (heads / kv_heads);
+#endif
+            const float* query = q + token * channels + head * dim;
+            float maximum = -INFINITY;
+            for (size_t j = 0; j < tokens; j++) {
+                scores[j] = dot_avx_lanes(query,k + j * kv_channels + kv_head * dim,dim) * scale;
+                maximum = fmaxf(maximum,scores[j]);
+            }
+            double sum = 0;
+            for (size_t j = 0; j < tokens; j++) {
+                scores[j] = expf(scores[j] - maximum);
+                sum += scores[j];
+            }
+            float* to = out + token * channels + head * dim;
+            for (size_t j = 0; j < tokens; j++) {
+                const float probability = (float)(scores[j] / sum);
+                const float* value = v + j * kv_channels + kv_head * dim;
+                for (size_t c = 0; c < dim; c++) to[c] += probability * value[c];
+            }
+        }
+    }
+    free(scores);
+    return 1;
+}

@@ -53,6 +53,8 @@ void orc_gelu(float* x, size_t count, int approximate);
 void orc_bias(float* x, size_t rows, size_t channels, const float* bias);
 void orc_add(float* x, const float* y, size_t count);
 void orc_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, int interleaved);
+int orc_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                  size_t channels, const uint64_t* ranges, size_t nranges, size_t query_offset, float* out);
 
 #ifdef __cplusplus
 }

@@ -139,6 +139,44 @@ void ref_add(float* x, const float* y, size_t count)
     std::copy(a.values.begin(),a.values.end(),x);
 }
 
+/* tensor_attention(q, k, v, heads, kv_heads, causal), src/tensor.cpp:347-382:
+ * q [rows][channels], k and v [keys][channels / heads * kv_heads].  Returns 1
+ * when the reference produced output. */
+int ref_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                  size_t channels, int causal, float* out)
+{
+    const size_t kv_channels = channels / heads * kv_heads;
+    PixTensor tq(rows,channels),tk(keys,kv_channels),tv(keys,kv_channels);
+    std::copy(q,q + rows * channels,tq.values.begin());
+    std::copy(k,k + keys * kv_channels,tk.values.begin());
+    std::copy(v,v + keys * kv_channels,tv.values.begin());
+    PixTensor o = tensor_attention(tq,tk,tv,heads,kv_heads,causal != 0);
+    if (o.values.size() != rows * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
+/* tensor_attention(q, k, v, heads, kv_heads, ranges, query_offset),
+ * src/tensor.cpp:384-427; ranges [n][4] = query_begin, query_end, key_end,
+ * causal (PixAttentionRange, src/tensor.h:58-63).  Returns 1 when the reference
+ * produced output (0: it rejected the arguments). */
+int ref_attention_ranges(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                         size_t channels, const uint64_t* ranges, size_t nranges, size_t query_offset, float* out)
+{
+    const size_t kv_channels = channels / heads * kv_heads;
+    PixTensor tq(rows,channels),tk(keys,kv_channels),tv(keys,kv_channels);
+    std::copy(q,q + rows * channels,tq.values.begin());
+    std::copy(k,k + keys * kv_channels,tk.values.begin());
+    std::copy(v,v + keys * kv_channels,tv.values.begin());
+    std::vector<PixAttentionRange> rs(nranges);
+    for (size_t i = 0; i < nranges; i++)
+        rs[i] = PixAttentionRange{size_t(ranges[4 * i]),size_t(ranges[4 * i + 1]),size_t(ranges[4 * i + 2]),ranges[4 * i + 3] != 0};
+    PixTensor o = tensor_attention(tq,tk,tv,heads,kv_heads,rs,query_offset);
+    if (o.values.size() != rows * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
 /* tensor_rope, src/tensor.cpp:429-452 */
 void ref_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, int interleaved)
 {

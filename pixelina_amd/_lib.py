@@ -61,6 +61,8 @@ SIGNATURES = {
     "pixhip_silu_gate_quantize": (_int, [_vp, _u32, _vp, _vp, _sz, _sz, _vp, _vp]),
     "pixhip_pointwise": (_int, [_vp, ctypes.c_uint, _vp, _vp, _sz, _sz]),
     "pixhip_rope": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
+    "pixhip_attention": (_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _int, _vp]),
+    "pixhip_attention_ranges": (_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _vp]),
     "pixhip_block_sums": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "pixhip_timer_start": (_int, [_vp]),
     "pixhip_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
@@ -98,3 +100,9 @@ def check(code, what):
     if code != OK:
         raise PixhipError(code, what)
     return code
+
+
+class AttentionRange(ctypes.Structure):
+    """pixhip_attention_range (PixAttentionRange, src/tensor.h:58-63)."""
+    _fields_ = [("query_begin", ctypes.c_size_t), ("query_end", ctypes.c_size_t), ("key_end", ctypes.c_size_t),
+                ("causal", ctypes.c_int)]

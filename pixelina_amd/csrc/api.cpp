@@ -142,6 +142,9 @@ struct pixhip_session {
     // staging for host or misaligned pointers
     void* stage = nullptr;
     size_t stage_bytes = 0;
+    // attention's bf16 split planes
+    void* attn = nullptr;
+    size_t attn_bytes = 0;
     // activations left by the last QUANTIZE stage
     int act_kind = 0;  // 0 none, 1 Q8_K, 2 Q8_0
     size_t act_columns = 0, act_inner = 0;
@@ -683,6 +686,7 @@ void pixhip_session_destroy(pixhip_session* s)
     if (s->scratch) (void)hipFree(s->scratch);
     if (s->partial) (void)hipFree(s->partial);
     if (s->stage) (void)hipFree(s->stage);
+    if (s->attn) (void)hipFree(s->attn);
     if (s->t0) (void)hipEventDestroy(s->t0);
     if (s->t1) (void)hipEventDestroy(s->t1);
     if (s->own_stream) (void)hipStreamDestroy(s->own_stream);
@@ -1147,6 +1151,86 @@ int pixhip_rope(pixhip_session* s, float* tensor, size_t rows, size_t channels, 
     if (ss) pixhip_free(s,ss);
     PIX_HIP(e,"rope");
     return PIXHIP_OK;
+}
+
+namespace {
+
+// The attention ranges' common path: operands resolved to device memory, one
+// kernel launch per range after the split pass.
+int attention_run(pixhip_session* s, const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads,
+                  size_t kv_heads, size_t channels, const pixhip::AttnRange* ranges, size_t count, size_t query_offset, float* output)
+{
+    const size_t dim = channels / heads, kv_channels = dim * kv_heads;
+    if (!pixhip::attention_dim_pad(dim))
+        return fail(PIXHIP_ERR_UNSUPPORTED,"attention head size " + std::to_string(dim) + " is not supported (1..128)");
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+         reinterpret_cast<uintptr_t>(output)) % 16)
+        return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 16-byte aligned");
+    int rc;
+    void* out = nullptr;
+    if ((rc = write_operand(s,output,&out))) return rc;
+    const void *qd = nullptr, *kd = nullptr, *vd = nullptr;
+    void *qs = nullptr, *ks = nullptr, *vs = nullptr;
+    auto release = [&]() {
+        if (qs) pixhip_free(s,qs);
+        if (ks) pixhip_free(s,ks);
+        if (vs) pixhip_free(s,vs);
+    };
+    if ((rc = read_operand(s,q,rows * channels * sizeof(float),&qd,&qs)) ||
+        (rc = read_operand(s,k,keys * kv_channels * sizeof(float),&kd,&ks)) ||
+        (rc = read_operand(s,v,keys * kv_channels * sizeof(float),&vd,&vs))) {
+        release();
+        return rc;
+    }
+    if ((rc = grow(s,&s->attn,&s->attn_bytes,pixhip::attention_workspace_bytes(rows,keys,heads,kv_heads,dim)))) {
+        release();
+        return rc;
+    }
+    hipError_t e = pixhip::launch_attention(static_cast<const float*>(qd),static_cast<const float*>(kd),static_cast<const float*>(vd),
+                                            static_cast<float*>(out),rows,keys,heads,kv_heads,dim,ranges,count,query_offset,s->attn,
+                                            s->stream);
+    release();
+    if (e == hipErrorInvalidValue) return fail(PIXHIP_ERR_ARGUMENT,"attention shape beyond the kernel's 32-bit index range");
+    PIX_HIP(e,"attention");
+    return PIXHIP_OK;
+}
+
+}  // namespace
+
+int pixhip_attention(pixhip_session* s, const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads,
+                     size_t kv_heads, size_t channels, int causal, float* output)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!q || !k || !v || !output) return fail(PIXHIP_ERR_ARGUMENT,"null pointer");
+    if (!rows || !keys || !heads || !kv_heads || heads % kv_heads || channels % heads)
+        return fail(PIXHIP_ERR_ARGUMENT,"empty tensors, or heads not a multiple of kv_heads, or channels not of heads");
+    if (causal && rows > keys) return fail(PIXHIP_ERR_ARGUMENT,"causal attention needs a key for every query row (rows <= keys)");
+    const pixhip::AttnRange all = {0,rows,keys,causal != 0};
+    return attention_run(s,q,rows,k,v,keys,heads,kv_heads,channels,&all,1,0,output);
+}
+
+int pixhip_attention_ranges(pixhip_session* s, const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads,
+                            size_t kv_heads, size_t channels, const pixhip_attention_range* ranges, size_t count,
+                            size_t query_offset, float* output)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!q || !k || !v || !output || (count && !ranges)) return fail(PIXHIP_ERR_ARGUMENT,"null pointer");
+    // the reference's checks (src/tensor.cpp:386-394)
+    if (!rows || !keys || !heads || !kv_heads || heads % kv_heads || channels % heads || query_offset > SIZE_MAX - rows)
+        return fail(PIXHIP_ERR_ARGUMENT,"empty tensors, or heads not a multiple of kv_heads, or channels not of heads");
+    std::vector<pixhip::AttnRange> rs(count);
+    size_t covered = 0;
+    for (size_t i = 0; i < count; i++) {
+        const pixhip_attention_range& r = ranges[i];
+        if (r.query_begin != covered || r.query_end <= r.query_begin || r.query_end > rows || !r.key_end || r.key_end > keys)
+            return fail(PIXHIP_ERR_ARGUMENT,"ranges must tile the query rows in order with 0 < key_end <= keys");
+        covered = r.query_end;
+        rs[i] = {r.query_begin,r.query_end,r.key_end,r.causal != 0};
+    }
+    if (covered != rows) return fail(PIXHIP_ERR_ARGUMENT,"ranges must cover every query row");
+    return attention_run(s,q,rows,k,v,keys,heads,kv_heads,channels,rs.data(),count,query_offset,output);
 }
 
 int pixhip_block_sums(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t columns, int32_t* sums, int32_t* mins)

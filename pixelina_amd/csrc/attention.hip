@@ -1,0 +1,420 @@
+// Attention: tensor_attention (src/tensor.cpp:347-427) and vulkan_attention
+// (src/backend_vulkan.cpp:1318-1340) on bf16 MFMA (gfx950), head sizes up to
+// 128.
+//
+// Numerics: the reference works in fp32 (scores = dot * 1/sqrt(dim), exp(score
+// - max), probabilities p / sum, out += p * v).  Here every fp32 operand x of
+// the two products is split into bf16 halves hi = bf16(x), lo = bf16(x - hi),
+// and each product a*b is taken as hi_a*hi_b + hi_a*lo_b + lo_a*hi_b on
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation (the dropped lo*lo term and
+// the rounding of lo leave about 2^-16 relative per product), so the result
+// stays within the fp32 reference's tolerance at three times the bf16 MFMA
+// work, and far above what fp32 MFMAs would give.  Softmax is the online form
+// (running maximum and sum per query, output rescaled per key tile), in fp32.
+//
+// Layout: a split pass writes Q and K as bf16 planes [head][row][D] and V
+// transposed, [head][D][key], with the keys of each 16-key group permuted (bits
+// 2 and 3 swapped) so that the operand a lane needs for P*V is 16 contiguous
+// bytes (D = 64 or 128: the head size rounded up, zero-padded).
+//
+// Kernel: a workgroup of 8 waves owns 256 queries of one head (32 per wave)
+// and streams 64-key tiles of K and V^T (both planes) through a 2-stage LDS
+// ring with buffer_load ... lds.  Per tile each wave computes S^T = K * Q^T
+// (keys as MFMA rows, its 32 queries as columns, so each lane owns one query:
+// the softmax statistics and the output rescale stay in the lane), then O^T +=
+// V^T * P^T, where the P^T operand is the lane's own S^T results converted to
+// bf16 -- the key order the S^T output layout gives is matched by the V^T
+// permutation above.  Q stays in registers for the whole key loop.
+#include <math.h>
+
+#include "pixhip_device.h"
+#include "pixhip_internal.h"
+
+#define PIX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+namespace pixhip {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t ARsrc;
+
+constexpr int kAQ = 256;  // queries per workgroup
+constexpr int kAK = 64;   // keys per tile
+constexpr int kAWaves = 8, kAThreads = 64 * kAWaves;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+__device__ __forceinline__ uint32_t bf16_rne(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// x -> (hi, lo) bf16 bit patterns with x ~ hi + lo.
+__device__ __forceinline__ void split2(float x, uint32_t& hi, uint32_t& lo)
+{
+    hi = bf16_rne(x);
+    lo = bf16_rne(x - __uint_as_float(hi << 16));
+}
+
+// ---------------------------------------------------------------- split pass
+
+// src [n][stride] fp32, head h's values at h*dim; planes [heads][npad][D] bf16
+// (hi, lo), zero beyond n and dim.  One thread per (head, row, 8 values).
+__global__ __launch_bounds__(256) void attn_split_rows(const float* __restrict__ src, size_t n, size_t stride, int heads, int dim,
+                                                        int D, size_t npad, uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
+{
+    const size_t groups = (size_t)D / 8;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)heads * npad * groups) return;
+    const int g = (int)(idx % groups);
+    const size_t row = (idx / groups) % npad;
+    const int h = (int)(idx / (groups * npad));
+    u32x4 vh, vl;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t h0, l0, h1, l1;
+        const int d = 8 * g + 2 * i;
+        const float x0 = row < n && d < dim? src[row * stride + (size_t)h * dim + d] : 0.0f;
+        const float x1 = row < n && d + 1 < dim? src[row * stride + (size_t)h * dim + d + 1] : 0.0f;
+        split2(x0,h0,l0);
+        split2(x1,h1,l1);
+        vh[i] = h0 | (h1 << 16);
+        vl[i] = l0 | (l1 << 16);
+    }
+    const size_t o = ((size_t)h * npad + row) * D + 8 * g;
+    *reinterpret_cast<u32x4*>(hi + o) = vh;
+    *reinterpret_cast<u32x4*>(lo + o) = vl;
+}
+
+// Position of key j (0..15) of a 16-key group in a V^T row: j = 8a + 4b + c is
+// stored at 8b + 4a + c.
+__device__ __forceinline__ int vt_pos(int j)
+{
+    return (((j >> 2) & 1) << 3) | (((j >> 3) & 1) << 2) | (j & 3);
+}
+
+// src [n][stride] -> planes [heads][D][npad] bf16 (hi, lo), keys permuted
+// within 16-key groups, zero beyond n and dim.  One thread per (head, 16-key
+// group, d), d fastest (coalesced reads along a source row).
+__global__ __launch_bounds__(256) void attn_split_vt(const float* __restrict__ src, size_t n, size_t stride, int heads, int dim,
+                                                      int D, size_t npad, uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
+{
+    const size_t kg = npad / 16;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)heads * kg * D) return;
+    const int d = (int)(idx % D);
+    const size_t grp = (idx / D) % kg;
+    const int h = (int)(idx / ((size_t)D * kg));
+    uint32_t bh[16], bl[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const size_t key = grp * 16 + j;
+        const float x = key < n && d < dim? src[key * stride + (size_t)h * dim + d] : 0.0f;
+        split2(x,bh[vt_pos(j)],bl[vt_pos(j)]);
+    }
+    u32x4 w[4];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        w[i / 4][i % 4] = bh[2 * i] | (bh[2 * i + 1] << 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        w[2 + i / 4][i % 4] = bl[2 * i] | (bl[2 * i + 1] << 16);
+    }
+    const size_t o = ((size_t)h * D + d) * npad + grp * 16;
+    *reinterpret_cast<u32x4*>(hi + o) = w[0];
+    *reinterpret_cast<u32x4*>(hi + o + 8) = w[1];
+    *reinterpret_cast<u32x4*>(lo + o) = w[2];
+    *reinterpret_cast<u32x4*>(lo + o + 8) = w[3];
+}
+
+// ---------------------------------------------------------------- main kernel
+
+struct AttnArgs {
+    const uint16_t *qh, *ql, *kh, *kl, *vh, *vl;  // split planes
+    float* out;                                    // [rows][channels]
+    int rows_pad, keys_pad;
+    int heads, kv_group, dim, channels;
+    int qb, qe, key_end, causal, qoff;  // this range (query rows [qb, qe))
+    int tiles_q;
+    float scale;
+};
+
+template <typename T> __device__ __forceinline__ T lds_read(const uint8_t* p)
+{
+    return *reinterpret_cast<const T*>(p);
+}
+
+__device__ __forceinline__ void adma(ARsrc r, uint8_t* lds_uniform, uint32_t voff, uint32_t soff)
+{
+    __builtin_assume(lds_uniform != nullptr);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r,PIX_LDS(lds_uniform),16,(int)voff,(int)soff,0,0);
+}
+
+template <int N> __device__ __forceinline__ void attn_wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// 16-byte piece swizzles (conflict-free ds_read_b128 of 32 rows at one logical
+// piece): K rows of 2*D bytes, V^T rows of 128 bytes.
+template <int D> __device__ __forceinline__ int swz_k(int r)
+{
+    return D == 128? (r & 15) : ((r >> 1) & 7);
+}
+__device__ __forceinline__ int swz_v(int r)
+{
+    return (r >> 1) & 7;
+}
+
+template <int D>
+__global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
+{
+    constexpr int PK = D / 8;            // 16-byte pieces per K row
+    constexpr int PLANE = kAK * D * 2;   // bytes of one plane's tile (K: 64 rows x 2D; V^T: D rows x 128)
+    constexpr int STAGE = 4 * PLANE;     // K hi, K lo, V hi, V lo
+    constexpr int CHUNKS = STAGE / 1024;
+    constexpr int PER_WAVE = CHUNKS / kAWaves;
+    constexpr int KS = D / 16;           // k-steps of S^T
+    constexpr int TD = D / 32;           // output dim tiles
+    static_assert(PER_WAVE * kAWaves == CHUNKS, "stage DMAs split evenly");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+
+    const int head = (int)blockIdx.x / a.tiles_q, qt = (int)blockIdx.x % a.tiles_q;
+    const int kvh = head / a.kv_group;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63), lr = lane & 31, hh = lane >> 5;
+    const int q = a.qb + qt * kAQ + wave * 32 + lr;  // this lane's query row
+    const bool live = q < a.qe;
+    const int limit = !live? 1 : a.causal? min(a.key_end,a.qoff + q + 1) : a.key_end;
+    const int q_last = min(a.qe,a.qb + (qt + 1) * kAQ) - 1;
+    const int wg_limit = a.causal? min(a.key_end,a.qoff + q_last + 1) : a.key_end;
+    const int ntiles = (wg_limit + kAK - 1) / kAK;
+
+    // Q fragments (B operand of S^T: lane = query, 8 dims per k-step half)
+    bf16x8 qfh[KS], qfl[KS];
+    {
+        const size_t row = (size_t)head * a.rows_pad + min(q,a.rows_pad - 1);
+        const uint16_t* ph = a.qh + row * D + 8 * hh;
+        const uint16_t* pl = a.ql + row * D + 8 * hh;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            qfh[s] = *reinterpret_cast<const bf16x8*>(ph + 16 * s);
+            qfl[s] = *reinterpret_cast<const bf16x8*>(pl + 16 * s);
+        }
+    }
+
+    const size_t kplane = (size_t)a.keys_pad * D * 2;
+    const ARsrc rk[2] = {__builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.kh) + (size_t)kvh * a.keys_pad * D,(short)0,(int)kplane,
+                                                           0x00020000),
+                         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.kl) + (size_t)kvh * a.keys_pad * D,(short)0,(int)kplane,
+                                                           0x00020000)};
+    const ARsrc rv[2] = {__builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.vh) + (size_t)kvh * a.keys_pad * D,(short)0,(int)kplane,
+                                                           0x00020000),
+                         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.vl) + (size_t)kvh * a.keys_pad * D,(short)0,(int)kplane,
+                                                           0x00020000)};
+
+    // DMA of key tile kt into stage `st`: chunk c = wave + 8i of the stage's
+    // 4 planes; lane j of a chunk lands at chunk + 16j, which holds row r,
+    // physical piece p of the plane, i.e. logical piece p ^ swizzle(r).
+    auto issue = [&](int kt, int st) {
+        uint8_t* base = lds + st * STAGE;
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; i++) {
+            const int c = wave + kAWaves * i;
+            const int plane = c / (PLANE / 1024), ci = c % (PLANE / 1024);
+            uint8_t* dst = base + plane * PLANE + ci * 1024;
+            if (plane < 2) {
+                const int r = ci * (1024 / (2 * D)) + lane / PK, p = lane % PK;
+                const uint32_t off = (uint32_t)((kt * kAK + r) * D * 2 + 16 * (p ^ swz_k<D>(r)));
+                adma(rk[plane],dst,off,0);
+            } else {
+                const int r = ci * 8 + lane / 8, p = lane % 8;
+                const uint32_t off = (uint32_t)(((size_t)r * a.keys_pad + kt * kAK) * 2 + 16 * (p ^ swz_v(r)));
+                adma(rv[plane - 2],dst,off,0);
+            }
+        }
+    };
+
+    v16f o[TD];
+#pragma unroll
+    for (int t = 0; t < TD; t++) o[t] = v16f{};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    if (ntiles > 0) issue(0,0);
+    for (int kt = 0; kt < ntiles; kt++) {
+        attn_wait_vmcnt<0>();
+        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < ntiles) issue(kt + 1,(kt + 1) & 1);
+        const uint8_t* st = lds + (kt & 1) * STAGE;
+
+        // S^T = K * Q^T for the tile's two 32-key halves
+        v16f s[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            s[u] = v16f{};
+            const int r = 32 * u + lr;
+            const uint8_t* rowh = st + r * (2 * D);
+            const uint8_t* rowl = st + PLANE + r * (2 * D);
+#pragma unroll
+            for (int k = 0; k < KS; k++) {
+                const int piece = (2 * k + hh) ^ swz_k<D>(r);
+                const bf16x8 ah = lds_read<bf16x8>(rowh + 16 * piece);
+                const bf16x8 al = lds_read<bf16x8>(rowl + 16 * piece);
+                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfh[k],s[u],0,0,0);
+                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfl[k],s[u],0,0,0);
+                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,qfh[k],s[u],0,0,0);
+            }
+        }
+
+        // online softmax over this lane's query (the other 32 keys of each
+        // half sit in lane ^ 32)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = kt * kAK + 32 * u + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const float x = key < limit? s[u][r] * a.scale : -INFINITY;
+                s[u][r] = x;
+                mx = fmaxf(mx,x);
+            }
+        mx = fmaxf(mx,__shfl_xor(mx,32));
+        const float m_new = fmaxf(m_run,mx);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
+        float psum = 0.0f;
+        uint32_t ph[4][4], pl[4][4];  // [k-step of P*V][dword]: bf16 pairs
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const float p0 = __builtin_amdgcn_exp2f((s[u][r] - m_new) * kLog2e);
+                const float p1 = __builtin_amdgcn_exp2f((s[u][r + 1] - m_new) * kLog2e);
+                psum += p0;
+                psum += p1;
+                uint32_t h0, l0, h1, l1;
+                split2(p0,h0,l0);
+                split2(p1,h1,l1);
+                const int t = 2 * u + r / 8, w = (r % 8) / 2;
+                ph[t][w] = h0 | (h1 << 16);
+                pl[t][w] = l0 | (l1 << 16);
+            }
+        psum += __shfl_xor(psum,32);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int t = 0; t < TD; t++) o[t] *= alpha;
+
+        // O^T += V^T * P^T
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const bf16x8 bh = __builtin_bit_cast(bf16x8,u32x4{ph[t][0],ph[t][1],ph[t][2],ph[t][3]});
+            const bf16x8 bl = __builtin_bit_cast(bf16x8,u32x4{pl[t][0],pl[t][1],pl[t][2],pl[t][3]});
+#pragma unroll
+            for (int td = 0; td < TD; td++) {
+                const int r = 32 * td + lr;
+                const int piece = (2 * t + hh) ^ swz_v(r);
+                const bf16x8 ah = lds_read<bf16x8>(st + 2 * PLANE + r * 128 + 16 * piece);
+                const bf16x8 al = lds_read<bf16x8>(st + 3 * PLANE + r * 128 + 16 * piece);
+                o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,bh,o[td],0,0,0);
+                o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,bl,o[td],0,0,0);
+                o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,bh,o[td],0,0,0);
+            }
+        }
+    }
+    attn_wait_vmcnt<0>();
+
+    // out[q][head*dim + d] = O^T[d][q] / l: lane holds 4 consecutive dims per
+    // (tile, row group)
+    if (!live) return;
+    float* row = a.out + (size_t)q * a.channels + (size_t)head * a.dim;
+    const bool vec = (a.dim & 3) == 0;
+#pragma unroll
+    for (int td = 0; td < TD; td++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int d0 = 32 * td + 8 * g + 4 * hh;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = o[td][4 * g + i] / l_run;
+            if (vec && d0 + 4 <= a.dim) {
+                *reinterpret_cast<float4*>(row + d0) = make_float4(v[0],v[1],v[2],v[3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (d0 + i < a.dim) row[d0 + i] = v[i];
+            }
+        }
+}
+
+// ---------------------------------------------------------------- host side
+
+static size_t aru(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+int attention_dim_pad(size_t dim)
+{
+    return dim == 0? 0 : dim <= 64? 64 : dim <= 128? 128 : 0;
+}
+
+size_t attention_workspace_bytes(size_t rows, size_t keys, size_t heads, size_t kv_heads, size_t dim)
+{
+    const int D = attention_dim_pad(dim);
+    if (!D) return 0;
+    const size_t q = heads * aru(rows,kAQ) * D, kv = kv_heads * aru(keys,kAK) * D;
+    return 2 * (q + 2 * kv) * sizeof(uint16_t);
+}
+
+hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, size_t rows, size_t keys, size_t heads,
+                            size_t kv_heads, size_t dim, const AttnRange* ranges, size_t count, size_t query_offset, void* workspace,
+                            hipStream_t s)
+{
+    const int D = attention_dim_pad(dim);
+    if (!D || !heads || !kv_heads || heads % kv_heads || !rows || !keys) return hipErrorInvalidValue;
+    const size_t rows_pad = aru(rows,kAQ), keys_pad = aru(keys,kAK);
+    const size_t channels = heads * dim, kv_channels = kv_heads * dim;
+    // 32-bit bounds: the per-head K / V^T planes are addressed with 32-bit
+    // buffer offsets, and the kernel's row indexes are ints.
+    if (keys_pad * D * 2 >= ((size_t)1 << 31) || rows_pad + query_offset >= ((size_t)1 << 31) || keys >= ((size_t)1 << 30))
+        return hipErrorInvalidValue;
+    uint16_t* w = static_cast<uint16_t*>(workspace);
+    const size_t qn = heads * rows_pad * D, kn = kv_heads * keys_pad * D;
+    uint16_t *qh = w, *ql = qh + qn, *kh = ql + qn, *kl = kh + kn, *vh = kl + kn, *vl = vh + kn;
+    {
+        const size_t nq = heads * rows_pad * (D / 8), nk = kv_heads * keys_pad * (D / 8), nv = kv_heads * (keys_pad / 16) * D;
+        attn_split_rows<<<dim3((unsigned)((nq + 255) / 256)),dim3(256),0,s>>>(q,rows,channels,(int)heads,(int)dim,D,rows_pad,qh,ql);
+        attn_split_rows<<<dim3((unsigned)((nk + 255) / 256)),dim3(256),0,s>>>(k,keys,kv_channels,(int)kv_heads,(int)dim,D,keys_pad,kh,kl);
+        attn_split_vt<<<dim3((unsigned)((nv + 255) / 256)),dim3(256),0,s>>>(v,keys,kv_channels,(int)kv_heads,(int)dim,D,keys_pad,vh,vl);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    AttnArgs a = {};
+    a.qh = qh; a.ql = ql; a.kh = kh; a.kl = kl; a.vh = vh; a.vl = vl;
+    a.out = out;
+    a.rows_pad = (int)rows_pad;
+    a.keys_pad = (int)keys_pad;
+    a.heads = (int)heads;
+    a.kv_group = (int)(heads / kv_heads);
+    a.dim = (int)dim;
+    a.channels = (int)channels;
+    a.qoff = (int)query_offset;
+    a.scale = 1.0f / sqrtf((float)dim);
+    for (size_t i = 0; i < count; i++) {
+        const AttnRange& r = ranges[i];
+        if (r.query_end <= r.query_begin || r.query_end > rows || !r.key_end || r.key_end > keys) return hipErrorInvalidValue;
+        a.qb = (int)r.query_begin;
+        a.qe = (int)r.query_end;
+        a.key_end = (int)r.key_end;
+        a.causal = r.causal? 1 : 0;
+        a.tiles_q = (int)((r.query_end - r.query_begin + kAQ - 1) / kAQ);
+        const dim3 grid((unsigned)(heads * a.tiles_q));
+        if (D == 128) attn_kernel<128><<<grid,dim3(kAThreads),0,s>>>(a);
+        else attn_kernel<64><<<grid,dim3(kAThreads),0,s>>>(a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace pixhip

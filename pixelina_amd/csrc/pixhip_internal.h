@@ -199,6 +199,22 @@ hipError_t launch_sums_q5_K(const Act8K& a, const PlanesQ5K& w, size_t M, size_t
 hipError_t launch_sums_q6_K(const Act8K& a, const PlanesQ6K& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s);
 hipError_t launch_sums_q8_0(const Act80& a, const PlanarQ80& w, size_t M, size_t N, size_t K, int32_t* sums, hipStream_t s);
 
+// attention.hip
+// One PixAttentionRange (src/tensor.h:58-63).
+struct AttnRange {
+    size_t query_begin, query_end, key_end;
+    bool causal;
+};
+// Head size rounded up to the kernel's (64 or 128); 0 when not supported.
+int attention_dim_pad(size_t dim);
+// Workspace of launch_attention (bf16 split planes of Q, K and V^T).
+size_t attention_workspace_bytes(size_t rows, size_t keys, size_t heads, size_t kv_heads, size_t dim);
+// out [rows][heads*dim] for q [rows][heads*dim], k and v [keys][kv_heads*dim]
+// (device pointers), one kernel launch per range (a range's rows only).
+hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, size_t rows, size_t keys, size_t heads,
+                            size_t kv_heads, size_t dim, const AttnRange* ranges, size_t count, size_t query_offset, void* workspace,
+                            hipStream_t s);
+
 // matvec.hip
 hipError_t launch_matvec_q5_K(const PlanarQ5K& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);
 hipError_t launch_matvec_q8_0(const PlanarQ80& w, const float* x, size_t N, size_t K, const Output& out, hipStream_t s);

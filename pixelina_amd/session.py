@@ -149,6 +149,17 @@ class Session:
     def rope(self, x_ptr, rows, channels, heads, cos_ptr, sin_ptr, interleaved):
         return self.lib.pixhip_rope(self.handle, x_ptr, rows, channels, heads, cos_ptr, sin_ptr, int(interleaved))
 
+    def attention(self, q_ptr, rows, k_ptr, v_ptr, keys, heads, kv_heads, channels, out_ptr, causal=False, ranges=None,
+                  query_offset=0):
+        """tensor_attention (src/tensor.cpp:347-427): the causal form, or the
+        ranges form when `ranges` [(query_begin, query_end, key_end, causal)]."""
+        if ranges is None:
+            return self.lib.pixhip_attention(self.handle, q_ptr, rows, k_ptr, v_ptr, keys, heads, kv_heads, channels,
+                                             int(causal), out_ptr)
+        arr = (_lib.AttentionRange * max(1, len(ranges)))(*[_lib.AttentionRange(*r) for r in ranges])
+        return self.lib.pixhip_attention_ranges(self.handle, q_ptr, rows, k_ptr, v_ptr, keys, heads, kv_heads, channels,
+                                                arr, len(ranges), query_offset, out_ptr)
+
     def block_sums(self, weight, x_ptr, columns, sums_ptr, mins_ptr=None):
         return self.lib.pixhip_block_sums(self.handle, weight, x_ptr, columns, sums_ptr, mins_ptr)
 

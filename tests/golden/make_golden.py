@@ -17,6 +17,9 @@ Fixtures (numpy .npz, data only):
                         values, and the Q8_K / Q8_0 blocks of the product
   g7_ops.npz            tensor_gelu (both forms), tensor_bias, tensor_add and
                         tensor_rope (split and interleaved halves)
+  g9_attention.npz      tensor_attention, causal form and ranges form: MHA and
+                        grouped heads, head sizes 64 / 72 / 128, causal and
+                        not, ranges with a query offset
 
     python tests/golden/make_golden.py g5 g6 g7   # only the named fixtures
 """
@@ -30,8 +33,8 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.dirname(HERE))
 
-from oracle_lib import (Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, norm_rows, quant_matmul, quantize, reference,  # noqa: E402
-                        rope, silu_gate)
+from oracle_lib import (Q5_K, Q6_K, Q8_0, add, attention, bias, dot, gelu, norm_rows, quant_matmul, quantize,  # noqa: E402
+                        reference, rope, silu_gate)
 from pixelina_amd import synth  # noqa: E402
 
 
@@ -141,6 +144,32 @@ def write_g7(ref):
                         rope_interleaved=rope(ref, "ref", x, heads, cos, sin, 1))
 
 
+# (rows, keys, heads, kv_heads, dim, causal, ranges or None, query_offset)
+G9_CASES = [
+    (33, 33, 4, 4, 64, 0, None, 0),
+    (40, 40, 6, 2, 64, 1, None, 0),
+    (24, 57, 2, 1, 72, 0, None, 0),
+    (64, 64, 2, 2, 128, 1, None, 0),
+    (30, 48, 4, 2, 64, 0, [(0, 7, 9, 1), (7, 30, 48, 0)], 5),
+    (20, 20, 3, 1, 128, 0, [(0, 12, 12, 0), (12, 20, 20, 1)], 0),
+]
+
+
+def write_g9(ref):
+    rng = np.random.default_rng(909)
+    g = {"count": np.array(len(G9_CASES))}
+    for c, (rows, keys, heads, kvh, dim, causal, ranges, offset) in enumerate(G9_CASES):
+        q = (rng.standard_normal((rows, heads * dim)) * 1.5).astype(np.float32)
+        k = (rng.standard_normal((keys, kvh * dim)) * 1.5).astype(np.float32)
+        v = rng.standard_normal((keys, kvh * dim)).astype(np.float32)
+        y = attention(ref, "ref", q, k, v, heads, kvh, ranges, offset, causal=bool(causal))
+        assert y is not None
+        g[f"c{c}_shape"] = np.array([rows, keys, heads, kvh, dim, causal, offset])
+        g[f"c{c}_ranges"] = np.array(ranges if ranges else [], np.uint64).reshape(-1, 4)
+        g[f"c{c}_q"], g[f"c{c}_k"], g[f"c{c}_v"], g[f"c{c}_y"] = q, k, v, y
+    np.savez_compressed(os.path.join(HERE, "g9_attention.npz"), **g)
+
+
 def main():
     ref = reference()
     if ref is None:
@@ -153,6 +182,8 @@ def main():
             write_g6(ref)
         if "g7" in only:
             write_g7(ref)
+        if "g9" in only:
+            write_g9(ref)
         return
     rng = np.random.default_rng(20260101)
 
@@ -217,6 +248,7 @@ def main():
     write_g5(ref)
     write_g6(ref)
     write_g7(ref)
+    write_g9(ref)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -47,6 +47,7 @@ def load_oracle(path):
         "orc_bias": (None, [_vp, _sz, _sz, _vp]),
         "orc_add": (None, [_vp, _vp, _sz]),
         "orc_rope": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _int]),
+        "orc_attention": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -89,6 +90,8 @@ def reference():
             "ref_bias": (None, [_vp, _sz, _sz, _vp]),
             "ref_add": (None, [_vp, _vp, _sz]),
             "ref_rope": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _int]),
+            "ref_attention": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _int, _vp]),
+            "ref_attention_ranges": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -195,6 +198,28 @@ def rope(lib, prefix, x, heads, cosine, sine, interleaved):
     getattr(lib, f"{prefix}_rope")(ptr(y), y.shape[0], y.shape[1], heads, ptr(np.ascontiguousarray(cosine, dtype=np.float32)),
                                    ptr(np.ascontiguousarray(sine, dtype=np.float32)), int(interleaved))
     return y
+
+
+def attention(lib, prefix, q, k, v, heads, kv_heads, ranges=None, query_offset=0, causal=False):
+    """tensor_attention through either library: `ranges` [(query_begin,
+    query_end, key_end, causal)] selects the ranges form; without it the causal
+    form (the reference's own entry for prefix "ref", the one range {0, rows,
+    keys, causal} for the oracle).  None when the library rejects the call."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    rows, channels = q.shape
+    keys = k.shape[0]
+    out = np.zeros((rows, channels), np.float32)
+    if ranges is None and prefix == "ref":
+        ok = lib.ref_attention(ptr(q), rows, ptr(k), ptr(v), keys, heads, kv_heads, channels, int(causal), ptr(out))
+        return out if ok else None
+    if ranges is None:
+        ranges = [(0, rows, keys, int(causal))]
+    rg = np.ascontiguousarray(np.array(ranges, dtype=np.uint64).reshape(-1, 4))
+    fn = lib.ref_attention_ranges if prefix == "ref" else lib.orc_attention
+    ok = fn(ptr(q), rows, ptr(k), ptr(v), keys, heads, kv_heads, channels, ptr(rg), len(rg), query_offset, ptr(out))
+    return out if ok else None
 
 
 def decode(lib, w, wtype, count):

@@ -1,0 +1,144 @@
+"""pixhip_attention / pixhip_attention_ranges (tensor_attention,
+src/tensor.cpp:347-427) through the C ABI, against the reference's own outputs
+(tests/golden/g9_attention, written by the compiled src/tensor.cpp) and the
+oracle (oracle/pix_oracle.c orc_attention, bit-exact with the reference).
+
+The kernel computes the two products with three bf16 MFMA terms per fp32
+product and an online fp32 softmax, so results are held to TOL = 1e-4 of each
+output row's largest magnitude (max |y - r| / max |r| per row).  At the DiT
+shape (30 heads of 128, 4608 tokens) the oracle runs on a sample of query rows
+(non-causal rows are independent of each other).  Size-independent properties
+at full size: V of ones gives ones, a key permutation leaves non-causal
+outputs unchanged, and repeats are bit-identical.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from gpu_helpers import TOL, row_rel_error
+from oracle_lib import attention, oracle
+from pixelina_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def sess():
+    from gpu_helpers import new_session
+    s = new_session()
+    yield s
+    s.close()
+
+
+def gpu_attention(sess, q, k, v, heads, kv_heads, causal=False, ranges=None, query_offset=0):
+    q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
+    rows, channels = q.shape
+    keys = k.shape[0]
+    qb, kb, vb = sess.to_device(q), sess.to_device(k), sess.to_device(v)
+    ob = sess.alloc(rows * channels * 4)
+    rc = sess.attention(qb.ptr, rows, kb.ptr, vb.ptr, keys, heads, kv_heads, channels, ob.ptr, causal, ranges, query_offset)
+    _lib.check(rc, "attention")
+    y = ob.download(np.float32, rows * channels).reshape(rows, channels)
+    for b in (qb, kb, vb, ob):
+        b.free()
+    return y
+
+
+def qkv(rng, rows, keys, heads, kv_heads, dim, qscale=1.5):
+    q = (rng.standard_normal((rows, heads * dim)) * qscale).astype(np.float32)
+    k = (rng.standard_normal((keys, kv_heads * dim)) * qscale).astype(np.float32)
+    v = rng.standard_normal((keys, kv_heads * dim)).astype(np.float32)
+    return q, k, v
+
+
+def test_reference_vectors(sess):
+    g = np.load(os.path.join(GOLDEN, "g9_attention.npz"))
+    for c in range(int(g["count"])):
+        rows, keys, heads, kvh, dim, causal, offset = (int(v) for v in g[f"c{c}_shape"])
+        ranges = [tuple(int(x) for x in r) for r in g[f"c{c}_ranges"]] or None
+        print(f"case {c}: rows={rows} keys={keys} heads={heads}/{kvh} dim={dim} causal={causal} ranges={ranges}", flush=True)
+        y = gpu_attention(sess, g[f"c{c}_q"], g[f"c{c}_k"], g[f"c{c}_v"], heads, kvh, bool(causal), ranges, offset)
+        err = row_rel_error(y, g[f"c{c}_y"]).max()
+        print(f"  rel={err:.2e}", flush=True)
+        assert err <= TOL, (c, err)
+
+
+@pytest.mark.parametrize("rows,keys,heads,kvh,dim,causal", [
+    (300, 300, 32, 8, 128, True),     # Qwen LM block: grouped heads, causal
+    (700, 700, 16, 16, 72, False),    # Qwen vision: head size 72
+    (257, 513, 4, 2, 64, False),      # ragged tiles, head size 64
+    (1, 77, 8, 8, 128, False),        # one query row
+    (65, 65, 2, 1, 40, True),         # head size 40 (zero-padded to 64)
+    (90, 90, 3, 3, 30, False),        # head size 30: rows not 16-byte aligned, scalar stores
+])
+def test_against_oracle(sess, rows, keys, heads, kvh, dim, causal):
+    rng = np.random.default_rng(rows * 7 + dim)
+    q, k, v = qkv(rng, rows, keys, heads, kvh, dim)
+    print(f"rows={rows} keys={keys} heads={heads}/{kvh} dim={dim} causal={causal}", flush=True)
+    y = gpu_attention(sess, q, k, v, heads, kvh, causal)
+    ref = attention(oracle(), "orc", q, k, v, heads, kvh, causal=causal)
+    err = row_rel_error(y, ref).max()
+    print(f"  rel={err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_ranges_with_query_offset(sess):
+    """The Qwen-Image layout: a causal text prefix, then image rows seeing every
+    key, then rows limited to a key prefix, with a query offset (KV cache)."""
+    rng = np.random.default_rng(41)
+    rows, keys, heads, dim, offset = 600, 700, 4, 128, 100
+    q, k, v = qkv(rng, rows, keys, heads, heads, dim)
+    ranges = [(0, 90, 700, 1), (90, 400, 700, 0), (400, 600, 333, 0)]
+    y = gpu_attention(sess, q, k, v, heads, heads, ranges=ranges, query_offset=offset)
+    ref = attention(oracle(), "orc", q, k, v, heads, heads, ranges, offset)
+    err = row_rel_error(y, ref).max()
+    print(f"rel={err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_dit_shape_sampled(sess):
+    """Z-Image DiT self-attention: 30 heads of 128, 4608 tokens, not causal;
+    the oracle on 48 query rows spread over the sequence."""
+    rng = np.random.default_rng(4608)
+    rows, heads, dim = 4608, 30, 128
+    q, k, v = qkv(rng, rows, rows, heads, heads, dim)
+    y = gpu_attention(sess, q, k, v, heads, heads)
+    pick = np.linspace(0, rows - 1, 48).astype(int)
+    ref = attention(oracle(), "orc", q[pick], k, v, heads, heads)
+    err = row_rel_error(y[pick], ref).max()
+    print(f"sampled rel={err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_properties_at_full_size(sess):
+    rng = np.random.default_rng(9)
+    rows, heads, dim = 4608, 30, 128
+    q, k, _ = qkv(rng, rows, rows, heads, heads, dim)
+    ones = np.ones((rows, heads * dim), np.float32)
+    y = gpu_attention(sess, q, k, ones, heads, heads)
+    assert np.abs(y - 1.0).max() <= 1e-5
+    v = rng.standard_normal((rows, heads * dim)).astype(np.float32)
+    y1 = gpu_attention(sess, q, k, v, heads, heads)
+    perm = rng.permutation(rows)
+    y2 = gpu_attention(sess, q, k[perm], v[perm], heads, heads)
+    assert row_rel_error(y2, y1).max() <= TOL
+    y3 = gpu_attention(sess, q, k, v, heads, heads)
+    assert np.array_equal(y1.view(np.uint32), y3.view(np.uint32)), "repeats differ"
+
+
+def test_errors(sess):
+    rng = np.random.default_rng(1)
+    q, k, v = qkv(rng, 8, 8, 2, 2, 64)
+    qb, kb, vb, ob = sess.to_device(q), sess.to_device(k), sess.to_device(v), sess.alloc(q.nbytes)
+    arg = _lib.ERR_ARGUMENT
+    assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 3, 1, 128, ob.ptr) == arg          # channels not of heads
+    assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 2, 3, 128, ob.ptr) == arg          # heads not of kv_heads
+    assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 7, 2, 2, 128, ob.ptr, True) == arg    # causal, rows > keys
+    assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 1, 1, 128 * 2, ob.ptr) == _lib.ERR_UNSUPPORTED  # head size 256
+    for bad in ([(0, 3, 8, 0)], [(1, 8, 8, 0)], [(0, 8, 0, 0)], [(0, 8, 9, 0)], [(0, 4, 8, 0), (5, 8, 8, 0)]):
+        assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 2, 2, 128, ob.ptr, ranges=bad) == arg, bad
+    for b in (qb, kb, vb, ob):
+        b.free()

@@ -8,8 +8,8 @@ import os
 import numpy as np
 import pytest
 
-from oracle_lib import (Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, norm_rows, oracle, quant_matmul, quantize, reference, rope,
-                        silu_gate)
+from oracle_lib import (Q5_K, Q6_K, Q8_0, add, attention, bias, dot, gelu, norm_rows, oracle, quant_matmul, quantize, reference,
+                        rope, silu_gate)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 WTYPES = {"q8_0": Q8_0, "q5_K": Q5_K, "q6_K": Q6_K}
@@ -155,3 +155,59 @@ def test_elementwise_ops_match_reference_vectors():
         cs, sn = rng.standard_normal((2, 16, 64)).astype(np.float32)
         for il in (0, 1):
             assert np.array_equal(bits(rope(o, "orc", x, 4, cs, sn, il)), bits(rope(ref, "ref", x, 4, cs, sn, il)))
+
+
+def g9_cases():
+    g = golden("g9_attention")
+    for c in range(int(g["count"])):
+        rows, keys, heads, kvh, dim, causal, offset = (int(v) for v in g[f"c{c}_shape"])
+        ranges = [tuple(int(x) for x in r) for r in g[f"c{c}_ranges"]] or None
+        yield c, g[f"c{c}_q"], g[f"c{c}_k"], g[f"c{c}_v"], heads, kvh, causal, ranges, offset, g[f"c{c}_y"]
+
+
+def test_attention_matches_reference_vectors():
+    """tensor_attention (src/tensor.cpp:347-427): both forms, grouped heads,
+    head sizes 64 / 72 / 128, ranges with a query offset; bit-exact."""
+    o = oracle()
+    for c, q, k, v, heads, kvh, causal, ranges, offset, y in g9_cases():
+        got = attention(o, "orc", q, k, v, heads, kvh, ranges, offset, causal=bool(causal))
+        assert got is not None and np.array_equal(bits(got), bits(y)), c
+
+
+def test_attention_closed_forms():
+    """What fixes attention without the reference: one key gives v exactly
+    (probability 1); equal scores give the mean of v; a causal first row sees
+    only key 0; the ranges form rejects what the reference rejects
+    (src/tensor.cpp:386-394)."""
+    o = oracle()
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((5, 2 * 64)).astype(np.float32)
+    k = rng.standard_normal((1, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 64)).astype(np.float32)
+    y = attention(o, "orc", q, k, v, 2, 1)
+    assert np.array_equal(y, np.tile(v, (5, 2)))
+    k = np.zeros((6, 64), np.float32)
+    v = rng.standard_normal((6, 64)).astype(np.float32)
+    y = attention(o, "orc", q, k, v, 2, 1)
+    assert np.allclose(y, np.tile(v.mean(0), (5, 2)), rtol=1e-6, atol=1e-6)
+    k = rng.standard_normal((6, 64)).astype(np.float32)
+    y = attention(o, "orc", q, k, v, 2, 1, causal=True)
+    assert np.array_equal(y[0], np.tile(v[0], 2))
+    for bad in ([(0, 3, 6, 0)], [(1, 5, 6, 0)], [(0, 5, 0, 0)], [(0, 5, 7, 0)], [(0, 2, 6, 0), (3, 5, 6, 0)]):
+        assert attention(o, "orc", q, k, v, 2, 1, bad) is None, bad
+    assert attention(o, "orc", q, k, v, 3, 1, [(0, 5, 6, 0)]) is None  # channels not a multiple of heads
+
+
+@pytest.mark.skipif(reference() is None, reason="oracle/_ref not built here")
+@pytest.mark.parametrize("seed", [1, 2])
+def test_attention_equals_compiled_reference(seed):
+    o, ref = oracle(), reference()
+    rng = np.random.default_rng(100 + seed)
+    rows, keys, heads, kvh, dim = 19 + seed, 45, 6, 3, 48 + 32 * seed
+    q = rng.standard_normal((rows, heads * dim)).astype(np.float32) * 2
+    k = rng.standard_normal((keys, kvh * dim)).astype(np.float32) * 2
+    v = rng.standard_normal((keys, kvh * dim)).astype(np.float32)
+    rg = [(0, 4, 10, 1), (4, 9, 45, 0), (9, rows, 40, 1)]
+    assert np.array_equal(bits(attention(o, "orc", q, k, v, heads, kvh, rg, 7)), bits(attention(ref, "ref", q, k, v, heads, kvh, rg, 7)))
+    assert np.array_equal(bits(attention(o, "orc", q, k[:rows], v[:rows], heads, kvh, causal=True)),
+                          bits(attention(ref, "ref", q, k[:rows], v[:rows], heads, kvh, causal=True)))

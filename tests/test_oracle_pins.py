@@ -9,8 +9,8 @@ import subprocess
 import numpy as np
 import pytest
 
-from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, add, bias, dot, gelu, load_oracle, modulate_rows, norm_rows, oracle, ptr,
-                        quant_matmul, quantize, rope, silu_gate)
+from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, add, attention, bias, dot, gelu, load_oracle, modulate_rows, norm_rows,
+                        oracle, ptr, quant_matmul, quantize, rope, silu_gate)
 from pixelina_amd import synth
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -350,6 +350,8 @@ MUTANTS = {
     12: "tanh GELU with v*v instead of v*v*v",
     13: "modulation as x + x*scale",
     14: "modulation by scale instead of 1 + scale",
+    15: "attention's grouped heads as head % kv_heads",
+    16: "causal attention without the query's own key",
 }
 
 
@@ -386,6 +388,12 @@ def golden_mismatches(lib):
                       (rope(lib, "orc", g7["x"], h, g7["cos"], g7["sin"], 0), g7["rope_split"]),
                       (rope(lib, "orc", g7["x"], h, g7["cos"], g7["sin"], 1), g7["rope_interleaved"])):
         bad += int(not np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+    g9 = np.load(os.path.join(GOLDEN, "g9_attention.npz"))
+    for c in range(int(g9["count"])):
+        rows, keys, heads, kvh, dim, causal, offset = (int(v) for v in g9[f"c{c}_shape"])
+        ranges = [tuple(int(x) for x in r) for r in g9[f"c{c}_ranges"]] or None
+        got = attention(lib, "orc", g9[f"c{c}_q"], g9[f"c{c}_k"], g9[f"c{c}_v"], heads, kvh, ranges, offset, causal=bool(causal))
+        bad += int(got is None or not np.array_equal(got.view(np.uint32), g9[f"c{c}_y"].view(np.uint32)))
     return bad
 
 
