@@ -27,6 +27,8 @@
 // permutation above.  Q stays in registers for the whole key loop.
 #include <math.h>
 
+#include <algorithm>
+
 #include "pixhip_device.h"
 #include "pixhip_internal.h"
 
@@ -138,6 +140,13 @@ struct AttnArgs {
     int qb, qe, key_end, causal, qoff;  // this range (query rows [qb, qe))
     int tiles_q;
     float scale;
+    // Key-split tail: units (head, query tile) full.. run as `splits` pieces of
+    // their key tiles each, writing unnormalised outputs and the running
+    // maximum and sum to `part` ([piece][unit - full][256 queries][D + 4]:
+    // the D outputs, the maximum, the sum, two unused), which attn_combine
+    // merges.
+    int full, tail, splits;
+    float* part;
 };
 
 template <typename T> __device__ __forceinline__ T lds_read(const uint8_t* p)
@@ -181,7 +190,12 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
     static_assert(PER_WAVE * kAWaves == CHUNKS, "stage DMAs split evenly");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
-    const int head = (int)blockIdx.x / a.tiles_q, qt = (int)blockIdx.x % a.tiles_q;
+    const int bid = (int)blockIdx.x;
+    const bool piece = bid >= a.full;
+    const int pidx = bid - a.full;
+    const int unit = piece? a.full + pidx % a.tail : bid;
+    const int split = piece? pidx / a.tail : 0;
+    const int head = unit / a.tiles_q, qt = unit % a.tiles_q;
     const int kvh = head / a.kv_group;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = (int)(threadIdx.x & 63), lr = lane & 31, hh = lane >> 5;
@@ -190,7 +204,9 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
     const int limit = !live? 1 : a.causal? min(a.key_end,a.qoff + q + 1) : a.key_end;
     const int q_last = min(a.qe,a.qb + (qt + 1) * kAQ) - 1;
     const int wg_limit = a.causal? min(a.key_end,a.qoff + q_last + 1) : a.key_end;
-    const int ntiles = (wg_limit + kAK - 1) / kAK;
+    const int all_tiles = (wg_limit + kAK - 1) / kAK;
+    const int t0 = piece? split * all_tiles / a.splits : 0;
+    const int t1 = piece? (split + 1) * all_tiles / a.splits : all_tiles;
 
     // Q fragments (B operand of S^T: lane = query, 8 dims per k-step half)
     bf16x8 qfh[KS], qfl[KS];
@@ -242,12 +258,12 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
     for (int t = 0; t < TD; t++) o[t] = v16f{};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    if (ntiles > 0) issue(0,0);
-    for (int kt = 0; kt < ntiles; kt++) {
+    if (t0 < t1) issue(t0,t0 & 1);
+    for (int kt = t0; kt < t1; kt++) {
         attn_wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        if (kt + 1 < ntiles) issue(kt + 1,(kt + 1) & 1);
+        if (kt + 1 < t1) issue(kt + 1,(kt + 1) & 1);
         const uint8_t* st = lds + (kt & 1) * STAGE;
 
         // S^T = K * Q^T for the tile's two 32-key halves
@@ -283,15 +299,19 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
             }
         mx = fmaxf(mx,__shfl_xor(mx,32));
         const float m_new = fmaxf(m_run,mx);
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
+        // A query can see no key of a whole key piece (causal rows in a
+        // tail piece past their limit): keep its state at zero instead of
+        // exp(-inf - -inf).
+        const float m_ref = m_new == -INFINITY? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_ref) * kLog2e);
         float psum = 0.0f;
         uint32_t ph[4][4], pl[4][4];  // [k-step of P*V][dword]: bf16 pairs
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
             for (int r = 0; r < 16; r += 2) {
-                const float p0 = __builtin_amdgcn_exp2f((s[u][r] - m_new) * kLog2e);
-                const float p1 = __builtin_amdgcn_exp2f((s[u][r + 1] - m_new) * kLog2e);
+                const float p0 = __builtin_amdgcn_exp2f((s[u][r] - m_ref) * kLog2e);
+                const float p1 = __builtin_amdgcn_exp2f((s[u][r + 1] - m_ref) * kLog2e);
                 psum += p0;
                 psum += p1;
                 uint32_t h0, l0, h1, l1;
@@ -326,6 +346,22 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
     }
     attn_wait_vmcnt<0>();
 
+    if (piece) {
+        // unnormalised O^T (as [query][D]) and the running max / sum
+        float* rec = a.part + ((size_t)(split * a.tail + pidx % a.tail) * kAQ + wave * 32 + lr) * (D + 4);
+#pragma unroll
+        for (int td = 0; td < TD; td++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4*>(rec + 32 * td + 8 * g + 4 * hh) =
+                    make_float4(o[td][4 * g],o[td][4 * g + 1],o[td][4 * g + 2],o[td][4 * g + 3]);
+        if (hh == 0) {
+            rec[D] = m_run;
+            rec[D + 1] = l_run;
+        }
+        return;
+    }
+
     // out[q][head*dim + d] = O^T[d][q] / l: lane holds 4 consecutive dims per
     // (tile, row group)
     if (!live) return;
@@ -349,7 +385,51 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
         }
 }
 
+// Merges the key pieces of the tail units: m = max_s m_s, w_s = exp(m_s - m),
+// out = sum_s w_s O_s / sum_s w_s l_s, pieces in order.  One thread per (tail
+// unit, query, 4 dims).
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine(AttnArgs a)
+{
+    const int per_unit = kAQ * (D / 4);
+    const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (idx >= a.tail * per_unit) return;
+    const int u = idx / per_unit, qi = (idx % per_unit) / (D / 4), d0 = 4 * (idx % (D / 4));
+    const int unit = a.full + u, head = unit / a.tiles_q, qt = unit % a.tiles_q;
+    const int q = a.qb + qt * kAQ + qi;
+    if (q >= a.qe || d0 >= a.dim) return;
+    const size_t stride = (size_t)a.tail * kAQ * (D + 4);
+    const float* rec = a.part + ((size_t)u * kAQ + qi) * (D + 4);
+    float m = -INFINITY;
+    for (int s = 0; s < a.splits; s++) m = fmaxf(m,rec[s * stride + D]);
+    float l = 0.0f, v[4] = {0.0f,0.0f,0.0f,0.0f};
+    for (int s = 0; s < a.splits; s++) {
+        const float* r = rec + s * stride;
+        const float w = __builtin_amdgcn_exp2f((r[D] - m) * kLog2e);  // an empty piece has m_s = -inf: w = 0
+        l += w * r[D + 1];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] += w * r[d0 + i];
+    }
+    float* row = a.out + (size_t)q * a.channels + (size_t)head * a.dim;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (d0 + i < a.dim) row[d0 + i] = v[i] / l;
+}
+
 // ---------------------------------------------------------------- host side
+
+static int attn_cus()
+{
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v,hipDeviceAttributeMultiprocessorCount,dev) == hipSuccess && v > 0)
+            cus = v;
+        else
+            cus = 256;
+    }
+    return cus;
+}
 
 static size_t aru(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
@@ -363,7 +443,8 @@ size_t attention_workspace_bytes(size_t rows, size_t keys, size_t heads, size_t 
     const int D = attention_dim_pad(dim);
     if (!D) return 0;
     const size_t q = heads * aru(rows,kAQ) * D, kv = kv_heads * aru(keys,kAK) * D;
-    return 2 * (q + 2 * kv) * sizeof(uint16_t);
+    // + the key-split pieces: at most one per CU
+    return 2 * (q + 2 * kv) * sizeof(uint16_t) + (size_t)attn_cus() * kAQ * (D + 4) * sizeof(float);
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, size_t rows, size_t keys, size_t heads,
@@ -381,6 +462,7 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
     uint16_t* w = static_cast<uint16_t*>(workspace);
     const size_t qn = heads * rows_pad * D, kn = kv_heads * keys_pad * D;
     uint16_t *qh = w, *ql = qh + qn, *kh = ql + qn, *kl = kh + kn, *vh = kl + kn, *vl = vh + kn;
+    float* part = reinterpret_cast<float*>(vl + kn);
     {
         const size_t nq = heads * rows_pad * (D / 8), nk = kv_heads * keys_pad * (D / 8), nv = kv_heads * (keys_pad / 16) * D;
         attn_split_rows<<<dim3((unsigned)((nq + 255) / 256)),dim3(256),0,s>>>(q,rows,channels,(int)heads,(int)dim,D,rows_pad,qh,ql);
@@ -408,11 +490,33 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
         a.key_end = (int)r.key_end;
         a.causal = r.causal? 1 : 0;
         a.tiles_q = (int)((r.query_end - r.query_begin + kAQ - 1) / kAQ);
-        const dim3 grid((unsigned)(heads * a.tiles_q));
+        // One workgroup per CU at a time: when the last round of (head, query
+        // tile) units would leave at least half of the CUs idle, its units
+        // are cut into key pieces that spread over every CU.
+        const int cus = attn_cus(), units = (int)heads * a.tiles_q;
+        const int tail = units % cus;
+        a.full = units;
+        a.tail = 1;
+        a.splits = 1;
+        a.part = part;
+        if (tail && tail * 2 <= cus) {
+            a.tail = tail;
+            a.full = units - tail;
+            a.splits = std::min(cus / tail,16);
+        }
+        const int pieces = a.splits > 1? a.tail * a.splits : 0;
+        const dim3 grid((unsigned)(a.full + pieces));
         if (D == 128) attn_kernel<128><<<grid,dim3(kAThreads),0,s>>>(a);
         else attn_kernel<64><<<grid,dim3(kAThreads),0,s>>>(a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        if (pieces) {
+            const int threads = a.tail * kAQ * (D / 4);
+            if (D == 128) attn_combine<128><<<dim3((unsigned)((threads + 255) / 256)),dim3(256),0,s>>>(a);
+            else attn_combine<64><<<dim3((unsigned)((threads + 255) / 256)),dim3(256),0,s>>>(a);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }
