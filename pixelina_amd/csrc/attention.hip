@@ -12,19 +12,20 @@
 // work, and far above what fp32 MFMAs would give.  Softmax is the online form
 // (running maximum and sum per query, output rescaled per key tile), in fp32.
 //
-// Layout: a split pass writes Q and K as bf16 planes [head][row][D] and V
-// transposed, [head][D][key], with the keys of each 16-key group permuted (bits
-// 2 and 3 swapped) so that the operand a lane needs for P*V is 16 contiguous
-// bytes (D = 64 or 128: the head size rounded up, zero-padded).
+// Layout: a split pass writes K as bf16 planes [head][key][D] and V transposed,
+// [head][D][key], with the keys of each 16-key group permuted (bits 2 and 3
+// swapped) so that the operand a lane needs for P*V is 16 contiguous bytes (D
+// = 64 or 128: the head size rounded up, zero-padded).  Q, read by one
+// workgroup per row, is split in the kernel.
 //
 // Kernel: a workgroup of 8 waves owns 256 queries of one head (32 per wave)
 // and streams 64-key tiles of K and V^T (both planes) through a 2-stage LDS
-// ring with buffer_load ... lds.  Per tile each wave computes S^T = K * Q^T
-// (keys as MFMA rows, its 32 queries as columns, so each lane owns one query:
-// the softmax statistics and the output rescale stay in the lane), then O^T +=
-// V^T * P^T, where the P^T operand is the lane's own S^T results converted to
-// bf16 -- the key order the S^T output layout gives is matched by the V^T
-// permutation above.  Q stays in registers for the whole key loop.
+// ring with buffer_load ... lds.  Per 32-key half tile each wave computes S^T
+// = K * Q^T (keys as MFMA rows, its 32 queries as columns, so each lane owns
+// one query: the softmax statistics and the output rescale stay in the lane),
+// then O^T += V^T * P^T, where the P^T operand is the lane's own S^T results
+// converted to bf16 -- the key order the S^T output layout gives is matched by
+// the V^T permutation above.  Q stays in registers for the whole key loop.
 #include <math.h>
 
 #include <algorithm>
@@ -63,7 +64,7 @@ __device__ __forceinline__ void split2(float x, uint32_t& hi, uint32_t& lo)
 // src [n][stride] fp32, head h's values at h*dim; planes [heads][npad][D] bf16
 // (hi, lo), zero beyond n and dim.  One thread per (head, row, 8 values).
 __global__ __launch_bounds__(256) void attn_split_rows(const float* __restrict__ src, size_t n, size_t stride, int heads, int dim,
-                                                        int D, size_t npad, uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
+                                                        int D, size_t npad, bool vec, uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
 {
     const size_t groups = (size_t)D / 8;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -71,15 +72,22 @@ __global__ __launch_bounds__(256) void attn_split_rows(const float* __restrict__
     const int g = (int)(idx % groups);
     const size_t row = (idx / groups) % npad;
     const int h = (int)(idx / (groups * npad));
+    float x[8];
+    const float* p = src + row * stride + (size_t)h * dim + 8 * g;
+    if (vec && row < n && 8 * g < dim) {  // 16-byte aligned rows, dim a multiple of 8
+        const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) x[i] = row < n && 8 * g + i < dim? p[i] : 0.0f;
+    }
     u32x4 vh, vl;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         uint32_t h0, l0, h1, l1;
-        const int d = 8 * g + 2 * i;
-        const float x0 = row < n && d < dim? src[row * stride + (size_t)h * dim + d] : 0.0f;
-        const float x1 = row < n && d + 1 < dim? src[row * stride + (size_t)h * dim + d + 1] : 0.0f;
-        split2(x0,h0,l0);
-        split2(x1,h1,l1);
+        split2(x[2 * i],h0,l0);
+        split2(x[2 * i + 1],h1,l1);
         vh[i] = h0 | (h1 << 16);
         vl[i] = l0 | (l1 << 16);
     }
@@ -133,9 +141,10 @@ __global__ __launch_bounds__(256) void attn_split_vt(const float* __restrict__ s
 // ---------------------------------------------------------------- main kernel
 
 struct AttnArgs {
-    const uint16_t *qh, *ql, *kh, *kl, *vh, *vl;  // split planes
-    float* out;                                    // [rows][channels]
-    int rows_pad, keys_pad;
+    const float* q;                      // [rows][channels]
+    const uint16_t *kh, *kl, *vh, *vl;  // split planes of K and V^T
+    float* out;                          // [rows][channels]
+    int rows, keys_pad;
     int heads, kv_group, dim, channels;
     int qb, qe, key_end, causal, qoff;  // this range (query rows [qb, qe))
     int tiles_q;
@@ -208,18 +217,32 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
     const int t0 = piece? split * all_tiles / a.splits : 0;
     const int t1 = piece? (split + 1) * all_tiles / a.splits : all_tiles;
 
-    // Q fragments (B operand of S^T: lane = query, 8 dims per k-step half)
+    // Q fragments (B operand of S^T: lane = query, dims 16k + 8hh .. +7), split
+    // here from fp32 (each query row is read by one workgroup only); rows
+    // past the tensor read its last row (their outputs are not stored).
     bf16x8 qfh[KS], qfl[KS];
     {
-        const size_t row = (size_t)head * a.rows_pad + min(q,a.rows_pad - 1);
-        const uint16_t* ph = a.qh + row * D + 8 * hh;
-        const uint16_t* pl = a.ql + row * D + 8 * hh;
+        const float* qrow = a.q + (size_t)min(q,a.rows - 1) * a.channels + (size_t)head * a.dim;
 #pragma unroll
-        for (int s = 0; s < KS; s++) {
-            qfh[s] = *reinterpret_cast<const bf16x8*>(ph + 16 * s);
-            qfl[s] = *reinterpret_cast<const bf16x8*>(pl + 16 * s);
+        for (int k = 0; k < KS; k++) {
+            u32x4 vh, vl;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = 16 * k + 8 * hh + 2 * i;
+                uint32_t h0, l0, h1, l1;
+                split2(d < a.dim? qrow[d] : 0.0f,h0,l0);
+                split2(d + 1 < a.dim? qrow[d + 1] : 0.0f,h1,l1);
+                vh[i] = h0 | (h1 << 16);
+                vl[i] = l0 | (l1 << 16);
+            }
+            qfh[k] = __builtin_bit_cast(bf16x8,vh);
+            qfl[k] = __builtin_bit_cast(bf16x8,vl);
         }
     }
+    // the smallest key limit of the wave: tiles below it need no masking
+    int wave_limit = limit;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) wave_limit = min(wave_limit,__shfl_xor(wave_limit,m));
 
     const size_t kplane = (size_t)a.keys_pad * D * 2;
     const ARsrc rk[2] = {__builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.kh) + (size_t)kvh * a.keys_pad * D,(short)0,(int)kplane,
@@ -256,82 +279,77 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
     v16f o[TD];
 #pragma unroll
     for (int t = 0; t < TD; t++) o[t] = v16f{};
+    // Running maximum (log2 units) and this lane's part of the sum (its 16 of
+    // each 32 keys; the two lanes of a query combine at the end).  The
+    // maximum is raised only when a half tile exceeds it by more than 8 (a
+    // factor 256), so probabilities stay below 256 and the output rescale is
+    // rare; output and sum share the maximum, so the final division is exact.
     float m_run = -INFINITY, l_run = 0.0f;
+    const float c2 = a.scale * kLog2e;
 
-    if (t0 < t1) issue(t0,t0 & 1);
-    for (int kt = t0; kt < t1; kt++) {
-        attn_wait_vmcnt<0>();
-        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
-        if (kt + 1 < t1) issue(kt + 1,(kt + 1) & 1);
-        const uint8_t* st = lds + (kt & 1) * STAGE;
-
-        // S^T = K * Q^T for the tile's two 32-key halves
-        v16f s[2];
+    // S^T = K * Q^T for the 32-key half u of the tile in `st`
+    auto score = [&](const uint8_t* st, int u, v16f& sv) {
+        sv = v16f{};
+        const int r = 32 * u + lr;
+        const uint8_t* rowh = st + r * (2 * D);
+        const uint8_t* rowl = st + PLANE + r * (2 * D);
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            s[u] = v16f{};
-            const int r = 32 * u + lr;
-            const uint8_t* rowh = st + r * (2 * D);
-            const uint8_t* rowl = st + PLANE + r * (2 * D);
-#pragma unroll
-            for (int k = 0; k < KS; k++) {
-                const int piece = (2 * k + hh) ^ swz_k<D>(r);
-                const bf16x8 ah = lds_read<bf16x8>(rowh + 16 * piece);
-                const bf16x8 al = lds_read<bf16x8>(rowl + 16 * piece);
-                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfh[k],s[u],0,0,0);
-                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfl[k],s[u],0,0,0);
-                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,qfh[k],s[u],0,0,0);
-            }
+        for (int k = 0; k < KS; k++) {
+            const int piece = (2 * k + hh) ^ swz_k<D>(r);
+            const bf16x8 ah = lds_read<bf16x8>(rowh + 16 * piece);
+            const bf16x8 al = lds_read<bf16x8>(rowl + 16 * piece);
+            sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfh[k],sv,0,0,0);
+            sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfl[k],sv,0,0,0);
+            sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,qfh[k],sv,0,0,0);
         }
-
-        // online softmax over this lane's query (the other 32 keys of each
-        // half sit in lane ^ 32)
+    };
+    // Online softmax of one half (keys key0 + 8(r/4) + 4hh + r%4) -> P^T as
+    // bf16 pairs for its two k-steps: hi = the top half of p, lo = p - hi
+    // rounded to nearest even.
+    auto softmax = [&](v16f& sv, int key0, uint32_t (&ph)[2][4], uint32_t (&pl)[2][4]) {
+        const bool edge = key0 + 32 > wave_limit;
         float mx = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = kt * kAK + 32 * u + 8 * (r >> 2) + 4 * hh + (r & 3);
-                const float x = key < limit? s[u][r] * a.scale : -INFINITY;
-                s[u][r] = x;
-                mx = fmaxf(mx,x);
-            }
+        for (int r = 0; r < 16; r++) {
+            float x = sv[r] * c2;
+            if (edge && key0 + 8 * (r >> 2) + 4 * hh + (r & 3) >= limit) x = -INFINITY;
+            sv[r] = x;
+            mx = fmaxf(mx,x);
+        }
         mx = fmaxf(mx,__shfl_xor(mx,32));
-        const float m_new = fmaxf(m_run,mx);
-        // A query can see no key of a whole key piece (causal rows in a
-        // tail piece past their limit): keep its state at zero instead of
-        // exp(-inf - -inf).
-        const float m_ref = m_new == -INFINITY? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_ref) * kLog2e);
-        float psum = 0.0f;
-        uint32_t ph[4][4], pl[4][4];  // [k-step of P*V][dword]: bf16 pairs
+        const bool need = mx > m_run + 8.0f;
+        const float m_use = need? mx : m_run;
+        if (__any(need)) {
+            const float alpha = need? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;  // exp2(-inf) = 0 at the start
 #pragma unroll
-        for (int u = 0; u < 2; u++)
+            for (int t = 0; t < TD; t++) o[t] *= alpha;
+            l_run *= alpha;
+        }
+        m_run = m_use;
+        // no key of this query seen yet (a key piece past a causal row's
+        // limit): p = exp2(-inf) = 0 rather than exp2(-inf - -inf)
+        const float m_ref = m_use == -INFINITY? 0.0f : m_use;
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                const float p0 = __builtin_amdgcn_exp2f((s[u][r] - m_ref) * kLog2e);
-                const float p1 = __builtin_amdgcn_exp2f((s[u][r + 1] - m_ref) * kLog2e);
-                psum += p0;
-                psum += p1;
-                uint32_t h0, l0, h1, l1;
-                split2(p0,h0,l0);
-                split2(p1,h1,l1);
-                const int t = 2 * u + r / 8, w = (r % 8) / 2;
-                ph[t][w] = h0 | (h1 << 16);
-                pl[t][w] = l0 | (l1 << 16);
-            }
-        psum += __shfl_xor(psum,32);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
+        for (int r = 0; r < 16; r += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(sv[r] - m_ref);
+            const float p1 = __builtin_amdgcn_exp2f(sv[r + 1] - m_ref);
+            l_run += p0;
+            l_run += p1;
+            const uint32_t u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
+            const uint32_t r0 = __float_as_uint(p0 - __uint_as_float(u0 & 0xFFFF0000u));
+            const uint32_t r1 = __float_as_uint(p1 - __uint_as_float(u1 & 0xFFFF0000u));
+            const int t = r / 8, w = (r % 8) / 2;
+            ph[t][w] = __builtin_amdgcn_perm(u1,u0,0x07060302u);
+            pl[t][w] = __builtin_amdgcn_perm(r1 + 0x7FFFu + ((r1 >> 16) & 1u),r0 + 0x7FFFu + ((r0 >> 16) & 1u),0x07060302u);
+        }
+    };
+    // O^T += V^T * P^T over the half's two 16-key k-steps
+    auto pv = [&](const uint8_t* st, int u, const uint32_t (&ph)[2][4], const uint32_t (&pl)[2][4]) {
 #pragma unroll
-        for (int t = 0; t < TD; t++) o[t] *= alpha;
-
-        // O^T += V^T * P^T
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const bf16x8 bh = __builtin_bit_cast(bf16x8,u32x4{ph[t][0],ph[t][1],ph[t][2],ph[t][3]});
-            const bf16x8 bl = __builtin_bit_cast(bf16x8,u32x4{pl[t][0],pl[t][1],pl[t][2],pl[t][3]});
+        for (int j = 0; j < 2; j++) {
+            const int t = 2 * u + j;
+            const bf16x8 bh = __builtin_bit_cast(bf16x8,u32x4{ph[j][0],ph[j][1],ph[j][2],ph[j][3]});
+            const bf16x8 bl = __builtin_bit_cast(bf16x8,u32x4{pl[j][0],pl[j][1],pl[j][2],pl[j][3]});
 #pragma unroll
             for (int td = 0; td < TD; td++) {
                 const int r = 32 * td + lr;
@@ -343,7 +361,32 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
                 o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,bh,o[td],0,0,0);
             }
         }
+    };
+
+    // Per tile: both halves' S^T MFMAs go out first, so the second half's run
+    // while the first half's softmax (vector ALU) does; then each half's P*V.
+    if (t0 < t1) issue(t0,t0 & 1);
+    for (int kt = t0; kt < t1; kt++) {
+        attn_wait_vmcnt<0>();
+        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < t1) issue(kt + 1,(kt + 1) & 1);
+        const uint8_t* st = lds + (kt & 1) * STAGE;
+        v16f s0, s1;
+        uint32_t ph[2][4], pl[2][4];
+        score(st,0,s0);
+        score(st,1,s1);
+        __builtin_amdgcn_sched_barrier(0);
+        softmax(s0,kt * kAK,ph,pl);
+        __builtin_amdgcn_sched_barrier(0);
+        pv(st,0,ph,pl);
+        __builtin_amdgcn_sched_barrier(0);
+        softmax(s1,kt * kAK + 32,ph,pl);
+        __builtin_amdgcn_sched_barrier(0);
+        pv(st,1,ph,pl);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    l_run += __shfl_xor(l_run,32);
     attn_wait_vmcnt<0>();
 
     if (piece) {
@@ -405,7 +448,7 @@ __global__ __launch_bounds__(256) void attn_combine(AttnArgs a)
     float l = 0.0f, v[4] = {0.0f,0.0f,0.0f,0.0f};
     for (int s = 0; s < a.splits; s++) {
         const float* r = rec + s * stride;
-        const float w = __builtin_amdgcn_exp2f((r[D] - m) * kLog2e);  // an empty piece has m_s = -inf: w = 0
+        const float w = __builtin_amdgcn_exp2f(r[D] - m);  // maxima in log2 units; an empty piece has -inf: w = 0
         l += w * r[D + 1];
 #pragma unroll
         for (int i = 0; i < 4; i++) v[i] += w * r[d0 + i];
@@ -442,9 +485,11 @@ size_t attention_workspace_bytes(size_t rows, size_t keys, size_t heads, size_t 
 {
     const int D = attention_dim_pad(dim);
     if (!D) return 0;
-    const size_t q = heads * aru(rows,kAQ) * D, kv = kv_heads * aru(keys,kAK) * D;
-    // + the key-split pieces: at most one per CU
-    return 2 * (q + 2 * kv) * sizeof(uint16_t) + (size_t)attn_cus() * kAQ * (D + 4) * sizeof(float);
+    (void)rows;
+    (void)heads;
+    const size_t kv = kv_heads * aru(keys,kAK) * D;
+    // K and V^T planes + the key-split pieces (at most one per CU)
+    return 4 * kv * sizeof(uint16_t) + (size_t)attn_cus() * kAQ * (D + 4) * sizeof(float);
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, size_t rows, size_t keys, size_t heads,
@@ -460,21 +505,23 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
     if (keys_pad * D * 2 >= ((size_t)1 << 31) || rows_pad + query_offset >= ((size_t)1 << 31) || keys >= ((size_t)1 << 30))
         return hipErrorInvalidValue;
     uint16_t* w = static_cast<uint16_t*>(workspace);
-    const size_t qn = heads * rows_pad * D, kn = kv_heads * keys_pad * D;
-    uint16_t *qh = w, *ql = qh + qn, *kh = ql + qn, *kl = kh + kn, *vh = kl + kn, *vl = vh + kn;
+    const size_t kn = kv_heads * keys_pad * D;
+    uint16_t *kh = w, *kl = kh + kn, *vh = kl + kn, *vl = vh + kn;
     float* part = reinterpret_cast<float*>(vl + kn);
     {
-        const size_t nq = heads * rows_pad * (D / 8), nk = kv_heads * keys_pad * (D / 8), nv = kv_heads * (keys_pad / 16) * D;
-        attn_split_rows<<<dim3((unsigned)((nq + 255) / 256)),dim3(256),0,s>>>(q,rows,channels,(int)heads,(int)dim,D,rows_pad,qh,ql);
-        attn_split_rows<<<dim3((unsigned)((nk + 255) / 256)),dim3(256),0,s>>>(k,keys,kv_channels,(int)kv_heads,(int)dim,D,keys_pad,kh,kl);
+        const size_t nk = kv_heads * keys_pad * (D / 8), nv = kv_heads * (keys_pad / 16) * D;
+        const bool vec = dim % 8 == 0 && (reinterpret_cast<uintptr_t>(k) & 15) == 0;
+        attn_split_rows<<<dim3((unsigned)((nk + 255) / 256)),dim3(256),0,s>>>(k,keys,kv_channels,(int)kv_heads,(int)dim,D,keys_pad,vec,kh,
+                                                                             kl);
         attn_split_vt<<<dim3((unsigned)((nv + 255) / 256)),dim3(256),0,s>>>(v,keys,kv_channels,(int)kv_heads,(int)dim,D,keys_pad,vh,vl);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     AttnArgs a = {};
-    a.qh = qh; a.ql = ql; a.kh = kh; a.kl = kl; a.vh = vh; a.vl = vl;
+    a.q = q;
+    a.kh = kh; a.kl = kl; a.vh = vh; a.vl = vl;
     a.out = out;
-    a.rows_pad = (int)rows_pad;
+    a.rows = (int)rows;
     a.keys_pad = (int)keys_pad;
     a.heads = (int)heads;
     a.kv_group = (int)(heads / kv_heads);
