@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
 
 
 // ---------------------------------------------------------------------------
-// K-grouped form for grids too small to fill the device (the 256-token
+// K-grouped form for grids far too small to fill the device (the 256-token
 // linear has thirty 256 x 128 tiles for 256 CUs).  A workgroup owns a 64 x 64
 // tile and splits its K range over four K-groups of four waves: group g runs
 // stages [g*Cg, (g+1)*Cg) with its own 3-slot ring, each of its waves owns a
@@ -636,11 +636,13 @@ int gemm_split_plan(size_t M, size_t N, size_t K, int& full_tiles, int& split_ch
 }
 
 // The Q8_0 GEMM runs the K-grouped 64 x 64 form when its 256 x 128 tiles
-// would fill at most half of the device.
+// would fill at most a quarter of the device (measured at N = K = 3840: 256
+// and 512 tokens faster in this form, 1024 tokens -- 120 tiles, split-K --
+// faster in the other).
 bool gemm_q8_0_grouped(size_t M, size_t N)
 {
     const size_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
-    return tiles * 2 <= (size_t)device_cus();
+    return tiles * 4 <= (size_t)device_cus();
 }
 
 size_t gemm_split_bytes(size_t M, size_t N, size_t K_stages)

@@ -251,6 +251,20 @@ bool hip_rope(float* tensor, size_t rows, size_t channels, size_t heads, const f
     return s && pixhip_rope(s,tensor,rows,channels,heads,cosine,sine,interleaved? 1 : 0) == PIXHIP_OK;
 }
 
+bool hip_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                   size_t channels, bool causal, float* output)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_attention(s,q,rows,k,v,keys,heads,kv_heads,channels,causal? 1 : 0,output) == PIXHIP_OK;
+}
+
+bool hip_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                   size_t channels, const pixhip_attention_range* ranges, size_t count, size_t query_offset, float* output)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_attention_ranges(s,q,rows,k,v,keys,heads,kv_heads,channels,ranges,count,query_offset,output) == PIXHIP_OK;
+}
+
 bool hip_available(std::string &description)
 {
     HipSession session;

@@ -144,6 +144,18 @@ bool hip_silu_gate_multiply(uint32_t type, pixhip_weight* down, const float* gat
 bool hip_pointwise(unsigned operation, float* destination, const float* second, size_t rows, size_t channels);
 bool hip_rope(float* tensor, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, bool interleaved);
 
+// vulkan_attention (src/backend_vulkan.h:143-144) for tensor_attention
+// (src/tensor.cpp:347-427): output [rows][channels] from q [rows][channels] and
+// k, v [keys][channels / heads * kv_heads], on the active session's stream.
+// The ranges form takes the reference's PixAttentionRange fields as
+// pixhip_attention_range.  False (with pixhip_last_error) on what the backend
+// does not take (head sizes above 128) or rejects, as vulkan_attention returns
+// an empty tensor.
+bool hip_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                   size_t channels, bool causal, float* output);
+bool hip_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
+                   size_t channels, const pixhip_attention_range* ranges, size_t count, size_t query_offset, float* output);
+
 bool hip_available(std::string &description);
 
 #endif /* PIXELINA_BACKEND_HIP_H */

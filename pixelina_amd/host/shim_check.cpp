@@ -18,7 +18,9 @@
 // norm(X) W2^T (hip_norm_multiply, with the weight and the modulation); the
 // normalized X [M][K]; D = (silu(G) * U) Wdown^T [M][K] (hip_silu_gate_multiply);
 // the gated product [M][F]; RoPE of X with K/64 heads of 64 (hip_rope, split
-// halves) [M][K]; Y + bias (hip_pointwise BIAS) [M][N].
+// halves) [M][K]; Y + bias (hip_pointwise BIAS) [M][N]; self-attention of X
+// with K/64 heads of 64 (hip_attention), causal [M][K], then in the ranges form
+// with rows [0, M/2) seeing every key and [M/2, M) causal [M][K].
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -121,12 +123,18 @@ int main(int argc, char** argv)
         for (size_t i = 0; i < biased.size(); i++) biased[i] = y[i];
         if (!hip_rope(roped.data(),M,K,K / 64,cosine.data(),sine.data(),false)) return fail("hip_rope");
         if (!hip_pointwise(PIXHIP_OP_BIAS,biased.data(),bias.data(),M,N)) return fail("hip_pointwise(BIAS)");
+        // tensor_attention, both forms
+        Vals<float> att(M * K), att2(M * K);
+        if (!hip_attention(x.data(),M,x.data(),x.data(),M,K / 64,K / 64,K,true,att.data())) return fail("hip_attention");
+        const pixhip_attention_range ranges[2] = {{0,M / 2,M,0},{M / 2,M,M,1}};
+        if (!hip_attention(x.data(),M,x.data(),x.data(),M,K / 64,K / 64,K,ranges,2,0,att2.data())) return fail("hip_attention(ranges)");
         if (!hip_synchronize()) return fail("hip_synchronize");
 
         FILE* out = std::fopen(argv[2],"wb");
         if (!out) return fail("cannot open output");
         const bool ok = write_floats(out,y) && write_floats(out,y1) && write_floats(out,y2) && write_floats(out,normalized) &&
-                        write_floats(out,d) && write_floats(out,gated) && write_floats(out,roped) && write_floats(out,biased);
+                        write_floats(out,d) && write_floats(out,gated) && write_floats(out,roped) && write_floats(out,biased) &&
+                        write_floats(out,att) && write_floats(out,att2);
         std::fclose(out);
         if (!ok) return fail("short write");
     }

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from gpu_helpers import TOL, row_rel_error
-from oracle_lib import Q5_K, Q8_0, bias, modulate_rows, norm_rows, oracle, quant_matmul, quantize, rope, silu_gate
+from oracle_lib import Q5_K, Q8_0, attention, bias, modulate_rows, norm_rows, oracle, quant_matmul, quantize, rope, silu_gate
 from pixelina_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -56,9 +56,18 @@ def test_shim_matmul_norm_and_gate(tmp_path):
     proc = subprocess.run([SHIM_CHECK, str(src), str(dst)], capture_output=True, text=True, timeout=120)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     out = np.fromfile(dst, np.float32)
-    sizes = [m * n, m * n, m * n, m * k, m * k, m * f, m * k, m * n]
+    sizes = [m * n, m * n, m * n, m * k, m * k, m * f, m * k, m * n, m * k, m * k]
     assert out.size == sum(sizes)
-    y, y1, y2, normalized, d, gated, roped, biased = np.split(out, np.cumsum(sizes)[:-1])
+    y, y1, y2, normalized, d, gated, roped, biased, att, att2 = np.split(out, np.cumsum(sizes)[:-1])
+
+    # hip_attention, both forms, against the oracle's tensor_attention
+    h = k // 64
+    for what, got, ranges in (("hip_attention (causal)", att, [(0, m, m, 1)]),
+                              ("hip_attention (ranges)", att2, [(0, m // 2, m, 0), (m // 2, m, m, 1)])):
+        want = attention(o, "orc", x, x, x, h, h, ranges)
+        err = row_rel_error(got.reshape(m, k), want).max()
+        print(f"{what}: rel={err:.2e}", flush=True)
+        assert err <= TOL, what
 
     # hip_rope / hip_pointwise(BIAS) were handed pageable std::vector tables:
     # bit-exact against the oracle's tensor_rope / tensor_bias
