@@ -289,6 +289,127 @@ int pixhip_attention_ranges(pixhip_session* session, const float* q, size_t rows
                             size_t heads, size_t kv_heads, size_t channels, const pixhip_attention_range* ranges, size_t count,
                             size_t query_offset, float* output);
 
+/* ---- the rest of the backend op surface (src/backend_vulkan.h:141-156) ----
+ *
+ * Tensors are row-major fp32 [rows][channels] (PixTensor, src/tensor.h:50-56).
+ * Outputs and in-place tensors are device memory or pinned host memory; other
+ * tensor operands may also be pageable host memory, staged to the device
+ * first.  4-byte aligned (16-byte alignment and channel counts that are
+ * multiples of 4 take the wider loads).  Every result is bit-identical to the
+ * reference's CPU op on the same inputs, except where a comment says
+ * otherwise. */
+
+/* More operation ids of vulkan_pointwise (src/vulkan_ops.h:31-49), for
+ * pixhip_pointwise_ex, and of vulkan_layout, for pixhip_layout. */
+#define PIXHIP_OP_MODULATE 8u   /* z_modulate, src/inference.cpp:263-277: v * (1.0f + second[part*channels + c]) */
+#define PIXHIP_OP_RESIDUAL 9u   /* z_residual, :279-291: v + second[i] * tanhf(third[part*channels + c]) (third NULL: * 1.0f) */
+#define PIXHIP_OP_AFFINE 10u    /* the VAE input and sampler steps, :474-478, :612-631: v * scale + bias */
+#define PIXHIP_OP_EULER 26u     /* qwen_image_euler, src/qwen_image.cpp:347-361: v + second[i] * scale */
+#define PIXHIP_OP_PATCH 15u     /* inference_diffuse's patchify loop, src/inference.cpp:374-390 */
+#define PIXHIP_OP_UNPATCH 16u   /* its inverse, :438-455 */
+#define PIXHIP_OP_UPSAMPLE 17u  /* tensor_upsample, src/tensor.cpp:304-319 */
+
+/* vulkan_pointwise(operation, destination, second, third, part, scale, bias)
+ * (src/backend_vulkan.cpp:1112-1127) in full: the ids of pixhip_pointwise
+ * (which this forwards to) plus MODULATE, RESIDUAL, AFFINE and EULER above,
+ * `destination` [rows][channels] updated in place.  MODULATE reads `second`
+ * values [part*channels, (part+1)*channels); RESIDUAL and EULER read `second`
+ * [rows][channels], RESIDUAL also `third` (NULL: no gate) at the same slice
+ * as MODULATE.  AFFINE takes only scale and bias.  tanhf is correctly rounded
+ * here (glibc's is within about an ulp). */
+int pixhip_pointwise_ex(pixhip_session* session, unsigned operation, float* destination, const float* second, const float* third,
+                        size_t rows, size_t channels, unsigned part, float scale, float bias);
+
+/* qwen_image_modulate (src/qwen_image.cpp:149-169; vulkan_qwen_modulate,
+ * src/backend_vulkan.cpp:1418-1430): `parameters` is two rows of
+ * `parameter_channels` (row 0 for the target rows >= target_begin, row 1 for
+ * the rows before), p = that row's values from part * channels; without
+ * `residual`, destination[r][c] *= 1 + p[c]; with it (same shape as
+ * destination), destination[r][c] += residual[r][c] * tanhf(p[c]).  Rejects
+ * (part + 1) * channels > parameter_channels, as the reference does. */
+int pixhip_qwen_modulate(pixhip_session* session, float* destination, size_t rows, size_t channels, const float* parameters,
+                         size_t parameter_channels, size_t target_begin, size_t part, const float* residual);
+
+/* tensor_l2norm (src/tensor.cpp:242-258; vulkan_l2norm, src/backend_vulkan.cpp:
+ * 1304-1316): per row, square = sum of x^2 in double, inverse =
+ * (float)(sqrt(channels) / max(sqrt(square), epsilon)), y = x * inverse *
+ * weight[c] (weight NULL: the empty weight).  epsilon must be > 0.  `output`
+ * may equal `input`.  The double sum is formed in another order than the
+ * reference's; an output differs (by an ulp) only when the two doubles fall on
+ * either side of an fp32 rounding boundary. */
+int pixhip_l2norm(pixhip_session* session, const float* input, size_t rows, size_t channels, const float* weight, float epsilon,
+                  float* output);
+
+/* tensor_groupnorm (src/tensor.cpp:454-485; vulkan_groupnorm, src/backend_vulkan.
+ * cpp:1211-1237) with the weight and bias vectors the reference decodes from
+ * the model (`name`.weight / `name`.bias): 32 groups of channels / 32
+ * consecutive channels, each over all rows; mean and variance in double,
+ * inverse = (float)(1 / sqrt(variance + 1e-6)), y = (float)(x - mean) *
+ * inverse * weight[c] + bias[c].  channels must be a multiple of 32 (the
+ * reference leaves the channels past the last whole group unwritten) and at
+ * most 8192 (PIXHIP_ERR_UNSUPPORTED).  `output` may equal `input`.  The double
+ * statistics are formed in another order than the reference's (chunked, then
+ * merged); as for pixhip_l2norm, outputs differ only at fp32 rounding
+ * boundaries. */
+int pixhip_groupnorm(pixhip_session* session, const float* input, size_t rows, size_t channels, const float* weight, const float* bias,
+                     float* output);
+
+/* vulkan_embedding (src/backend_vulkan.cpp:1239-1255; the CPU path decodes
+ * row by row, src/inference.cpp:184, src/qwen_vl.cpp:337): output [count][inner]
+ * = rows ids[i] of `table` (table_rows GGUF rows of `inner` values of `type`:
+ * F32 0, F16 1, BF16 30, Q8_0 8, Q5_K 13, Q6_K 14) decoded as cpu_decode does
+ * (src/backend_cpu.cpp:24-101).  `ids` is host memory (the reference's
+ * std::vector<int>); ids outside [0, table_rows) are rejected.  `table` is the
+ * model file's mapping (host memory: only the selected rows are moved, as the
+ * reference packs them) or device memory (gathered on the device). */
+int pixhip_embedding(pixhip_session* session, const void* table, uint32_t type, uint64_t inner, uint64_t table_rows, const int32_t* ids,
+                     size_t count, float* output);
+
+/* tensor_gather / tensor_scatter (src/tensor.cpp:274-302; vulkan_rows,
+ * src/backend_vulkan.cpp:1343-1357): gather (scatter = 0) writes destination
+ * row i = source row rows[i] (destination_rows == count); scatter writes
+ * destination row rows[i] = source row i (source_rows == count), a row listed
+ * twice keeping the last, as the reference's loop does.  `rows` is host memory
+ * (the reference's std::vector<size_t>); indices out of range and an empty
+ * list are rejected. */
+int pixhip_rows(pixhip_session* session, const float* source, size_t source_rows, float* destination, size_t destination_rows,
+                size_t channels, const size_t* rows, size_t count, int scatter);
+
+/* vulkan_copy_rows (src/backend_vulkan.cpp:1257-1269; tensor_slice,
+ * src/tensor.cpp:260-272): destination rows destination_row .. + rows, all
+ * destination_channels of them, = source rows source_row .. + rows from
+ * feature source_feature.  The two tensors' shapes are given so that the
+ * ranges are checked; they must not overlap. */
+int pixhip_copy_rows(pixhip_session* session, const float* source, size_t source_rows, size_t source_channels, float* destination,
+                     size_t destination_rows, size_t destination_channels, size_t rows, size_t source_row, size_t source_feature,
+                     size_t destination_row);
+
+/* vulkan_copy_features (src/backend_vulkan.cpp:1271-1281): one row of
+ * source_channels values into a one-row destination from destination_feature,
+ * with the reference's range checks. */
+int pixhip_copy_features(pixhip_session* session, const float* source, size_t source_channels, float* destination,
+                         size_t destination_channels, size_t destination_feature);
+
+/* vulkan_layout (src/backend_vulkan.cpp:1283-1295): PATCH turns pixels
+ * [width*height][C] into tokens [(width/patch)*(height/patch)][patch*patch*C]
+ * (token (x, y), feature (dy*patch + dx)*C + c = pixel (x*patch + dx,
+ * y*patch + dy), channel c); UNPATCH is its inverse (`width` the pixel width,
+ * destination [width*height][C]); UPSAMPLE doubles a [width*height][C] image
+ * by repeating each pixel 2x2 (`patch` unused).  The shapes must agree
+ * (PIXHIP_ERR_ARGUMENT otherwise). */
+int pixhip_layout(pixhip_session* session, unsigned operation, const float* source, size_t source_rows, size_t source_channels,
+                  float* destination, size_t destination_rows, size_t destination_channels, size_t width, size_t patch);
+
+/* tensor_resample_shortcut (src/tensor.cpp:487-527; vulkan_shortcut,
+ * src/backend_vulkan.cpp:1404-1416): the Qwen VAE's parameter-free resampling
+ * shortcut of a [width*height][source_channels] image into `destination`
+ * [out_width*out_height][channels] (out = width*2 up, width/2 down when
+ * spatial, else unchanged): up repeats channels from the last time step; down
+ * averages the last time step's items of each group (fp32 sum in order, then
+ * / group).  The reference's shape checks apply. */
+int pixhip_shortcut(pixhip_session* session, const float* source, size_t width, size_t height, size_t source_channels,
+                    float* destination, size_t channels, size_t temporal, int up, int spatial);
+
 /* ---- integer parity gate ---- */
 
 /* Runs the GEMM kernel's integer path and writes, for every (column c, row r,

@@ -36,6 +36,22 @@
  *  12 tanh GELU with v*v instead of v*v*v
  *  13 modulation as x + x*scale instead of x*(1 + scale)
  *  14 modulation by scale instead of 1 + scale
+ *  15 attention's grouped heads as head % kv_heads
+ *  16 causal attention without the query's own key
+ *  17 l2norm without the sqrt(channels) factor
+ *  18 l2norm adding epsilon instead of taking the larger
+ *  19 groupnorm variance over n - 1
+ *  20 groupnorm weight and bias indexed by group
+ *  21 BF16 decoded as F16
+ *  22 F16 decode keeping the NaN payload
+ *  23 scatter keeping the first of a repeated row
+ *  24 patch layout with dx and dy swapped
+ *  25 upsample reading rows of the doubled width
+ *  26 shortcut (down) without the division by the group
+ *  27 shortcut (up) from the first time step
+ *  28 qwen modulation with the two parameter rows swapped
+ *  29 residual gate without tanh
+ *  30 affine adding the bias before the scale
  */
 #ifndef ORC_MUTANT
 #define ORC_MUTANT 0
@@ -681,5 +697,277 @@ int orc_attention(const float* q, size_t rows, const float* k, const float* v, s
         }
     }
     free(scores);
+    return 1;
+}
+
+/* ---- the rest of the backend op surface ---- */
+
+/* Channel ops in place on x [rows][channels] (op ids of src/vulkan_ops.h:31-49):
+ *   8  z_modulate, src/inference.cpp:263-277: x * (1.0f + p[c])
+ *   9  z_residual, :279-291: x + other[i] * (p? tanhf(p[c]) : 1.0f)
+ *  10  the VAE input step as vulkan_pointwise runs it (:474-476): x * scale + bias
+ *  26  qwen_image_euler, src/qwen_image.cpp:347-361: x + delta * other[i]
+ * `p` is the modulation already offset to its part (part * channels). */
+void orc_channel_op(int op, float* x, const float* other, const float* p, size_t rows, size_t channels, float scale, float bias)
+{
+    for (size_t i = 0; i < rows * channels; i++) {
+        const size_t c = i % channels;
+        if (op == 8) {
+            x[i] = x[i] * (1.0f + p[c]);
+        } else if (op == 9) {
+#if ORC_MUTANT == 29
+            x[i] += other[i] * (p? p[c] : 1.0f);
+#else
+            x[i] += other[i] * (p? tanhf(p[c]) : 1.0f);
+#endif
+        } else if (op == 10) {
+#if ORC_MUTANT == 30
+            x[i] = (x[i] + bias) * scale;
+#else
+            x[i] = x[i] * scale + bias;
+#endif
+        } else {
+            x[i] += scale * other[i];
+        }
+    }
+}
+
+/* qwen_image_modulate, src/qwen_image.cpp:149-169: parameters [2][parameter_channels];
+ * row r uses parameter row (r >= target_begin? 0 : 1) from part * channels;
+ * x *= 1 + p, or with a residual x += residual * tanhf(p).  Returns 0 on the
+ * reference's rejection (:152). */
+int orc_qwen_modulate(float* x, size_t rows, size_t channels, const float* parameters, size_t parameter_channels, size_t target_begin,
+                      size_t part, const float* residual)
+{
+    if (!rows || !channels || (part + 1) * channels > parameter_channels) return 0;
+    for (size_t row = 0; row < rows; row++) {
+#if ORC_MUTANT == 28
+        const size_t parameter = (row >= target_begin? 1 : 0) * parameter_channels + part * channels;
+#else
+        const size_t parameter = (row >= target_begin? 0 : 1) * parameter_channels + part * channels;
+#endif
+        for (size_t c = 0; c < channels; c++) {
+            const size_t index = row * channels + c;
+            if (residual) x[index] += residual[index] * tanhf(parameters[parameter + c]);
+            else x[index] *= 1 + parameters[parameter + c];
+        }
+    }
+    return 1;
+}
+
+/* tensor_l2norm, src/tensor.cpp:242-258: square = running double sum of
+ * double(x) * x; inverse = (float)(sqrt(double(channels)) / max(sqrt(square),
+ * double(epsilon))); y = x * inverse * w[c] in fp32 (w NULL: * 1).  Returns 0
+ * on the reference's rejection (epsilon <= 0). */
+int orc_l2norm(const float* x, size_t rows, size_t channels, const float* weight, float epsilon, float* out)
+{
+    if (!rows || !channels || !(epsilon > 0)) return 0;
+    for (size_t row = 0; row < rows; row++) {
+        const float* from = x + row * channels;
+        double square = 0;
+        for (size_t c = 0; c < channels; c++) square += (double)from[c] * from[c];
+        const double root = sqrt(square);
+#if ORC_MUTANT == 17
+        const float inverse = (float)(1.0 / (root < (double)epsilon? (double)epsilon : root));
+#elif ORC_MUTANT == 18
+        const float inverse = (float)(sqrt((double)channels) / (root + (double)epsilon));
+#else
+        const float inverse = (float)(sqrt((double)channels) / (root < (double)epsilon? (double)epsilon : root));
+#endif
+        for (size_t c = 0; c < channels; c++) out[row * channels + c] = from[c] * inverse * (weight? weight[c] : 1.0f);
+    }
+    return 1;
+}
+
+/* tensor_groupnorm, src/tensor.cpp:454-485 (COMPUTE_VAE_GROUPS 32,
+ * COMPUTE_NORM_EPSILON 1e-6f, src/tensor.h:32-34): group g = channels
+ * [g*gs, (g+1)*gs), gs = channels / 32, over all rows; running double sums in
+ * row-then-channel order: mean = sum / n, square = sum of (x - mean)^2,
+ * inverse = (float)(1 / sqrt(square / n + 1e-6)); y = (float)(x - mean) *
+ * inverse * w[c] + b[c] in fp32. */
+void orc_groupnorm(const float* x, size_t rows, size_t channels, const float* weight, const float* bias, float* out)
+{
+    const size_t gs = channels / 32, count = rows * gs;
+    for (size_t g = 0; g < 32; g++) {
+        double sum = 0, square = 0;
+        for (size_t r = 0; r < rows; r++)
+            for (size_t c = g * gs; c < (g + 1) * gs; c++) sum += x[r * channels + c];
+        const double mean = sum / count;
+        for (size_t r = 0; r < rows; r++)
+            for (size_t c = g * gs; c < (g + 1) * gs; c++) {
+                const double delta = x[r * channels + c] - mean;
+                square += delta * delta;
+            }
+#if ORC_MUTANT == 19
+        const float inverse = (float)(1.0 / sqrt(square / (double)(count - 1) + 1e-6f));
+#else
+        const float inverse = (float)(1.0 / sqrt(square / count + 1e-6f));
+#endif
+        for (size_t r = 0; r < rows; r++)
+            for (size_t c = g * gs; c < (g + 1) * gs; c++) {
+#if ORC_MUTANT == 20
+                out[r * channels + c] = (float)(x[r * channels + c] - mean) * inverse * weight[g] + bias[g];
+#else
+                out[r * channels + c] = (float)(x[r * channels + c] - mean) * inverse * weight[c] + bias[c];
+#endif
+            }
+    }
+}
+
+/* half_float, src/backend_cpu.cpp:12-22: exact, NaN without its payload. */
+static float half_float_ref(uint16_t h)
+{
+#if ORC_MUTANT == 22
+    if ((h & 0x7c00) == 0x7c00 && (h & 0x3ff)) {
+        uint32_t bits = ((uint32_t)(h & 0x8000) << 16) | 0x7f800000u | ((uint32_t)(h & 0x3ff) << 13) | 0x00400000u;
+        float f;
+        memcpy(&f,&bits,4);
+        return f;
+    }
+#endif
+    if ((h & 0x7c00) == 0x7c00 && (h & 0x3ff)) return (h & 0x8000)? -NAN : NAN;
+    return orc_half_to_float(h);
+}
+
+/* cpu_decode, src/backend_cpu.cpp:24-101: `count` values of `type` (F32 0,
+ * F16 1, BF16 30, Q8_0, Q5_K, Q6_K) to fp32 in its order of operations:
+ * Q8_0 (float)q * d; Q5_K d * scale * q - dmin * min; Q6_K d * scale * (q - 32). */
+void orc_decode_f32(const void* data, uint32_t type, size_t count, float* out)
+{
+    const uint8_t* p = (const uint8_t*)data;
+    if (type == 0) {
+        memcpy(out,p,count * 4);
+        return;
+    }
+    if (type == 1 || type == 30) {
+        for (size_t i = 0; i < count; i++) {
+            const uint16_t raw = rd16(p + 2 * i);
+#if ORC_MUTANT == 21
+            if (1) {
+#else
+            if (type == 1) {
+#endif
+                out[i] = half_float_ref(raw);
+            } else {
+                const uint32_t bits = (uint32_t)raw << 16;
+                memcpy(out + i,&bits,4);
+            }
+        }
+        return;
+    }
+    const size_t block = type == ORC_Q8_0? QK8_0 : QK_K;
+    for (size_t base = 0; base < count; base += block) {
+        float* o = out + base;
+        if (type == ORC_Q8_0) {
+            const float d = half_float_ref(rd16(p));
+            for (int i = 0; i < QK8_0; i++) o[i] = (int8_t)p[2 + i] * d;
+            p += Q8_0_BYTES;
+        } else if (type == ORC_Q5_K) {
+            const float d = half_float_ref(rd16(p)), dmin = half_float_ref(rd16(p + 2));
+            int scale[8], min[8];
+            q5_scales(p + 4,scale,min);
+            for (int s = 0; s < 8; s++)
+                for (int i = 0; i < 32; i++) o[32 * s + i] = d * (float)scale[s] * (float)q5_value(p,s,i) - dmin * (float)min[s];
+            p += Q5_K_BYTES;
+        } else {
+            const float d = half_float_ref(rd16(p + 208));
+            const int8_t* sc = (const int8_t*)(p + 192);
+            for (int e = 0; e < QK_K; e++) {
+                o[e] = d * (float)sc[e / 16] * (float)(q6_value(p,e) - 32);
+            }
+            p += Q6_K_BYTES;
+        }
+    }
+}
+
+/* tensor_gather (scatter 0) and tensor_scatter, src/tensor.cpp:274-302: row
+ * copies in list order (a scattered row listed twice keeps the last).  The
+ * reference's checks: every index within its tensor; returns 0 otherwise. */
+int orc_rows(const float* source, size_t source_rows, float* destination, size_t destination_rows, size_t channels,
+             const uint64_t* rows, size_t count, int scatter)
+{
+    for (size_t i = 0; i < count; i++)
+        if (rows[i] >= (scatter? destination_rows : source_rows)) return 0;
+    if (scatter) {
+#if ORC_MUTANT == 23
+        for (size_t i = count; i-- > 0;) memcpy(destination + rows[i] * channels,source + i * channels,channels * 4);
+#else
+        for (size_t i = 0; i < count; i++) memcpy(destination + rows[i] * channels,source + i * channels,channels * 4);
+#endif
+    } else {
+        for (size_t i = 0; i < count; i++) memcpy(destination + i * channels,source + rows[i] * channels,channels * 4);
+    }
+    return 1;
+}
+
+/* The DiT patch / unpatch loops (src/inference.cpp:374-390, :438-455) and
+ * tensor_upsample (src/tensor.cpp:304-319).  op 15: pixels [width*height][C]
+ * -> tokens [(width/p)(height/p)][p*p*C]; 16: the inverse (width, height the
+ * pixel image's); 17: [width*height][C] -> [2width*2height][C]. */
+void orc_layout(int op, const float* source, float* destination, size_t width, size_t height, size_t channels, size_t patch)
+{
+    if (op == 17) {
+        for (size_t y = 0; y < height * 2; y++)
+            for (size_t x = 0; x < width * 2; x++) {
+#if ORC_MUTANT == 25
+                const size_t from = ((y / 2) * width * 2 + x / 2) % (width * height);
+#else
+                const size_t from = (y / 2) * width + x / 2;
+#endif
+                memcpy(destination + (y * width * 2 + x) * channels,source + from * channels,channels * 4);
+            }
+        return;
+    }
+    const size_t pw = width / patch, ph = height / patch;
+    for (size_t y = 0; y < ph; y++)
+        for (size_t x = 0; x < pw; x++)
+            for (size_t dy = 0; dy < patch; dy++)
+                for (size_t dx = 0; dx < patch; dx++) {
+                    const size_t pixel = (y * patch + dy) * width + x * patch + dx;
+#if ORC_MUTANT == 24
+                    const size_t token = (y * pw + x) * patch * patch + dx * patch + dy;
+#else
+                    const size_t token = (y * pw + x) * patch * patch + dy * patch + dx;
+#endif
+                    if (op == 15) memcpy(destination + token * channels,source + pixel * channels,channels * 4);
+                    else memcpy(destination + pixel * channels,source + token * channels,channels * 4);
+                }
+}
+
+/* tensor_resample_shortcut, src/tensor.cpp:487-527, with its checks (returns
+ * 0 where the reference returns an empty tensor).  `out` [out_width *
+ * out_height][channels]. */
+int orc_shortcut(const float* input, size_t width, size_t height, size_t input_channels, size_t channels, size_t temporal, int up,
+                 int spatial, float* out)
+{
+    if (!width || !height || !channels || !temporal || !input_channels) return 0;
+    const size_t side = spatial? 2 : 1, factor = temporal * side * side;
+    if ((up && channels * factor % input_channels) || (!up && input_channels * factor % channels)) return 0;
+    if (!up && (width % side || height % side)) return 0;
+    const size_t ow = up? width * side : width / side, oh = up? height * side : height / side;
+    const size_t group = up? channels * factor / input_channels : input_channels * factor / channels;
+    for (size_t y = 0; y < oh; y++)
+        for (size_t x = 0; x < ow; x++)
+            for (size_t c = 0; c < channels; c++) {
+                float value = 0;
+                if (up) {
+#if ORC_MUTANT == 27
+                    const size_t sc = (c * factor + (y % side) * side + x % side) / group;
+#else
+                    const size_t sc = (c * factor + (temporal - 1) * side * side + (y % side) * side + x % side) / group;
+#endif
+                    value = input[((y / side) * width + x / side) * input_channels + sc];
+                } else {
+                    for (size_t i = 0; i < group; i++) {
+                        const size_t item = c * group + i, sc = item / factor;
+                        const size_t time = item / (side * side) % temporal, dy = item / side % side, dx = item % side;
+                        if (time == temporal - 1) value += input[((y * side + dy) * width + x * side + dx) * input_channels + sc];
+                    }
+#if ORC_MUTANT != 26
+                    value /= group;
+#endif
+                }
+                out[(y * ow + x) * channels + c] = value;
+            }
     return 1;
 }

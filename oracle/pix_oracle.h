@@ -10,6 +10,9 @@
  * tests/test_oracle.py against golden vectors written by the compiled
  * reference (tests/golden/) plus closed-form / brute-force checks.
  *
+ * Besides the linear path it restates the reference's other backend ops
+ * (norms, row moves, layouts, decode, modulation), each at its file:line.
+ *
  * Block layouts are the reference's (src/kernels_quant.cpp:14-38,
  * src/model_types.h:10-21):
  *   Q8_0   34 B : fp16 d, int8 qs[32]
@@ -55,6 +58,18 @@ void orc_add(float* x, const float* y, size_t count);
 void orc_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, int interleaved);
 int orc_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
                   size_t channels, const uint64_t* ranges, size_t nranges, size_t query_offset, float* out);
+
+void orc_channel_op(int op, float* x, const float* other, const float* p, size_t rows, size_t channels, float scale, float bias);
+int orc_qwen_modulate(float* x, size_t rows, size_t channels, const float* parameters, size_t parameter_channels, size_t target_begin,
+                      size_t part, const float* residual);
+int orc_l2norm(const float* x, size_t rows, size_t channels, const float* weight, float epsilon, float* out);
+void orc_groupnorm(const float* x, size_t rows, size_t channels, const float* weight, const float* bias, float* out);
+void orc_decode_f32(const void* data, uint32_t type, size_t count, float* out);
+int orc_rows(const float* source, size_t source_rows, float* destination, size_t destination_rows, size_t channels,
+             const uint64_t* rows, size_t count, int scatter);
+void orc_layout(int op, const float* source, float* destination, size_t width, size_t height, size_t channels, size_t patch);
+int orc_shortcut(const float* input, size_t width, size_t height, size_t input_channels, size_t channels, size_t temporal, int up,
+                 int spatial, float* out);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,11 @@
  * leg (cpu_baseline.kind = "reference").
  */
 #include "kernels_quant.cpp"
+#include "model.h"
+#include "tensor.h"
+#include "tensor_names.h"
+
+#include <cstring>
 
 extern "C" {
 
@@ -185,6 +190,100 @@ void ref_rope(float* x, size_t rows, size_t channels, size_t heads, const float*
     const size_t half = rows * (channels / heads) / 2;
     tensor_rope(t,heads,std::vector<float>(cosine,cosine + half),std::vector<float>(sine,sine + half),interleaved != 0);
     std::copy(t.values.begin(),t.values.end(),x);
+}
+
+/* tensor_l2norm, src/tensor.cpp:242-258 (weight NULL: the empty vector).
+ * Returns 1 when the reference produced output. */
+int ref_l2norm(const float* x, size_t rows, size_t channels, const float* weight, float epsilon, float* out)
+{
+    PixTensor in(rows,channels);
+    std::copy(x,x + rows * channels,in.values.begin());
+    std::vector<float> w;
+    if (weight) w.assign(weight,weight + channels);
+    PixTensor o = tensor_l2norm(in,w,epsilon);
+    if (o.values.size() != rows * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
+/* tensor_groupnorm, src/tensor.cpp:454-485, which reads `name`.weight and
+ * `name`.bias from a model file: here a PixModelFile whose mapping is a
+ * buffer holding the two F32 vectors (detached again before it is destroyed,
+ * so that close() unmaps nothing). */
+int ref_groupnorm(const float* x, size_t rows, size_t channels, const float* weight, const float* bias, float* out)
+{
+    std::vector<float> blob(weight,weight + channels);
+    blob.insert(blob.end(),bias,bias + channels);
+    PixModelFile model;
+    model.data = reinterpret_cast<const unsigned char*>(blob.data());
+    model.size = blob.size() * sizeof(float);
+    model.weights["g" WEIGHT_SUFFIX] = PixWeight{"g" WEIGHT_SUFFIX,{uint64_t(channels)},MODEL_F32,0,uint64_t(channels) * 4};
+    model.weights["g" BIAS_SUFFIX] = PixWeight{"g" BIAS_SUFFIX,{uint64_t(channels)},MODEL_F32,uint64_t(channels) * 4,uint64_t(channels) * 4};
+    PixTensor in(rows,channels);
+    std::copy(x,x + rows * channels,in.values.begin());
+    PixTensor o = tensor_groupnorm(model,"g",in);
+    model.data = nullptr;
+    model.size = 0;
+    if (o.values.size() != rows * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
+/* tensor_slice, src/tensor.cpp:260-272: out [rows][channels] */
+int ref_slice(const float* x, size_t in_rows, size_t in_channels, size_t row, size_t rows, size_t feature, size_t channels, float* out)
+{
+    PixTensor in(in_rows,in_channels);
+    std::copy(x,x + in_rows * in_channels,in.values.begin());
+    PixTensor o = tensor_slice(in,row,rows,feature,channels);
+    if (o.values.size() != rows * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
+/* tensor_gather, src/tensor.cpp:274-289: out [count][channels] */
+int ref_gather(const float* x, size_t in_rows, size_t channels, const uint64_t* rows, size_t count, float* out)
+{
+    PixTensor in(in_rows,channels);
+    std::copy(x,x + in_rows * channels,in.values.begin());
+    PixTensor o = tensor_gather(in,std::vector<size_t>(rows,rows + count));
+    if (o.values.size() != count * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
+/* tensor_scatter, src/tensor.cpp:291-302: destination [dst_rows][channels] in place */
+int ref_scatter(float* destination, size_t dst_rows, size_t channels, const float* source, const uint64_t* rows, size_t count)
+{
+    PixTensor d(dst_rows,channels),src(count,channels);
+    std::copy(destination,destination + dst_rows * channels,d.values.begin());
+    std::copy(source,source + count * channels,src.values.begin());
+    if (!tensor_scatter(d,src,std::vector<size_t>(rows,rows + count))) return 0;
+    std::copy(d.values.begin(),d.values.end(),destination);
+    return 1;
+}
+
+/* tensor_upsample, src/tensor.cpp:304-319: out [4*width*height][channels] */
+int ref_upsample(const float* x, size_t width, size_t height, size_t channels, float* out)
+{
+    PixTensor in(width * height,channels);
+    std::copy(x,x + width * height * channels,in.values.begin());
+    PixTensor o = tensor_upsample(in,width,height);
+    if (o.values.size() != 4 * width * height * channels) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return 1;
+}
+
+/* tensor_resample_shortcut, src/tensor.cpp:487-527: out [out_pixels][channels];
+ * returns the number of output values (0: the reference rejected the shape). */
+size_t ref_shortcut(const float* x, size_t width, size_t height, size_t in_channels, size_t channels, size_t temporal, int up, int spatial,
+                    float* out, size_t capacity)
+{
+    PixTensor in(width * height,in_channels);
+    std::copy(x,x + width * height * in_channels,in.values.begin());
+    PixTensor o = tensor_resample_shortcut(in,width,height,channels,temporal,up != 0,spatial != 0);
+    if (o.values.empty() || o.values.size() > capacity) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return o.values.size();
 }
 
 }

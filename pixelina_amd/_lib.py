@@ -63,6 +63,16 @@ SIGNATURES = {
     "pixhip_rope": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
     "pixhip_attention": (_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _int, _vp]),
     "pixhip_attention_ranges": (_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _vp]),
+    "pixhip_pointwise_ex": (_int, [_vp, ctypes.c_uint, _vp, _vp, _vp, _sz, _sz, ctypes.c_uint, ctypes.c_float, ctypes.c_float]),
+    "pixhip_qwen_modulate": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _sz, _sz, _vp]),
+    "pixhip_l2norm": (_int, [_vp, _vp, _sz, _sz, _vp, ctypes.c_float, _vp]),
+    "pixhip_groupnorm": (_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp]),
+    "pixhip_embedding": (_int, [_vp, _vp, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, _vp, _sz, _vp]),
+    "pixhip_rows": (_int, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _sz, _int]),
+    "pixhip_copy_rows": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _sz, _sz, _sz, _sz, _sz]),
+    "pixhip_copy_features": (_int, [_vp, _vp, _sz, _vp, _sz, _sz]),
+    "pixhip_layout": (_int, [_vp, ctypes.c_uint, _vp, _sz, _sz, _vp, _sz, _sz, _sz, _sz]),
+    "pixhip_shortcut": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _sz, _sz, _int, _int]),
     "pixhip_block_sums": (_int, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "pixhip_timer_start": (_int, [_vp]),
     "pixhip_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),

@@ -23,6 +23,7 @@ SOURCES = [
     "csrc/fuse.hip",
     "csrc/ops.hip",
     "csrc/attention.hip",
+    "csrc/tensor_ops.hip",
     "csrc/api.cpp",
     "host/backend_hip.cpp",
 ]

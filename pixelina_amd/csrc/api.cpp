@@ -145,6 +145,9 @@ struct pixhip_session {
     // attention's bf16 split planes
     void* attn = nullptr;
     size_t attn_bytes = 0;
+    // groupnorm's chunk statistics
+    void* gn = nullptr;
+    size_t gn_bytes = 0;
     // activations left by the last QUANTIZE stage
     int act_kind = 0;  // 0 none, 1 Q8_K, 2 Q8_0
     size_t act_columns = 0, act_inner = 0;
@@ -687,6 +690,7 @@ void pixhip_session_destroy(pixhip_session* s)
     if (s->partial) (void)hipFree(s->partial);
     if (s->stage) (void)hipFree(s->stage);
     if (s->attn) (void)hipFree(s->attn);
+    if (s->gn) (void)hipFree(s->gn);
     if (s->t0) (void)hipEventDestroy(s->t0);
     if (s->t1) (void)hipEventDestroy(s->t1);
     if (s->own_stream) (void)hipStreamDestroy(s->own_stream);
@@ -1286,6 +1290,376 @@ int pixhip_bench_matmul(pixhip_session* s, const pixhip_weight* const* weights, 
     float v = 0;
     PIX_HIP(hipEventElapsedTime(&v,s->t0,s->t1),"hipEventElapsedTime");
     if (ms) *ms = v;
+    return PIXHIP_OK;
+}
+
+}  // extern "C"
+
+/* ---- the rest of the backend op surface ---- */
+
+namespace {
+
+// Operands staged by read_operand, released together after the launch (the
+// pool reuses a block only for work queued after it).
+struct Staged {
+    pixhip_session* s;
+    std::vector<void*> blocks;
+    explicit Staged(pixhip_session* session) : s(session) {}
+    ~Staged()
+    {
+        for (void* b : blocks) pixhip_free(s,b);
+    }
+    int read(const void* p, size_t bytes, const void** dev)
+    {
+        void* staged = nullptr;
+        const int rc = read_operand(s,p,bytes,dev,&staged);
+        if (staged) blocks.push_back(staged);
+        return rc;
+    }
+};
+
+bool aligned4(const void* p)
+{
+    return reinterpret_cast<uintptr_t>(p) % 4 == 0;
+}
+
+// a * b * 4 bytes without overflow
+bool float_bytes(size_t a, size_t b, size_t* bytes)
+{
+    if (b && a > SIZE_MAX / b / sizeof(float)) return false;
+    *bytes = a * b * sizeof(float);
+    return true;
+}
+
+// Bytes of one GGUF row of `inner` values (weight_bytes, src/model.cpp:87-121);
+// 0 for a type cpu_decode does not know or a ragged block.
+size_t gguf_row_bytes(uint32_t type, uint64_t inner)
+{
+    switch (type) {
+    case PIX_F32: return inner * 4;
+    case PIX_F16:
+    case PIX_BF16: return inner * 2;
+    case PIX_Q8_0: return inner % PIX_QK8? 0 : inner / PIX_QK8 * PIX_Q8_0_BYTES;
+    case PIX_Q5_K: return inner % PIX_QK? 0 : inner / PIX_QK * PIX_Q5_K_BYTES;
+    case PIX_Q6_K: return inner % PIX_QK? 0 : inner / PIX_QK * PIX_Q6_K_BYTES;
+    default: return 0;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int pixhip_pointwise_ex(pixhip_session* s, unsigned operation, float* destination, const float* second, const float* third, size_t rows,
+                        size_t channels, unsigned part, float scale, float bias)
+{
+    if (operation != PIXHIP_OP_MODULATE && operation != PIXHIP_OP_RESIDUAL && operation != PIXHIP_OP_AFFINE &&
+        operation != PIXHIP_OP_EULER)
+        return pixhip_pointwise(s,operation,destination,second,rows,channels);
+    int rc = use_device(s);
+    if (rc) return rc;
+    size_t bytes = 0;
+    const bool needs_second = operation != PIXHIP_OP_AFFINE;
+    if (!rows || !channels || !destination || (needs_second && !second) || !float_bytes(rows,channels,&bytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    if (!aligned4(destination) || !aligned4(second) || !aligned4(third)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    if ((size_t)part > SIZE_MAX / channels - 1) return fail(PIXHIP_ERR_ARGUMENT,"part out of range");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    Staged st(s);
+    const void *other = nullptr, *param = nullptr;
+    const size_t slice = (size_t)part * channels;
+    if (operation == PIXHIP_OP_MODULATE) {
+        if ((rc = st.read(second + slice,channels * sizeof(float),&param))) return rc;
+    } else if (operation == PIXHIP_OP_RESIDUAL || operation == PIXHIP_OP_EULER) {
+        if ((rc = st.read(second,bytes,&other))) return rc;
+        if (operation == PIXHIP_OP_RESIDUAL && third && (rc = st.read(third + slice,channels * sizeof(float),&param))) return rc;
+    }
+    const int op = operation == PIXHIP_OP_MODULATE? pixhip::kOpModulate
+                 : operation == PIXHIP_OP_RESIDUAL? pixhip::kOpResidual
+                 : operation == PIXHIP_OP_AFFINE? pixhip::kOpAffine
+                                                 : pixhip::kOpEuler;
+    hipError_t e = pixhip::launch_channel_op(op,static_cast<float*>(dst),static_cast<const float*>(other),static_cast<const float*>(param),
+                                             nullptr,rows,channels,0,scale,bias,s->stream);
+    if (e == hipErrorInvalidValue) return fail(PIXHIP_ERR_ARGUMENT,"too many rows for one launch");
+    PIX_HIP(e,"pointwise");
+    return PIXHIP_OK;
+}
+
+int pixhip_qwen_modulate(pixhip_session* s, float* destination, size_t rows, size_t channels, const float* parameters,
+                         size_t parameter_channels, size_t target_begin, size_t part, const float* residual)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    size_t bytes = 0, pbytes = 0;
+    if (!destination || !parameters || !rows || !channels || !float_bytes(rows,channels,&bytes) || !float_bytes(2,parameter_channels,&pbytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    // the reference's check (src/qwen_image.cpp:152)
+    if (part >= SIZE_MAX / channels || (part + 1) * channels > parameter_channels)
+        return fail(PIXHIP_ERR_ARGUMENT,"parameters hold fewer than (part + 1) * channels values per row");
+    if (!aligned4(destination) || !aligned4(parameters) || !aligned4(residual)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    Staged st(s);
+    const void *param = nullptr, *other = nullptr;
+    if ((rc = st.read(parameters,pbytes,&param))) return rc;
+    if (residual && (rc = st.read(residual,bytes,&other))) return rc;
+    const float* p0 = static_cast<const float*>(param) + part * channels;
+    hipError_t e = pixhip::launch_channel_op(residual? pixhip::kOpQwenResidual : pixhip::kOpQwenScale,static_cast<float*>(dst),
+                                             static_cast<const float*>(other),p0,p0 + parameter_channels,rows,channels,target_begin,0.0f,
+                                             0.0f,s->stream);
+    if (e == hipErrorInvalidValue) return fail(PIXHIP_ERR_ARGUMENT,"too many rows for one launch");
+    PIX_HIP(e,"qwen modulate");
+    return PIXHIP_OK;
+}
+
+int pixhip_l2norm(pixhip_session* s, const float* input, size_t rows, size_t channels, const float* weight, float epsilon, float* output)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    size_t bytes = 0;
+    // the reference's checks (src/tensor.cpp:244)
+    if (!input || !output || !rows || !channels || !float_bytes(rows,channels,&bytes) || !(epsilon > 0.0f))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer, empty tensor or epsilon <= 0");
+    if (!aligned4(input) || !aligned4(output) || !aligned4(weight)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    void* out = nullptr;
+    if ((rc = write_operand(s,output,&out))) return rc;
+    Staged st(s);
+    const void *in = nullptr, *w = nullptr;
+    if ((rc = st.read(input,bytes,&in))) return rc;
+    if (weight && (rc = st.read(weight,channels * sizeof(float),&w))) return rc;
+    hipError_t e = pixhip::launch_l2norm(static_cast<const float*>(in),static_cast<const float*>(w),static_cast<float*>(out),rows,channels,
+                                         epsilon,s->stream);
+    if (e == hipErrorInvalidValue) return fail(PIXHIP_ERR_ARGUMENT,"too many rows for one launch");
+    PIX_HIP(e,"l2norm");
+    return PIXHIP_OK;
+}
+
+int pixhip_groupnorm(pixhip_session* s, const float* input, size_t rows, size_t channels, const float* weight, const float* bias,
+                     float* output)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    size_t bytes = 0;
+    if (!input || !output || !weight || !bias || !rows || !channels || !float_bytes(rows,channels,&bytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    if (channels % 32) return fail(PIXHIP_ERR_ARGUMENT,"channels must be a multiple of the 32 groups");
+    const size_t work = pixhip::groupnorm_workspace_bytes(rows,channels);
+    if (!work) return fail(PIXHIP_ERR_UNSUPPORTED,"groupnorm supports groups of up to 256 channels");
+    if (!aligned4(input) || !aligned4(output) || !aligned4(weight) || !aligned4(bias))
+        return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    void* out = nullptr;
+    if ((rc = write_operand(s,output,&out))) return rc;
+    Staged st(s);
+    const void *in = nullptr, *w = nullptr, *b = nullptr;
+    if ((rc = st.read(input,bytes,&in)) || (rc = st.read(weight,channels * sizeof(float),&w)) ||
+        (rc = st.read(bias,channels * sizeof(float),&b)))
+        return rc;
+    if ((rc = grow(s,&s->gn,&s->gn_bytes,work))) return rc;
+    hipError_t e = pixhip::launch_groupnorm(static_cast<const float*>(in),static_cast<const float*>(w),static_cast<const float*>(b),
+                                            static_cast<float*>(out),rows,channels,1e-6f,s->gn,s->stream);
+    if (e == hipErrorInvalidValue) return fail(PIXHIP_ERR_ARGUMENT,"too many rows for one launch");
+    PIX_HIP(e,"groupnorm");
+    return PIXHIP_OK;
+}
+
+int pixhip_embedding(pixhip_session* s, const void* table, uint32_t type, uint64_t inner, uint64_t table_rows, const int32_t* ids,
+                     size_t count, float* output)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!table || !ids || !output || !count || !inner || !table_rows) return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    const size_t stride = gguf_row_bytes(type,inner);
+    if (type != PIX_F32 && type != PIX_F16 && type != PIX_BF16 && type != PIX_Q8_0 && type != PIX_Q5_K && type != PIX_Q6_K)
+        return fail(PIXHIP_ERR_UNSUPPORTED,"unsupported embedding type " + std::to_string(type));
+    size_t bytes = 0;
+    if (!stride || inner > SIZE_MAX / 4 || table_rows > SIZE_MAX / stride || !float_bytes(count,inner,&bytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"inner is not a whole number of blocks, or the table is too large");
+    if (!aligned4(output)) return fail(PIXHIP_ERR_ARGUMENT,"output must be 4-byte aligned");
+    for (size_t i = 0; i < count; i++)
+        if (ids[i] < 0 || (uint64_t)ids[i] >= table_rows) return fail(PIXHIP_ERR_ARGUMENT,"token id " + std::to_string(ids[i]) + " out of range");
+    void* out = nullptr;
+    if ((rc = write_operand(s,output,&out))) return rc;
+    Staged st(s);
+    const void* dev_table = nullptr;
+    hipError_t e;
+    if (device_visible(s,table,&dev_table)) {
+        // a device-resident table: gather on the device
+        std::vector<int64_t> rows(ids,ids + count);
+        const void* dev_ids = nullptr;
+        if ((rc = st.read(rows.data(),count * sizeof(int64_t),&dev_ids))) return rc;
+        e = pixhip::launch_decode_rows(dev_table,type,stride,static_cast<const int64_t*>(dev_ids),count,inner,static_cast<float*>(out),s->stream);
+    } else {
+        // the model file's mapping: pack the selected rows (vulkan_embedding,
+        // src/backend_vulkan.cpp:1241-1243) and move only those
+        std::vector<unsigned char> packed(count * stride);
+        const unsigned char* base = static_cast<const unsigned char*>(table);
+        for (size_t i = 0; i < count; i++) memcpy(packed.data() + i * stride,base + (size_t)ids[i] * stride,stride);
+        const void* dev_rows = nullptr;
+        if ((rc = st.read(packed.data(),packed.size(),&dev_rows))) return rc;
+        e = pixhip::launch_decode_rows(dev_rows,type,stride,nullptr,count,inner,static_cast<float*>(out),s->stream);
+    }
+    PIX_HIP(e,"embedding");
+    return PIXHIP_OK;
+}
+
+int pixhip_rows(pixhip_session* s, const float* source, size_t source_rows, float* destination, size_t destination_rows, size_t channels,
+                const size_t* rows, size_t count, int scatter)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    size_t sbytes = 0, dbytes = 0;
+    if (!source || !destination || !rows || !count || !channels || !source_rows || !destination_rows ||
+        !float_bytes(source_rows,channels,&sbytes) || !float_bytes(destination_rows,channels,&dbytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    // the reference's checks (src/tensor.cpp:277-279, :293-296)
+    if ((scatter? source_rows : destination_rows) != count) return fail(PIXHIP_ERR_ARGUMENT,"row count does not match the row list");
+    const size_t bound = scatter? destination_rows : source_rows;
+    for (size_t i = 0; i < count; i++)
+        if (rows[i] >= bound) return fail(PIXHIP_ERR_ARGUMENT,"row " + std::to_string(rows[i]) + " out of range");
+    std::vector<uint64_t> src_rows, dst_rows;
+    if (scatter) {
+        // a row listed twice keeps the last copy, as the reference's in-order loop does
+        std::unordered_map<size_t,size_t> last;
+        for (size_t i = 0; i < count; i++) last[rows[i]] = i;
+        for (size_t i = 0; i < count; i++)
+            if (last[rows[i]] == i) {
+                src_rows.push_back(i);
+                dst_rows.push_back(rows[i]);
+            }
+    } else {
+        src_rows.assign(rows,rows + count);
+    }
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    Staged st(s);
+    const void *src = nullptr, *sr = nullptr, *dr = nullptr;
+    if ((rc = st.read(source,sbytes,&src)) || (rc = st.read(src_rows.data(),src_rows.size() * sizeof(uint64_t),&sr))) return rc;
+    if (scatter && (rc = st.read(dst_rows.data(),dst_rows.size() * sizeof(uint64_t),&dr))) return rc;
+    hipError_t e = pixhip::launch_rows(static_cast<const float*>(src),static_cast<float*>(dst),static_cast<const uint64_t*>(sr),
+                                       static_cast<const uint64_t*>(dr),src_rows.size(),channels,s->stream);
+    PIX_HIP(e,"rows");
+    return PIXHIP_OK;
+}
+
+int pixhip_copy_rows(pixhip_session* s, const float* source, size_t source_rows, size_t source_channels, float* destination,
+                     size_t destination_rows, size_t destination_channels, size_t rows, size_t source_row, size_t source_feature,
+                     size_t destination_row)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    size_t sbytes = 0, dbytes = 0;
+    if (!source || !destination || !rows || !destination_channels || !float_bytes(source_rows,source_channels,&sbytes) ||
+        !float_bytes(destination_rows,destination_channels,&dbytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    if (source_row > source_rows || rows > source_rows - source_row || destination_row > destination_rows ||
+        rows > destination_rows - destination_row || source_feature > source_channels ||
+        destination_channels > source_channels - source_feature)
+        return fail(PIXHIP_ERR_ARGUMENT,"the copied rows do not lie within both tensors");
+    if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    Staged st(s);
+    const void* src = nullptr;
+    if ((rc = st.read(source,sbytes,&src))) return rc;
+    hipError_t e = pixhip::launch_copy2d(static_cast<const float*>(src) + source_row * source_channels + source_feature,source_channels,
+                                         static_cast<float*>(dst) + destination_row * destination_channels,destination_channels,rows,
+                                         destination_channels,s->stream);
+    PIX_HIP(e,"copy rows");
+    return PIXHIP_OK;
+}
+
+int pixhip_copy_features(pixhip_session* s, const float* source, size_t source_channels, float* destination, size_t destination_channels,
+                         size_t destination_feature)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    // the reference's checks (src/backend_vulkan.cpp:1273)
+    if (!source || !destination || !source_channels || !destination_channels || destination_feature > destination_channels ||
+        source_channels > destination_channels - destination_feature)
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer, empty tensor, or the source does not fit at the destination feature");
+    if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    Staged st(s);
+    const void* src = nullptr;
+    if ((rc = st.read(source,source_channels * sizeof(float),&src))) return rc;
+    hipError_t e = pixhip::launch_copy2d(static_cast<const float*>(src),source_channels,static_cast<float*>(dst) + destination_feature,
+                                         destination_channels,1,source_channels,s->stream);
+    PIX_HIP(e,"copy features");
+    return PIXHIP_OK;
+}
+
+int pixhip_layout(pixhip_session* s, unsigned operation, const float* source, size_t source_rows, size_t source_channels, float* destination,
+                  size_t destination_rows, size_t destination_channels, size_t width, size_t patch)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (operation != PIXHIP_OP_PATCH && operation != PIXHIP_OP_UNPATCH && operation != PIXHIP_OP_UPSAMPLE)
+        return fail(PIXHIP_ERR_UNSUPPORTED,"unsupported layout operation " + std::to_string(operation));
+    size_t sbytes = 0, dbytes = 0;
+    if (!source || !destination || !source_rows || !source_channels || !destination_rows || !destination_channels || !width ||
+        !float_bytes(source_rows,source_channels,&sbytes) || !float_bytes(destination_rows,destination_channels,&dbytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    bool ok;
+    if (operation == PIXHIP_OP_UPSAMPLE) {
+        // tensor_upsample's checks (src/tensor.cpp:306)
+        ok = source_rows % width == 0 && source_rows <= SIZE_MAX / 4 && destination_rows == source_rows * 4 &&
+             destination_channels == source_channels;
+    } else {
+        // the DiT layout (src/inference.cpp:364, :374-376): width and height multiples of the patch
+        const bool to_tokens = operation == PIXHIP_OP_PATCH;
+        const size_t pixels = to_tokens? source_rows : destination_rows, tokens = to_tokens? destination_rows : source_rows;
+        const size_t narrow = to_tokens? source_channels : destination_channels, wide = to_tokens? destination_channels : source_channels;
+        ok = patch && width % patch == 0 && pixels % width == 0 && (pixels / width) % patch == 0 && patch <= SIZE_MAX / patch &&
+             narrow <= SIZE_MAX / (patch * patch) && wide == narrow * patch * patch &&
+             tokens == (width / patch) * (pixels / width / patch);
+    }
+    if (!ok) return fail(PIXHIP_ERR_ARGUMENT,"tensor shapes do not match the layout");
+    if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    Staged st(s);
+    const void* src = nullptr;
+    if ((rc = st.read(source,sbytes,&src))) return rc;
+    const int op = operation == PIXHIP_OP_PATCH? pixhip::kLayoutPatch : operation == PIXHIP_OP_UNPATCH? pixhip::kLayoutUnpatch : pixhip::kLayoutUpsample;
+    hipError_t e = pixhip::launch_layout(op,static_cast<const float*>(src),static_cast<float*>(dst),destination_rows,destination_channels,width,
+                                         source_channels,patch,s->stream);
+    PIX_HIP(e,"layout");
+    return PIXHIP_OK;
+}
+
+int pixhip_shortcut(pixhip_session* s, const float* source, size_t width, size_t height, size_t source_channels, float* destination,
+                    size_t channels, size_t temporal, int up, int spatial)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    // tensor_resample_shortcut's checks (src/tensor.cpp:489-500)
+    if (!source || !destination || !width || !height || !channels || !temporal || !source_channels || width > SIZE_MAX / height)
+        return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty tensor");
+    const size_t side = spatial? 2 : 1;
+    if (temporal > SIZE_MAX / (side * side) || width > SIZE_MAX / side || height > SIZE_MAX / side)
+        return fail(PIXHIP_ERR_ARGUMENT,"shape too large");
+    const size_t factor = temporal * side * side;
+    if (channels > SIZE_MAX / factor || source_channels > SIZE_MAX / factor) return fail(PIXHIP_ERR_ARGUMENT,"shape too large");
+    if ((up && channels * factor % source_channels) || (!up && source_channels * factor % channels))
+        return fail(PIXHIP_ERR_ARGUMENT,"channels do not divide into the resampled groups");
+    if (!up && (width % side || height % side)) return fail(PIXHIP_ERR_ARGUMENT,"width and height must be even to go down");
+    const size_t out_width = up? width * side : width / side, out_height = up? height * side : height / side;
+    size_t sbytes = 0, dbytes = 0;
+    if (out_width > SIZE_MAX / out_height || !float_bytes(width * height,source_channels,&sbytes) ||
+        !float_bytes(out_width * out_height,channels,&dbytes))
+        return fail(PIXHIP_ERR_ARGUMENT,"shape too large");
+    if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    void* dst = nullptr;
+    if ((rc = write_operand(s,destination,&dst))) return rc;
+    Staged st(s);
+    const void* src = nullptr;
+    if ((rc = st.read(source,sbytes,&src))) return rc;
+    hipError_t e = pixhip::launch_shortcut(static_cast<const float*>(src),static_cast<float*>(dst),out_width * out_height,channels,
+                                           source_channels,width,side,temporal,up != 0,s->stream);
+    PIX_HIP(e,"shortcut");
     return PIXHIP_OK;
 }
 

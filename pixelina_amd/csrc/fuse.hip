@@ -112,28 +112,6 @@ __device__ __forceinline__ int row_chunks(const FuseArgs& a)
     return (int)(((a.kind == 2? a.kpad : a.K) + 255) / 256);
 }
 
-template <int CTRL> __device__ __forceinline__ double dpp_f64(double v)
-{
-    const int2 h = __builtin_bit_cast(int2,v);
-    return __builtin_bit_cast(double,make_int2(dpp_i32<CTRL>(h.x),dpp_i32<CTRL>(h.y)));
-}
-__device__ __forceinline__ double lane_f64(double v, int lane)
-{
-    const int2 h = __builtin_bit_cast(int2,v);
-    return __builtin_bit_cast(double,make_int2(__builtin_amdgcn_readlane(h.x,lane),__builtin_amdgcn_readlane(h.y,lane)));
-}
-
-// Sum over the 64 lanes in double (every lane active), the same value in every
-// lane: rows of 16 by DPP, then the four row sums in order.
-__device__ __forceinline__ double wave_sum_f64(double v)
-{
-    v += dpp_f64<kDppXor1>(v);
-    v += dpp_f64<kDppXor2>(v);
-    v += dpp_f64<kDppHalfMirror>(v);
-    v += dpp_f64<kDppMirror>(v);
-    return (lane_f64(v,0) + lane_f64(v,16)) + (lane_f64(v,32) + lane_f64(v,48));
-}
-
 // Sum over the WPR waves of one row (consecutive waves of the workgroup).
 // Every wave of the workgroup must call it when WPR > 1 (it synchronises).
 template <int WPR>

@@ -73,6 +73,28 @@ __device__ __forceinline__ float wave_sum(float v)
     return (lane_f32(v,0) + lane_f32(v,16)) + (lane_f32(v,32) + lane_f32(v,48));
 }
 
+template <int CTRL> __device__ __forceinline__ double dpp_f64(double v)
+{
+    const int2 h = __builtin_bit_cast(int2,v);
+    return __builtin_bit_cast(double,make_int2(dpp_i32<CTRL>(h.x),dpp_i32<CTRL>(h.y)));
+}
+__device__ __forceinline__ double lane_f64(double v, int lane)
+{
+    const int2 h = __builtin_bit_cast(int2,v);
+    return __builtin_bit_cast(double,make_int2(__builtin_amdgcn_readlane(h.x,lane),__builtin_amdgcn_readlane(h.y,lane)));
+}
+
+// Sum over the 64 lanes in double (every lane active), the same value in every
+// lane: rows of 16 by DPP, then the four row sums in order.
+__device__ __forceinline__ double wave_sum_f64(double v)
+{
+    v += dpp_f64<kDppXor1>(v);
+    v += dpp_f64<kDppXor2>(v);
+    v += dpp_f64<kDppHalfMirror>(v);
+    v += dpp_f64<kDppMirror>(v);
+    return (lane_f64(v,0) + lane_f64(v,16)) + (lane_f64(v,32) + lane_f64(v,48));
+}
+
 // One Q8_K block (256 values) quantized by one full wave, 4 consecutive values
 // per lane (lane l holds x[4l..4l+3]).  Semantics of quantize_row_q8_K_ref
 // (src/kernels_quant.cpp:80-118):

@@ -52,6 +52,9 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#define PIX_F32 0
+#define PIX_F16 1
+#define PIX_BF16 30
 #define PIX_Q8_0 8
 #define PIX_Q5_K 13
 #define PIX_Q6_K 14
@@ -163,6 +166,30 @@ constexpr int kOpSilu = 2, kOpGate = 3, kOpAdd = 4, kOpBias = 14, kOpGeluExact =
 hipError_t launch_pointwise(int op, float* x, const float* other, size_t rows, size_t channels, hipStream_t s);
 hipError_t launch_rope(float* x, size_t rows, size_t channels, size_t heads, const float* cosine, const float* sine, bool interleaved,
                        hipStream_t s);
+
+// tensor_ops.hip: the rest of the backend op surface (ids of src/vulkan_ops.h:24-49)
+constexpr int kOpModulate = 8, kOpResidual = 9, kOpAffine = 10, kOpQwenScale = 24, kOpQwenResidual = 25, kOpEuler = 26;
+constexpr int kLayoutPatch = 15, kLayoutUnpatch = 16, kLayoutUpsample = 17;
+// x [rows][channels] in place; p0 / p1 per-channel parameters (p1 for rows
+// below `split`, QWEN ops only), `other` [rows][channels].
+hipError_t launch_channel_op(int op, float* x, const float* other, const float* p0, const float* p1, size_t rows, size_t channels,
+                             size_t split, float scale, float bias, hipStream_t s);
+hipError_t launch_l2norm(const float* x, const float* w, float* y, size_t rows, size_t channels, float eps, hipStream_t s);
+// Workspace of launch_groupnorm; 0 when the shape is not supported (channels
+// not a multiple of 32, or groups wider than 1024 channels).
+size_t groupnorm_workspace_bytes(size_t rows, size_t channels);
+hipError_t launch_groupnorm(const float* x, const float* w, const float* b, float* y, size_t rows, size_t channels, float eps,
+                            void* workspace, hipStream_t s);
+// Rows ids[r] (ids null: r) of a table of GGUF rows `stride` bytes apart, decoded to fp32 [count][inner].
+hipError_t launch_decode_rows(const void* table, uint32_t type, size_t stride, const int64_t* ids, size_t count, size_t inner, float* out,
+                              hipStream_t s);
+hipError_t launch_rows(const float* src, float* dst, const uint64_t* src_rows, const uint64_t* dst_rows, size_t n, size_t channels,
+                       hipStream_t s);
+hipError_t launch_copy2d(const float* src, size_t src_stride, float* dst, size_t dst_stride, size_t rows, size_t columns, hipStream_t s);
+hipError_t launch_layout(int op, const float* src, float* dst, size_t rows, size_t channels, size_t width, size_t src_channels, size_t patch,
+                         hipStream_t s);
+hipError_t launch_shortcut(const float* src, float* dst, size_t out_rows, size_t channels, size_t src_channels, size_t width, size_t side,
+                           size_t temporal, bool up, hipStream_t s);
 
 // repack.hip
 hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,

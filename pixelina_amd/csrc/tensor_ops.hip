@@ -1,0 +1,680 @@
+// The rest of the reference's backend op surface on device tensors (the
+// counterparts of src/backend_vulkan.h:141-156 and of the CPU ops they stand
+// in for).  All of it is HBM-bound data movement or one pass of arithmetic per
+// value; each kernel moves contiguous runs of a row per wave (float4 where the
+// shapes and pointers allow) and keeps the reference's fp32 operation order,
+// so that results are bit-identical to the CPU path:
+//   channel ops   z_modulate / z_residual (src/inference.cpp:263-291), the VAE
+//                 and sampler affine steps (:474-478, :612-631),
+//                 qwen_image_euler (src/qwen_image.cpp:347-361),
+//                 qwen_image_modulate (:149-169)
+//   l2norm        tensor_l2norm (src/tensor.cpp:242-258)
+//   groupnorm     tensor_groupnorm (src/tensor.cpp:454-485)
+//   decode        cpu_decode (src/backend_cpu.cpp:24-101) for vulkan_embedding
+//   rows, copies  tensor_gather / tensor_scatter (src/tensor.cpp:274-302),
+//                 vulkan_copy_rows / vulkan_copy_features
+//                 (src/backend_vulkan.cpp:1257-1281)
+//   layout        the DiT patch / unpatch loops (src/inference.cpp:374-390,
+//                 :438-455) and tensor_upsample (src/tensor.cpp:304-319)
+//   shortcut      tensor_resample_shortcut (src/tensor.cpp:487-527)
+// tanh and the norms' sums are the exceptions: tanh is the fp32 rounding of the
+// double function (the reference's glibc tanhf is within about an ulp of it),
+// and the norms' double sums are formed in another order than the reference's
+// running sums, which moves the fp32 results only when a double lands within
+// its last bits of an fp32 rounding boundary.
+#include <algorithm>
+
+#include "pixhip_device.h"
+#include "pixhip_internal.h"
+
+namespace pixhip {
+
+namespace {
+
+unsigned grid_for(size_t work, size_t per_block = 256)
+{
+    return (unsigned)std::min<size_t>((work + per_block - 1) / per_block,(size_t)1 << 20);
+}
+
+bool aligned16(const void* p)
+{
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+template <int VEC> struct Vec;
+template <> struct Vec<1> {
+    typedef float T;
+    static __device__ __forceinline__ float get(const T& v, int) { return v; }
+    static __device__ __forceinline__ void set(T& v, int, float x) { v = x; }
+};
+template <> struct Vec<4> {
+    typedef float4 T;
+    static __device__ __forceinline__ float get(const T& v, int i) { return i == 0? v.x : i == 1? v.y : i == 2? v.z : v.w; }
+    static __device__ __forceinline__ void set(T& v, int i, float x)
+    {
+        if (i == 0) v.x = x;
+        else if (i == 1) v.y = x;
+        else if (i == 2) v.z = x;
+        else v.w = x;
+    }
+};
+
+__device__ __forceinline__ float tanh_value(float v)
+{
+    return (float)tanh((double)v);
+}
+
+}  // namespace
+
+// ---- channel ops ---------------------------------------------------------
+//
+// Thread (block x, lane) owns VEC consecutive channels and walks kChanRows
+// rows of them, so the per-channel factor (1 + p, tanh p) is formed once:
+//   MODULATE       x *= (1.0f + p0[c])
+//   RESIDUAL       x += other[i] * tanh(p0[c])      (p0 NULL: x += other[i] * 1.0f)
+//   AFFINE         x = x * scale + bias
+//   EULER          x += other[i] * scale
+//   QWEN_SCALE     x *= (1 + p[c]),         p = row >= split? p0 : p1
+//   QWEN_RESIDUAL  x += other[i] * tanh(p[c]), p as above
+constexpr int kChanRows = 8;
+
+struct ChanArgs {
+    float* x;
+    const float* other;
+    const float *p0, *p1;
+    size_t rows, channels, split;
+    float scale, bias;
+};
+
+template <int OP, int VEC>
+__global__ __launch_bounds__(256) void channel_kernel(ChanArgs a)
+{
+    typedef typename Vec<VEC>::T T;
+    const size_t c0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * VEC;
+    if (c0 >= a.channels) return;
+    float f0[VEC], f1[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; j++) {
+        f0[j] = f1[j] = 1.0f;
+        if constexpr (OP == kOpModulate || OP == kOpQwenScale) f0[j] = __fadd_rn(1.0f,a.p0[c0 + j]);
+        if constexpr (OP == kOpQwenScale) f1[j] = __fadd_rn(1.0f,a.p1[c0 + j]);
+        if constexpr (OP == kOpResidual) f0[j] = a.p0? tanh_value(a.p0[c0 + j]) : 1.0f;
+        if constexpr (OP == kOpQwenResidual) {
+            f0[j] = tanh_value(a.p0[c0 + j]);
+            f1[j] = tanh_value(a.p1[c0 + j]);
+        }
+    }
+    const size_t r0 = (size_t)blockIdx.y * kChanRows, r1 = std::min(r0 + kChanRows,a.rows);
+    for (size_t r = r0; r < r1; r++) {
+        const size_t i = r * a.channels + c0;
+        T v = *reinterpret_cast<const T*>(a.x + i);
+        T o{};
+        if constexpr (OP == kOpResidual || OP == kOpEuler || OP == kOpQwenResidual) o = *reinterpret_cast<const T*>(a.other + i);
+        const bool first = r >= a.split;
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+            const float x = Vec<VEC>::get(v,j), f = first? f0[j] : f1[j];
+            float y;
+            if constexpr (OP == kOpModulate || OP == kOpQwenScale) y = __fmul_rn(x,f);
+            else if constexpr (OP == kOpResidual || OP == kOpQwenResidual) y = __fadd_rn(x,__fmul_rn(Vec<VEC>::get(o,j),f));
+            else if constexpr (OP == kOpAffine) y = __fadd_rn(__fmul_rn(x,a.scale),a.bias);
+            else y = __fadd_rn(x,__fmul_rn(Vec<VEC>::get(o,j),a.scale));
+            Vec<VEC>::set(v,j,y);
+        }
+        *reinterpret_cast<T*>(a.x + i) = v;
+    }
+}
+
+template <int OP>
+static hipError_t channel_launch(const ChanArgs& a, bool vec, hipStream_t s)
+{
+    const size_t vecw = vec? 4 : 1;
+    const dim3 grid((unsigned)((a.channels / vecw + 255) / 256),(unsigned)((a.rows + kChanRows - 1) / kChanRows));
+    if (vec) channel_kernel<OP,4><<<grid,dim3(256),0,s>>>(a);
+    else channel_kernel<OP,1><<<grid,dim3(256),0,s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_channel_op(int op, float* x, const float* other, const float* p0, const float* p1, size_t rows, size_t channels,
+                             size_t split, float scale, float bias, hipStream_t s)
+{
+    if (!rows || !channels) return hipSuccess;
+    if ((rows + kChanRows - 1) / kChanRows > 65535) return hipErrorInvalidValue;
+    const ChanArgs a{x,other,p0,p1,rows,channels,split,scale,bias};
+    const bool vec = channels % 4 == 0 && aligned16(x) && (!other || aligned16(other)) && (!p0 || aligned16(p0)) &&
+                     (!p1 || aligned16(p1));
+    switch (op) {
+    case kOpModulate: return channel_launch<kOpModulate>(a,vec,s);
+    case kOpResidual: return channel_launch<kOpResidual>(a,vec,s);
+    case kOpAffine: return channel_launch<kOpAffine>(a,vec,s);
+    case kOpEuler: return channel_launch<kOpEuler>(a,vec,s);
+    case kOpQwenScale: return channel_launch<kOpQwenScale>(a,vec,s);
+    case kOpQwenResidual: return channel_launch<kOpQwenResidual>(a,vec,s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ---- l2norm ---------------------------------------------------------------
+//
+// One wave per row, four rows per block:
+//   square  = sum of (double)x * x
+//   inverse = (float)(sqrt((double)channels) / max(sqrt(square), (double)eps))
+//   y       = x * inverse * w[c]      (fp32, left to right; w NULL: * 1)
+// The second pass re-reads the row, which the first has just brought into L2.
+template <int VEC>
+__global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+                                                     size_t rows, size_t channels, float eps)
+{
+    typedef typename Vec<VEC>::T T;
+    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // whole waves leave together
+    const int lane = threadIdx.x & 63;
+    const float* in = x + row * channels;
+    float* out = y + row * channels;
+    double sq = 0.0;
+    for (size_t c = (size_t)lane * VEC; c < channels; c += 64 * VEC) {
+        const T v = *reinterpret_cast<const T*>(in + c);
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+            const double d = Vec<VEC>::get(v,j);
+            sq += d * d;
+        }
+    }
+    sq = wave_sum_f64(sq);
+    const double root = sqrt(sq), floor = (double)eps;
+    const float inverse = (float)(sqrt((double)channels) / (root < floor? floor : root));
+    for (size_t c = (size_t)lane * VEC; c < channels; c += 64 * VEC) {
+        T v = *reinterpret_cast<const T*>(in + c);
+#pragma unroll
+        for (int j = 0; j < VEC; j++)
+            Vec<VEC>::set(v,j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v,j),inverse),w? w[c + j] : 1.0f));
+        *reinterpret_cast<T*>(out + c) = v;
+    }
+}
+
+hipError_t launch_l2norm(const float* x, const float* w, float* y, size_t rows, size_t channels, float eps, hipStream_t s)
+{
+    if (!rows || !channels) return hipSuccess;
+    if ((rows + 3) / 4 > 0x7fffffffu) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    if (channels % 4 == 0 && aligned16(x) && aligned16(y)) l2norm_kernel<4><<<grid,block,0,s>>>(x,w,y,rows,channels,eps);
+    else l2norm_kernel<1><<<grid,block,0,s>>>(x,w,y,rows,channels,eps);
+    return hipGetLastError();
+}
+
+// ---- groupnorm ------------------------------------------------------------
+//
+// 32 groups of gs = channels / 32 consecutive channels, each normalised over
+// all rows (the VAE's GroupNorm over pixels):
+//   mean    = sum of x / n                       (double, n = rows * gs)
+//   square  = sum of (x - mean)^2                (double)
+//   inverse = (float)(1 / sqrt(square / n + eps))
+//   y       = (float)(x - mean) * inverse * w[c] + b[c]     (fp32)
+// Three passes:
+//   partial  a block holds kGnRows passes of a [rp rows x L columns] tile in
+//            registers (columns of VEC channels, L a multiple of gs / VEC, so
+//            no group straddles two tiles) and writes each group's chunk mean
+//            and sum of squared deviations from it (two passes over the
+//            registers, double);
+//   merge    one block per group combines the chunks in a fixed order with the
+//            pairwise update (Chan, Golub and LeVeque): n = na + nb,
+//            d = mb - ma, mean = ma + d * nb / n, M2 = M2a + M2b + d^2 na nb / n;
+//   apply    one pass over x and the output.
+// HBM traffic is two reads and one write of the tensor.
+constexpr int kGroups = 32;
+constexpr int kGnRows = 8;
+
+// rows x channels in columns of VEC channels (cvec of them); a partial block
+// covers a tile of `lanes` columns and rp * kGnRows rows (one chunk).
+struct GnShape {
+    size_t rows, channels, gs, cvec, chunks;
+    int lanes, rp, tiles;
+};
+
+struct GnStat {
+    double mean;
+    float inverse;
+    float pad;
+};
+
+template <int VEC>
+__global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict__ x, GnShape sh, double* __restrict__ part)
+{
+    typedef typename Vec<VEC>::T T;
+    __shared__ double red[256];
+    __shared__ double colsum[256];
+    __shared__ double gmean[256];
+    const int t = threadIdx.x, col = t % sh.lanes, ro = t / sh.lanes;
+    const size_t tile = blockIdx.y, chunk = blockIdx.x;
+    const size_t cv = tile * sh.lanes + col;
+    const int q = (int)(sh.gs / VEC);  // columns per group
+    const int tile_cols = (int)std::min<size_t>(sh.lanes,sh.cvec - tile * sh.lanes);
+    const bool active = ro < sh.rp && col < tile_cols;
+    const size_t row0 = chunk * sh.rp * kGnRows;
+    const size_t valid = std::min<size_t>(sh.rows - row0,(size_t)sh.rp * kGnRows);
+    T v[kGnRows];
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < kGnRows; k++) {
+        const size_t r = row0 + ro + (size_t)k * sh.rp;
+        v[k] = T{};
+        if (active && r < sh.rows) {
+            v[k] = *reinterpret_cast<const T*>(x + r * sh.channels + cv * VEC);
+#pragma unroll
+            for (int j = 0; j < VEC; j++) sum += (double)Vec<VEC>::get(v[k],j);
+        }
+    }
+    const int groups = tile_cols / q;
+    const double n = (double)valid * (double)sh.gs;
+    // pass 1: chunk means; pass 2: squared deviations from them
+    for (int pass = 0; pass < 2; pass++) {
+        double local = sum;
+        if (pass == 1) {
+            local = 0.0;
+            if (active) {
+                const double m = gmean[col / q];
+#pragma unroll
+                for (int k = 0; k < kGnRows; k++) {
+                    const size_t r = row0 + ro + (size_t)k * sh.rp;
+                    if (r < sh.rows) {
+#pragma unroll
+                        for (int j = 0; j < VEC; j++) {
+                            const double d = (double)Vec<VEC>::get(v[k],j) - m;
+                            local += d * d;
+                        }
+                    }
+                }
+            }
+        }
+        red[t] = active? local : 0.0;
+        __syncthreads();
+        if (t < tile_cols) {
+            double s = 0.0;
+            for (int i = 0; i < sh.rp; i++) s += red[i * sh.lanes + t];
+            colsum[t] = s;
+        }
+        __syncthreads();
+        if (t < groups) {
+            double s = 0.0;
+            for (int i = 0; i < q; i++) s += colsum[t * q + i];
+            const size_t g = (tile * sh.lanes) / q + t;
+            if (pass == 0) {
+                gmean[t] = s / n;
+                part[(chunk * kGroups + g) * 2] = s / n;
+            } else {
+                part[(chunk * kGroups + g) * 2 + 1] = s;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void gn_merge_kernel(const double* __restrict__ part, GnShape sh, float eps, GnStat* __restrict__ stat)
+{
+    __shared__ double sn[256], sm[256], s2[256];
+    const int g = blockIdx.x, t = threadIdx.x;
+    const size_t per_chunk = (size_t)sh.rp * kGnRows;
+    double n = 0.0, mean = 0.0, m2 = 0.0;
+    for (size_t c = t; c < sh.chunks; c += 256) {
+        const double nb = (double)std::min<size_t>(sh.rows - c * per_chunk,per_chunk) * (double)sh.gs;
+        const double mb = part[(c * kGroups + g) * 2], qb = part[(c * kGroups + g) * 2 + 1];
+        if (n == 0.0) {
+            n = nb;
+            mean = mb;
+            m2 = qb;
+        } else {
+            const double total = n + nb, d = mb - mean;
+            mean += d * (nb / total);
+            m2 += qb + d * d * (n * nb / total);
+            n = total;
+        }
+    }
+    sn[t] = n;
+    sm[t] = mean;
+    s2[t] = m2;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if (t < stride && sn[t + stride] != 0.0) {
+            const double na = sn[t], nb = sn[t + stride];
+            if (na == 0.0) {
+                sn[t] = nb;
+                sm[t] = sm[t + stride];
+                s2[t] = s2[t + stride];
+            } else {
+                const double total = na + nb, d = sm[t + stride] - sm[t];
+                sm[t] += d * (nb / total);
+                s2[t] += s2[t + stride] + d * d * (na * nb / total);
+                sn[t] = total;
+            }
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        const double count = (double)sh.rows * (double)sh.gs;
+        stat[g].mean = sm[0];
+        stat[g].inverse = (float)(1.0 / sqrt(s2[0] / count + (double)eps));
+        stat[g].pad = 0.0f;
+    }
+}
+
+template <int VEC>
+__global__ __launch_bounds__(256) void gn_apply_kernel(const float* __restrict__ x, GnShape sh, const GnStat* __restrict__ stat,
+                                                       const float* __restrict__ w, const float* __restrict__ b, float* __restrict__ y)
+{
+    typedef typename Vec<VEC>::T T;
+    __shared__ GnStat st[kGroups];
+    if (threadIdx.x < kGroups) st[threadIdx.x] = stat[threadIdx.x];
+    __syncthreads();
+    const size_t total = sh.rows * sh.cvec, stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const size_t cv = e % sh.cvec, c = cv * VEC;
+        const GnStat gs = st[c / sh.gs];
+        T v = *reinterpret_cast<const T*>(x + e * VEC);
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+            const float d = (float)((double)Vec<VEC>::get(v,j) - gs.mean);
+            Vec<VEC>::set(v,j,__fadd_rn(__fmul_rn(__fmul_rn(d,gs.inverse),w[c + j]),b[c + j]));
+        }
+        *reinterpret_cast<T*>(y + e * VEC) = v;
+    }
+}
+
+bool groupnorm_shape(size_t rows, size_t channels, bool vec, GnShape* sh)
+{
+    if (!rows || !channels || channels % kGroups) return false;
+    const int w = vec? 4 : 1;
+    sh->rows = rows;
+    sh->channels = channels;
+    sh->gs = channels / kGroups;
+    if (sh->gs % w) return false;
+    sh->cvec = channels / w;
+    const size_t q = sh->gs / w;
+    if (q > 256) return false;
+    sh->lanes = (int)(sh->cvec <= 256? sh->cvec : 256 / q * q);
+    sh->rp = 256 / sh->lanes;
+    sh->tiles = (sh->cvec + sh->lanes - 1) / sh->lanes;
+    sh->chunks = (rows + (size_t)sh->rp * kGnRows - 1) / ((size_t)sh->rp * kGnRows);
+    return sh->chunks <= 0x7fffffffu && sh->tiles <= 65535;
+}
+
+// Workspace: the 32 group statistics, then [chunks][32] (mean, M2) pairs for
+// the larger chunk count of the two column widths.
+size_t groupnorm_workspace_bytes(size_t rows, size_t channels)
+{
+    GnShape scalar{}, vec{};
+    if (!groupnorm_shape(rows,channels,false,&scalar)) return 0;
+    size_t chunks = scalar.chunks;
+    if (groupnorm_shape(rows,channels,true,&vec)) chunks = std::max(chunks,vec.chunks);
+    return kGroups * sizeof(GnStat) + chunks * kGroups * 2 * sizeof(double);
+}
+
+hipError_t launch_groupnorm(const float* x, const float* w, const float* b, float* y, size_t rows, size_t channels, float eps,
+                            void* workspace, hipStream_t s)
+{
+    const bool vec = channels % (4 * kGroups) == 0 && aligned16(x) && aligned16(y);
+    GnShape sh{};
+    if (!groupnorm_shape(rows,channels,vec,&sh)) return hipErrorInvalidValue;
+    GnStat* stat = static_cast<GnStat*>(workspace);
+    double* part = reinterpret_cast<double*>(stat + kGroups);
+    const dim3 pgrid((unsigned)sh.chunks,(unsigned)sh.tiles), block(256);
+    if (vec) gn_partial_kernel<4><<<pgrid,block,0,s>>>(x,sh,part);
+    else gn_partial_kernel<1><<<pgrid,block,0,s>>>(x,sh,part);
+    gn_merge_kernel<<<dim3(kGroups),block,0,s>>>(part,sh,eps,stat);
+    const unsigned agrid = grid_for(rows * sh.cvec);
+    if (vec) gn_apply_kernel<4><<<dim3(agrid),block,0,s>>>(x,sh,stat,w,b,y);
+    else gn_apply_kernel<1><<<dim3(agrid),block,0,s>>>(x,sh,stat,w,b,y);
+    return hipGetLastError();
+}
+
+// ---- decode (embedding rows) ----------------------------------------------
+//
+// Row r of the output is row ids[r] (ids NULL: row r) of a table of GGUF rows
+// `stride` bytes apart, decoded as cpu_decode does, in its fp32 order:
+//   F32 the bits; BF16 the bits << 16; F16 exact (NaN as the reference's
+//   half_float: a quiet NaN with the sign, whatever the payload);
+//   Q8_0  (float)q * d
+//   Q5_K  d * scale * q - dmin * min
+//   Q6_K  d * scale * (q - 32)
+// One thread per output value; the block bytes it reads are shared with its
+// neighbours through the cache.
+__device__ __forceinline__ float half_float_ref(uint16_t h)
+{
+    if ((h & 0x7c00u) == 0x7c00u && (h & 0x03ffu)) return __uint_as_float((h & 0x8000u)? 0xffc00000u : 0x7fc00000u);
+    return half_bits_to_float(h);
+}
+
+__device__ __forceinline__ uint16_t load16(const uint8_t* p)
+{
+    return (uint16_t)(p[0] | (p[1] << 8));
+}
+
+template <uint32_t TYPE>
+__device__ __forceinline__ float decode_value(const uint8_t* row, size_t j)
+{
+    if constexpr (TYPE == PIX_F32) {
+        return __uint_as_float((uint32_t)row[4 * j] | ((uint32_t)row[4 * j + 1] << 8) | ((uint32_t)row[4 * j + 2] << 16) |
+                               ((uint32_t)row[4 * j + 3] << 24));
+    } else if constexpr (TYPE == PIX_F16) {
+        return half_float_ref(load16(row + 2 * j));
+    } else if constexpr (TYPE == PIX_BF16) {
+        return __uint_as_float((uint32_t)load16(row + 2 * j) << 16);
+    } else if constexpr (TYPE == PIX_Q8_0) {
+        const uint8_t* blk = row + (j / PIX_QK8) * PIX_Q8_0_BYTES;
+        return __fmul_rn((float)(int8_t)blk[2 + j % PIX_QK8],half_float_ref(load16(blk)));
+    } else if constexpr (TYPE == PIX_Q5_K) {
+        const uint8_t* blk = row + (j / PIX_QK) * PIX_Q5_K_BYTES;
+        const unsigned within = (unsigned)(j % PIX_QK), group = within / 32, i = within % 32;
+        const uint8_t* sc = blk + 4;
+        unsigned scale, min;
+        if (group < 4) {
+            scale = sc[group] & 63u;
+            min = sc[group + 4] & 63u;
+        } else {
+            scale = (sc[group + 4] & 15u) | ((unsigned)(sc[group - 4] >> 6) << 4);
+            min = (unsigned)(sc[group + 4] >> 4) | ((unsigned)(sc[group] >> 6) << 4);
+        }
+        unsigned q = blk[48 + (group / 2) * 32 + i];
+        q = group % 2? q >> 4 : q & 15u;
+        if (blk[16 + i] & (1u << group)) q += 16;
+        const float d = half_float_ref(load16(blk)), dmin = half_float_ref(load16(blk + 2));
+        return __fsub_rn(__fmul_rn(__fmul_rn(d,(float)scale),(float)q),__fmul_rn(dmin,(float)min));
+    } else {
+        const uint8_t* blk = row + (j / PIX_QK) * PIX_Q6_K_BYTES;
+        const unsigned within = (unsigned)(j % PIX_QK), half = within / 128, group = (within % 128) / 32, i = within % 32;
+        unsigned q = blk[half * 64 + i + (group % 2) * 32];
+        q = group < 2? q & 15u : q >> 4;
+        q |= ((unsigned)(blk[128 + half * 32 + i] >> (group * 2)) & 3u) << 4;
+        const int scale = (int8_t)blk[192 + half * 8 + i / 16 + group * 2];
+        return __fmul_rn(__fmul_rn(half_float_ref(load16(blk + 208)),(float)scale),(float)((int)q - 32));
+    }
+}
+
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__ table, const int64_t* __restrict__ ids, size_t stride,
+                                                     size_t count, size_t inner, float* __restrict__ out)
+{
+    const size_t total = count * inner, step = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
+        const size_t r = e / inner, j = e % inner;
+        const uint8_t* row = table + (size_t)(ids? ids[r] : (int64_t)r) * stride;
+        out[e] = decode_value<TYPE>(row,j);
+    }
+}
+
+hipError_t launch_decode_rows(const void* table, uint32_t type, size_t stride, const int64_t* ids, size_t count, size_t inner, float* out,
+                              hipStream_t s)
+{
+    if (!count || !inner) return hipSuccess;
+    const dim3 g(grid_for(count * inner)), b(256);
+    const uint8_t* t = static_cast<const uint8_t*>(table);
+    switch (type) {
+    case PIX_F32: decode_kernel<PIX_F32><<<g,b,0,s>>>(t,ids,stride,count,inner,out); break;
+    case PIX_F16: decode_kernel<PIX_F16><<<g,b,0,s>>>(t,ids,stride,count,inner,out); break;
+    case PIX_BF16: decode_kernel<PIX_BF16><<<g,b,0,s>>>(t,ids,stride,count,inner,out); break;
+    case PIX_Q8_0: decode_kernel<PIX_Q8_0><<<g,b,0,s>>>(t,ids,stride,count,inner,out); break;
+    case PIX_Q5_K: decode_kernel<PIX_Q5_K><<<g,b,0,s>>>(t,ids,stride,count,inner,out); break;
+    case PIX_Q6_K: decode_kernel<PIX_Q6_K><<<g,b,0,s>>>(t,ids,stride,count,inner,out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---- row moves ------------------------------------------------------------
+//
+// rows: destination row dst_rows[k] (NULL: k) = source row src_rows[k] (NULL:
+// k), k < n, `cvec` columns of VEC floats.  copy2d: `rows` rows of cvec
+// columns between two row strides (in floats).
+template <int VEC>
+__global__ __launch_bounds__(256) void rows_kernel(const float* __restrict__ src, float* __restrict__ dst, const uint64_t* __restrict__ src_rows,
+                                                   const uint64_t* __restrict__ dst_rows, size_t n, size_t cvec)
+{
+    typedef typename Vec<VEC>::T T;
+    const size_t total = n * cvec, step = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
+        const size_t k = e / cvec, j = e % cvec;
+        const size_t sr = src_rows? src_rows[k] : k, dr = dst_rows? dst_rows[k] : k;
+        reinterpret_cast<T*>(dst)[dr * cvec + j] = reinterpret_cast<const T*>(src)[sr * cvec + j];
+    }
+}
+
+hipError_t launch_rows(const float* src, float* dst, const uint64_t* src_rows, const uint64_t* dst_rows, size_t n, size_t channels,
+                       hipStream_t s)
+{
+    if (!n || !channels) return hipSuccess;
+    const bool vec = channels % 4 == 0 && aligned16(src) && aligned16(dst);
+    const size_t cvec = vec? channels / 4 : channels;
+    const dim3 g(grid_for(n * cvec)), b(256);
+    if (vec) rows_kernel<4><<<g,b,0,s>>>(src,dst,src_rows,dst_rows,n,cvec);
+    else rows_kernel<1><<<g,b,0,s>>>(src,dst,src_rows,dst_rows,n,cvec);
+    return hipGetLastError();
+}
+
+template <int VEC>
+__global__ __launch_bounds__(256) void copy2d_kernel(const float* __restrict__ src, size_t src_stride, float* __restrict__ dst,
+                                                     size_t dst_stride, size_t rows, size_t cvec)
+{
+    typedef typename Vec<VEC>::T T;
+    const size_t total = rows * cvec, step = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
+        const size_t r = e / cvec, j = e % cvec;
+        *reinterpret_cast<T*>(dst + r * dst_stride + j * VEC) = *reinterpret_cast<const T*>(src + r * src_stride + j * VEC);
+    }
+}
+
+hipError_t launch_copy2d(const float* src, size_t src_stride, float* dst, size_t dst_stride, size_t rows, size_t columns, hipStream_t s)
+{
+    if (!rows || !columns) return hipSuccess;
+    const bool vec = columns % 4 == 0 && src_stride % 4 == 0 && dst_stride % 4 == 0 && aligned16(src) && aligned16(dst);
+    const size_t cvec = vec? columns / 4 : columns;
+    const dim3 g(grid_for(rows * cvec)), b(256);
+    if (vec) copy2d_kernel<4><<<g,b,0,s>>>(src,src_stride,dst,dst_stride,rows,cvec);
+    else copy2d_kernel<1><<<g,b,0,s>>>(src,src_stride,dst,dst_stride,rows,cvec);
+    return hipGetLastError();
+}
+
+// ---- layout ---------------------------------------------------------------
+//
+// Each destination value (VEC of them at a time; VEC = 4 needs the run of
+// `inner` channels that moves together to be a multiple of 4) reads one source
+// value:
+//   PATCH    dst [ (W/p)(H/p) ][ p*p*C ]: token t, feature f -> pixel
+//            (x, y) = ((t % (W/p))*p + (f/C) % p, (t / (W/p))*p + (f/C) / p),
+//            channel f % C
+//   UNPATCH  dst [ W*H ][ C ]: pixel (x, y), channel c -> token
+//            (y/p)*(W/p) + x/p, feature ((y % p)*p + x % p)*C + c
+//   UPSAMPLE dst [ 4*W*H ][ C ]: pixel (x, y) of width 2W -> (x/2, y/2)
+// (W the source width for PATCH and UPSAMPLE, the destination width for UNPATCH.)
+template <int OP, int VEC>
+__global__ __launch_bounds__(256) void layout_kernel(const float* __restrict__ src, float* __restrict__ dst, size_t rows, size_t channels,
+                                                     size_t width, size_t src_channels, size_t patch)
+{
+    typedef typename Vec<VEC>::T T;
+    const size_t cvec = channels / VEC, total = rows * cvec, step = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
+        const size_t row = e / cvec, f = (e % cvec) * VEC;
+        size_t from;
+        if constexpr (OP == kLayoutPatch) {
+            const size_t pw = width / patch, pixel = f / src_channels;
+            const size_t x = (row % pw) * patch + pixel % patch, y = (row / pw) * patch + pixel / patch;
+            from = (y * width + x) * src_channels + f % src_channels;
+        } else if constexpr (OP == kLayoutUnpatch) {
+            const size_t x = row % width, y = row / width;
+            const size_t token = (y / patch) * (width / patch) + x / patch;
+            from = token * src_channels + ((y % patch) * patch + x % patch) * channels + f;
+        } else {
+            const size_t x = row % (width * 2), y = row / (width * 2);
+            from = ((y / 2) * width + x / 2) * channels + f;
+        }
+        *reinterpret_cast<T*>(dst + row * channels + f) = *reinterpret_cast<const T*>(src + from);
+    }
+}
+
+template <int OP>
+static hipError_t layout_launch(const float* src, float* dst, size_t rows, size_t channels, size_t width, size_t src_channels, size_t patch,
+                                bool vec, hipStream_t s)
+{
+    const dim3 g(grid_for(rows * (vec? channels / 4 : channels))), b(256);
+    if (vec) layout_kernel<OP,4><<<g,b,0,s>>>(src,dst,rows,channels,width,src_channels,patch);
+    else layout_kernel<OP,1><<<g,b,0,s>>>(src,dst,rows,channels,width,src_channels,patch);
+    return hipGetLastError();
+}
+
+hipError_t launch_layout(int op, const float* src, float* dst, size_t rows, size_t channels, size_t width, size_t src_channels, size_t patch,
+                         hipStream_t s)
+{
+    if (!rows || !channels) return hipSuccess;
+    // the run of channels that stays contiguous through the move
+    const size_t run = op == kLayoutPatch? src_channels : channels;
+    const bool vec = run % 4 == 0 && channels % 4 == 0 && src_channels % 4 == 0 && aligned16(src) && aligned16(dst);
+    switch (op) {
+    case kLayoutPatch: return layout_launch<kLayoutPatch>(src,dst,rows,channels,width,src_channels,patch,vec,s);
+    case kLayoutUnpatch: return layout_launch<kLayoutUnpatch>(src,dst,rows,channels,width,src_channels,patch,vec,s);
+    case kLayoutUpsample: return layout_launch<kLayoutUpsample>(src,dst,rows,channels,width,src_channels,patch,vec,s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ---- resample shortcut ----------------------------------------------------
+//
+// Output pixel (x, y) of the resampled width, channel c, with side = 2 when
+// spatial (else 1) and factor = temporal * side * side:
+//   up    source pixel (x/side, y/side), channel (c*factor + (temporal-1)*side*side
+//         + (y % side)*side + x % side) / (channels*factor / src_channels)
+//   down  over the group = src_channels*factor / channels items i = c*group + k,
+//         those whose time index i / (side*side) % temporal is the last add
+//         source pixel (x*side + i % side, y*side + i/side % side), channel
+//         i / factor, to an fp32 running sum in k order; then / group.
+__global__ __launch_bounds__(256) void shortcut_kernel(const float* __restrict__ src, float* __restrict__ dst, size_t out_rows, size_t channels,
+                                                       size_t src_channels, size_t width, size_t side, size_t temporal, bool up)
+{
+    const size_t factor = temporal * side * side, out_width = up? width * side : width / side;
+    const size_t total = out_rows * channels, step = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
+        const size_t c = e % channels, pixel = e / channels, x = pixel % out_width, y = pixel / out_width;
+        float value = 0.0f;
+        if (up) {
+            const size_t repeats = channels * factor / src_channels;
+            const size_t source = (c * factor + (temporal - 1) * side * side + (y % side) * side + x % side) / repeats;
+            value = src[((y / side) * width + x / side) * src_channels + source];
+        } else {
+            const size_t group = src_channels * factor / channels;
+            for (size_t k = 0; k < group; k++) {
+                const size_t item = c * group + k, source = item / factor;
+                const size_t time = item / (side * side) % temporal, dy = item / side % side, dx = item % side;
+                if (time == temporal - 1) value = __fadd_rn(value,src[((y * side + dy) * width + x * side + dx) * src_channels + source]);
+            }
+            value = __fdiv_rn(value,(float)group);
+        }
+        dst[e] = value;
+    }
+}
+
+hipError_t launch_shortcut(const float* src, float* dst, size_t out_rows, size_t channels, size_t src_channels, size_t width, size_t side,
+                           size_t temporal, bool up, hipStream_t s)
+{
+    if (!out_rows || !channels) return hipSuccess;
+    shortcut_kernel<<<dim3(grid_for(out_rows * channels)),dim3(256),0,s>>>(src,dst,out_rows,channels,src_channels,width,side,temporal,up);
+    return hipGetLastError();
+}
+
+}  // namespace pixhip

@@ -160,6 +160,53 @@ class Session:
         return self.lib.pixhip_attention_ranges(self.handle, q_ptr, rows, k_ptr, v_ptr, keys, heads, kv_heads, channels,
                                                 arr, len(ranges), query_offset, out_ptr)
 
+    # ---- the rest of the backend op surface (src/backend_vulkan.h:141-156) ----
+
+    def pointwise_ex(self, op, dst_ptr, second_ptr, third_ptr, rows, channels, part=0, scale=0.0, bias=0.0):
+        """vulkan_pointwise with all its arguments (src/backend_vulkan.cpp:1112-1127)."""
+        return self.lib.pixhip_pointwise_ex(self.handle, op, dst_ptr, second_ptr, third_ptr, rows, channels, part, scale, bias)
+
+    def qwen_modulate(self, dst_ptr, rows, channels, params_ptr, param_channels, target_begin, part, residual_ptr=None):
+        """qwen_image_modulate (src/qwen_image.cpp:149-169)."""
+        return self.lib.pixhip_qwen_modulate(self.handle, dst_ptr, rows, channels, params_ptr, param_channels, target_begin, part,
+                                             residual_ptr)
+
+    def l2norm(self, x_ptr, rows, channels, weight_ptr, eps, out_ptr):
+        """tensor_l2norm (src/tensor.cpp:242-258)."""
+        return self.lib.pixhip_l2norm(self.handle, x_ptr, rows, channels, weight_ptr, eps, out_ptr)
+
+    def groupnorm(self, x_ptr, rows, channels, weight_ptr, bias_ptr, out_ptr):
+        """tensor_groupnorm (src/tensor.cpp:454-485)."""
+        return self.lib.pixhip_groupnorm(self.handle, x_ptr, rows, channels, weight_ptr, bias_ptr, out_ptr)
+
+    def embedding(self, table_ptr, wtype, inner, table_rows, ids, out_ptr):
+        """vulkan_embedding (src/backend_vulkan.cpp:1239-1255); `ids` a sequence of ints."""
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*[int(i) for i in ids])
+        return self.lib.pixhip_embedding(self.handle, table_ptr, wtype, inner, table_rows, arr, len(ids), out_ptr)
+
+    def rows(self, src_ptr, src_rows, dst_ptr, dst_rows, channels, rows, scatter):
+        """tensor_gather / tensor_scatter (src/tensor.cpp:274-302); `rows` a sequence of ints."""
+        arr = (ctypes.c_size_t * max(1, len(rows)))(*[int(r) for r in rows])
+        return self.lib.pixhip_rows(self.handle, src_ptr, src_rows, dst_ptr, dst_rows, channels, arr, len(rows), int(scatter))
+
+    def copy_rows(self, src_ptr, src_rows, src_channels, dst_ptr, dst_rows, dst_channels, rows, src_row=0, src_feature=0, dst_row=0):
+        """vulkan_copy_rows (src/backend_vulkan.cpp:1257-1269)."""
+        return self.lib.pixhip_copy_rows(self.handle, src_ptr, src_rows, src_channels, dst_ptr, dst_rows, dst_channels, rows, src_row,
+                                         src_feature, dst_row)
+
+    def copy_features(self, src_ptr, src_channels, dst_ptr, dst_channels, dst_feature):
+        """vulkan_copy_features (src/backend_vulkan.cpp:1271-1281)."""
+        return self.lib.pixhip_copy_features(self.handle, src_ptr, src_channels, dst_ptr, dst_channels, dst_feature)
+
+    def layout(self, op, src_ptr, src_rows, src_channels, dst_ptr, dst_rows, dst_channels, width, patch=0):
+        """vulkan_layout (src/backend_vulkan.cpp:1283-1295)."""
+        return self.lib.pixhip_layout(self.handle, op, src_ptr, src_rows, src_channels, dst_ptr, dst_rows, dst_channels, width, patch)
+
+    def shortcut(self, src_ptr, width, height, src_channels, dst_ptr, channels, temporal, up, spatial):
+        """tensor_resample_shortcut (src/tensor.cpp:487-527)."""
+        return self.lib.pixhip_shortcut(self.handle, src_ptr, width, height, src_channels, dst_ptr, channels, temporal, int(up),
+                                        int(spatial))
+
     def block_sums(self, weight, x_ptr, columns, sums_ptr, mins_ptr=None):
         return self.lib.pixhip_block_sums(self.handle, weight, x_ptr, columns, sums_ptr, mins_ptr)
 

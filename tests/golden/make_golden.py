@@ -20,6 +20,11 @@ Fixtures (numpy .npz, data only):
   g9_attention.npz      tensor_attention, causal form and ranges form: MHA and
                         grouped heads, head sizes 64 / 72 / 128, causal and
                         not, ranges with a query offset
+  g10_tensor_ops.npz    tensor_l2norm, tensor_groupnorm (group widths 4, 2, 3),
+                        cpu_decode of every type (fp16 specials, random
+                        blocks), tensor_gather / tensor_scatter (repeated rows),
+                        tensor_slice, tensor_upsample, tensor_resample_shortcut
+                        (up and down, spatial or not, one or two time steps)
 
     python tests/golden/make_golden.py g5 g6 g7   # only the named fixtures
 """
@@ -33,8 +38,9 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.dirname(HERE))
 
-from oracle_lib import (Q5_K, Q6_K, Q8_0, add, attention, bias, dot, gelu, norm_rows, quant_matmul, quantize,  # noqa: E402
-                        reference, rope, silu_gate)
+from oracle_lib import (BF16, F16, F32, Q5_K, Q6_K, Q8_0, add, attention, bias, decode_f32, dot, gather,  # noqa: E402
+                        gelu, groupnorm, l2norm, norm_rows, quant_matmul, quantize, reference, rope, scatter, shortcut,
+                        silu_gate, upsample_ref)
 from pixelina_amd import synth  # noqa: E402
 
 
@@ -170,6 +176,90 @@ def write_g9(ref):
     np.savez_compressed(os.path.join(HERE, "g9_attention.npz"), **g)
 
 
+# (width, height, in_channels, channels, temporal, up, spatial)
+G10_SHORTCUTS = [
+    (3, 2, 16, 8, 2, 1, 1),
+    (4, 6, 8, 16, 2, 0, 1),
+    (3, 3, 12, 24, 2, 1, 0),
+    (3, 3, 24, 12, 2, 0, 0),
+    (2, 2, 32, 8, 1, 1, 1),
+    (4, 4, 8, 32, 1, 0, 1),
+]
+
+
+def random_blocks(rng, wtype, nblocks):
+    """Random block bytes with finite fp16 scales (exponent field below 31)."""
+    size, scales = {Q8_0: (34, (0,)), Q5_K: (176, (0, 2)), Q6_K: (210, (208,))}[wtype]
+    b = rng.integers(0, 256, (nblocks, size), dtype=np.uint8)
+    for off in scales:
+        b[:, off + 1] = (b[:, off + 1] & 0x83) | (rng.integers(0, 30, nblocks, dtype=np.uint8) << 2 & 0x7c)
+    return b.reshape(-1)
+
+
+def write_g10(ref):
+    rng = np.random.default_rng(1010)
+    g = {}
+    # l2norm: crafted rows (zero, tiny where epsilon wins, large) and random ones
+    x = (rng.standard_normal((24, 96)) * rng.choice([1e-3, 1.0, 50.0], (24, 1))).astype(np.float32)
+    x[0] = 0.0
+    x[1] = 1e-7
+    x[2, ::2] = -3e4
+    w = (1.0 + 0.2 * rng.standard_normal(96)).astype(np.float32)
+    g["l2_x"], g["l2_w"] = x, w
+    g["l2_eps"] = np.array([1e-12, 0.5], np.float32)
+    g["l2_y0"] = l2norm(ref, "ref", x, None, 1e-12)
+    g["l2_y1"] = l2norm(ref, "ref", x, w, 1e-12)
+    g["l2_y2"] = l2norm(ref, "ref", x, w, 0.5)
+    # groupnorm: group widths 4 (128 channels), 2 (64) and 3 (96)
+    for name, rows, ch in (("gn", 37, 128), ("gn2", 5, 64), ("gn3", 70, 96)):
+        xg = (rng.standard_normal((rows, ch)) * rng.uniform(0.1, 4.0, ch) + rng.uniform(-3, 3, ch)).astype(np.float32)
+        wg = (1.0 + 0.3 * rng.standard_normal(ch)).astype(np.float32)
+        bg = (0.2 * rng.standard_normal(ch)).astype(np.float32)
+        g[f"{name}_x"], g[f"{name}_w"], g[f"{name}_b"] = xg, wg, bg
+        g[f"{name}_y"] = groupnorm(ref, "ref", xg, wg, bg)
+    # decode: every type
+    halves = np.concatenate([np.arange(0, 64, dtype=np.uint16), np.arange(0x7bf0, 0x7c10, dtype=np.uint16),
+                             np.arange(0xfbf8, 0xfc08, dtype=np.uint16), np.array([0x7e00, 0xfe00, 0x7d01, 0x8000, 0x3c00], np.uint16),
+                             rng.integers(0, 65536, 1024, dtype=np.uint64).astype(np.uint16)])
+    g["dec_f16"] = halves.view(np.uint8)
+    g["dec_bf16"] = rng.integers(0, 65536, 1024, dtype=np.uint64).astype(np.uint16).view(np.uint8)
+    g["dec_f32"] = rng.standard_normal(256).astype(np.float32).view(np.uint8)
+    g["dec_q8_0"] = random_blocks(rng, Q8_0, 16)
+    g["dec_q5_K"] = random_blocks(rng, Q5_K, 8)
+    g["dec_q6_K"] = random_blocks(rng, Q6_K, 8)
+    for key, wtype, count in (("f16", F16, halves.size), ("bf16", BF16, 1024), ("f32", F32, 256), ("q8_0", Q8_0, 16 * 32),
+                              ("q5_K", Q5_K, 8 * 256), ("q6_K", Q6_K, 8 * 256)):
+        g[f"dec_{key}_y"] = decode_f32(ref, "ref", g[f"dec_{key}"], wtype, count)
+    # rows: gather with repeats, scatter with a repeated destination row
+    src = rng.standard_normal((9, 12)).astype(np.float32)
+    g["rows_src"] = src
+    g["gather_rows"] = np.array([3, 0, 8, 3, 5], np.uint64)
+    g["gather_y"] = gather(ref, "ref", src, g["gather_rows"])
+    dst = rng.standard_normal((7, 12)).astype(np.float32)
+    g["scatter_dst"] = dst
+    g["scatter_rows"] = np.array([6, 1, 6, 0, 2, 4, 3, 1, 5], np.uint64)
+    g["scatter_y"] = scatter(ref, "ref", dst, src, g["scatter_rows"])
+    # slices (row, rows, feature, channels) of a 10 x 20 tensor
+    xs = rng.standard_normal((10, 20)).astype(np.float32)
+    g["slice_x"] = xs
+    g["slice_cases"] = np.array([[0, 10, 0, 20], [3, 4, 5, 7], [9, 1, 19, 1], [2, 8, 0, 20]], np.int64)
+    for i, (r0, nr, f0, nc) in enumerate(g["slice_cases"]):
+        out = np.full((nr, nc), np.nan, np.float32)
+        assert ref.ref_slice(xs.ctypes.data, 10, 20, int(r0), int(nr), int(f0), int(nc), out.ctypes.data)
+        g[f"slice_y{i}"] = out
+    # upsample 6 x 4 pixels of 8 channels
+    xu = rng.standard_normal((24, 8)).astype(np.float32)
+    g["up_x"], g["up_y"] = xu, upsample_ref(ref, xu, 6, 4)
+    # shortcuts
+    g["sc_cases"] = np.array(G10_SHORTCUTS, np.int64)
+    for i, (wd, ht, cin, ch, t, up, sp) in enumerate(G10_SHORTCUTS):
+        xi = rng.standard_normal((wd * ht, cin)).astype(np.float32)
+        y = shortcut(ref, "ref", xi, wd, ht, ch, t, up, sp)
+        assert y is not None, G10_SHORTCUTS[i]
+        g[f"sc_x{i}"], g[f"sc_y{i}"] = xi, y
+    np.savez_compressed(os.path.join(HERE, "g10_tensor_ops.npz"), **g)
+
+
 def main():
     ref = reference()
     if ref is None:
@@ -184,6 +274,8 @@ def main():
             write_g7(ref)
         if "g9" in only:
             write_g9(ref)
+        if "g10" in only:
+            write_g10(ref)
         return
     rng = np.random.default_rng(20260101)
 
@@ -249,6 +341,7 @@ def main():
     write_g6(ref)
     write_g7(ref)
     write_g9(ref)
+    write_g10(ref)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

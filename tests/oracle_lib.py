@@ -48,6 +48,14 @@ def load_oracle(path):
         "orc_add": (None, [_vp, _vp, _sz]),
         "orc_rope": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _int]),
         "orc_attention": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _vp]),
+        "orc_channel_op": (None, [_int, _vp, _vp, _vp, _sz, _sz, ctypes.c_float, ctypes.c_float]),
+        "orc_qwen_modulate": (_int, [_vp, _sz, _sz, _vp, _sz, _sz, _sz, _vp]),
+        "orc_l2norm": (_int, [_vp, _sz, _sz, _vp, ctypes.c_float, _vp]),
+        "orc_groupnorm": (None, [_vp, _sz, _sz, _vp, _vp, _vp]),
+        "orc_decode_f32": (None, [_vp, _u32, _sz, _vp]),
+        "orc_rows": (_int, [_vp, _sz, _vp, _sz, _sz, _vp, _sz, _int]),
+        "orc_layout": (None, [_int, _vp, _vp, _sz, _sz, _sz, _sz]),
+        "orc_shortcut": (_int, [_vp, _sz, _sz, _sz, _sz, _sz, _int, _int, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -92,6 +100,13 @@ def reference():
             "ref_rope": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _int]),
             "ref_attention": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _int, _vp]),
             "ref_attention_ranges": (_int, [_vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _vp]),
+            "ref_l2norm": (_int, [_vp, _sz, _sz, _vp, ctypes.c_float, _vp]),
+            "ref_groupnorm": (_int, [_vp, _sz, _sz, _vp, _vp, _vp]),
+            "ref_slice": (_int, [_vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+            "ref_gather": (_int, [_vp, _sz, _sz, _vp, _sz, _vp]),
+            "ref_scatter": (_int, [_vp, _sz, _sz, _vp, _vp, _sz]),
+            "ref_upsample": (_int, [_vp, _sz, _sz, _sz, _vp]),
+            "ref_shortcut": (_sz, [_vp, _sz, _sz, _sz, _sz, _sz, _int, _int, _vp, _sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -243,3 +258,111 @@ def q8_K_blocks(blocks):
     qs = b[..., 4:260].view(np.int8)
     bs = b[..., 260:292].copy().view(np.int16)
     return d, qs, bs
+
+
+# ---- the rest of the backend op surface ----
+
+F32, F16, BF16 = 0, 1, 30
+OP_MODULATE, OP_RESIDUAL, OP_AFFINE, OP_EULER = 8, 9, 10, 26
+OP_PATCH, OP_UNPATCH, OP_UPSAMPLE = 15, 16, 17
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def channel_op(lib, op, x, other=None, p=None, scale=0.0, bias=0.0):
+    """orc_channel_op on a copy of x; `p` is the modulation slice [channels]."""
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    o = None if other is None else _f32(other)
+    pp = None if p is None else _f32(p)
+    lib.orc_channel_op(op, ptr(y), None if o is None else ptr(o), None if pp is None else ptr(pp), y.shape[0], y.shape[1], scale, bias)
+    return y
+
+
+def qwen_modulate(lib, x, parameters, target_begin, part, residual=None):
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    pm = _f32(parameters)
+    r = None if residual is None else _f32(residual)
+    ok = lib.orc_qwen_modulate(ptr(y), y.shape[0], y.shape[1], ptr(pm), pm.shape[1], target_begin, part, None if r is None else ptr(r))
+    return y if ok else None
+
+
+def l2norm(lib, prefix, x, weight, eps):
+    x = _f32(x)
+    out = np.full_like(x, np.nan)
+    w = None if weight is None else _f32(weight)
+    ok = getattr(lib, f"{prefix}_l2norm")(ptr(x), x.shape[0], x.shape[1], None if w is None else ptr(w), eps, ptr(out))
+    return out if ok else None
+
+
+def groupnorm(lib, prefix, x, weight, b):
+    x, w, b = _f32(x), _f32(weight), _f32(b)
+    out = np.full_like(x, np.nan)
+    ok = getattr(lib, f"{prefix}_groupnorm")(ptr(x), x.shape[0], x.shape[1], ptr(w), ptr(b), ptr(out))
+    return out if (ok is None or ok) else None
+
+
+def decode_f32(lib, prefix, data, wtype, count):
+    """cpu_decode (prefix "ref") or its restatement ("orc") of `count` values."""
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.full(count, np.nan, np.float32)
+    getattr(lib, "orc_decode_f32" if prefix == "orc" else "ref_decode")(ptr(data), wtype, count, ptr(out))
+    return out
+
+
+def gather(lib, prefix, x, rows):
+    x = _f32(x)
+    r = np.ascontiguousarray(rows, dtype=np.uint64)
+    out = np.full((len(r), x.shape[1]), np.nan, np.float32)
+    if prefix == "ref":
+        ok = lib.ref_gather(ptr(x), x.shape[0], x.shape[1], ptr(r), len(r), ptr(out))
+    else:
+        ok = lib.orc_rows(ptr(x), x.shape[0], ptr(out), len(r), x.shape[1], ptr(r), len(r), 0)
+    return out if ok else None
+
+
+def scatter(lib, prefix, destination, source, rows):
+    d = np.array(destination, dtype=np.float32, copy=True, order="C")
+    src = _f32(source)
+    r = np.ascontiguousarray(rows, dtype=np.uint64)
+    if prefix == "ref":
+        ok = lib.ref_scatter(ptr(d), d.shape[0], d.shape[1], ptr(src), ptr(r), len(r))
+    else:
+        ok = lib.orc_rows(ptr(src), src.shape[0], ptr(d), d.shape[0], d.shape[1], ptr(r), len(r), 1)
+    return d if ok else None
+
+
+def layout(lib, op, x, width, height, channels, patch=1):
+    """orc_layout: op 15 pixels -> tokens, 16 tokens -> pixels, 17 upsample;
+    width, height and channels are the pixel image's."""
+    x = _f32(x)
+    if op == OP_UPSAMPLE:
+        out = np.full((4 * width * height, channels), np.nan, np.float32)
+    elif op == OP_PATCH:
+        out = np.full((width * height // (patch * patch), patch * patch * channels), np.nan, np.float32)
+    else:
+        out = np.full((width * height, channels), np.nan, np.float32)
+    lib.orc_layout(op, ptr(x), ptr(out), width, height, channels, patch)
+    return out
+
+
+def upsample_ref(lib, x, width, height):
+    x = _f32(x)
+    out = np.full((4 * width * height, x.shape[1]), np.nan, np.float32)
+    return out if lib.ref_upsample(ptr(x), width, height, x.shape[1], ptr(out)) else None
+
+
+def shortcut_out_pixels(width, height, up, spatial):
+    side = 2 if spatial else 1
+    return (width * side) * (height * side) if up else (width // side) * (height // side)
+
+
+def shortcut(lib, prefix, x, width, height, channels, temporal, up, spatial):
+    x = _f32(x)
+    out = np.full((shortcut_out_pixels(width, height, up, spatial), channels), np.nan, np.float32)
+    if prefix == "ref":
+        n = lib.ref_shortcut(ptr(x), width, height, x.shape[1], channels, temporal, int(up), int(spatial), ptr(out), out.size)
+        return out if n == out.size else None
+    ok = lib.orc_shortcut(ptr(x), width, height, x.shape[1], channels, temporal, int(up), int(spatial), ptr(out))
+    return out if ok else None

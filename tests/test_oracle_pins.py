@@ -9,8 +9,10 @@ import subprocess
 import numpy as np
 import pytest
 
-from oracle_lib import (ORACLE_DIR, Q5_K, Q6_K, Q8_0, add, attention, bias, dot, gelu, load_oracle, modulate_rows, norm_rows,
-                        oracle, ptr, quant_matmul, quantize, rope, silu_gate)
+from oracle_lib import (BF16, F16, F32, OP_AFFINE, OP_EULER, OP_PATCH, OP_RESIDUAL, OP_UNPATCH, OP_UPSAMPLE, ORACLE_DIR, Q5_K,
+                        Q6_K, Q8_0, add, attention, bias, channel_op, decode_f32, dot, gather, gelu, groupnorm, l2norm, layout,
+                        load_oracle, modulate_rows, norm_rows, oracle, ptr, quant_matmul, quantize, qwen_modulate, rope, scatter,
+                        shortcut, silu_gate)
 from pixelina_amd import synth
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -352,6 +354,20 @@ MUTANTS = {
     14: "modulation by scale instead of 1 + scale",
     15: "attention's grouped heads as head % kv_heads",
     16: "causal attention without the query's own key",
+    17: "l2norm without the sqrt(channels) factor",
+    18: "l2norm adding epsilon instead of taking the larger",
+    19: "groupnorm variance over n - 1",
+    20: "groupnorm weight and bias indexed by group",
+    21: "BF16 decoded as F16",
+    22: "F16 decode keeping the NaN payload",
+    23: "scatter keeping the first of a repeated row",
+    24: "patch layout with dx and dy swapped",
+    25: "upsample reading rows of the doubled width",
+    26: "shortcut (down) without the division by the group",
+    27: "shortcut (up) from the first time step",
+    28: "qwen modulation with the two parameter rows swapped",
+    29: "residual gate without tanh",
+    30: "affine adding the bias before the scale",
 }
 
 
@@ -394,6 +410,82 @@ def golden_mismatches(lib):
         ranges = [tuple(int(x) for x in r) for r in g9[f"c{c}_ranges"]] or None
         got = attention(lib, "orc", g9[f"c{c}_q"], g9[f"c{c}_k"], g9[f"c{c}_v"], heads, kvh, ranges, offset, causal=bool(causal))
         bad += int(got is None or not np.array_equal(got.view(np.uint32), g9[f"c{c}_y"].view(np.uint32)))
+    bad += tensor_ops_mismatches(lib)
+    return bad
+
+
+def tensor_ops_mismatches(lib):
+    """How many of the g10 comparisons (the reference's tensor_l2norm,
+    tensor_groupnorm, cpu_decode, tensor_gather / _scatter, tensor_upsample and
+    tensor_resample_shortcut outputs) an oracle build fails."""
+    g = np.load(os.path.join(GOLDEN, "g10_tensor_ops.npz"))
+
+    def differs(got, want):
+        return int(got is None or not np.array_equal(np.asarray(got, np.float32).view(np.uint32), want.view(np.uint32)))
+    bad = differs(l2norm(lib, "orc", g["l2_x"], None, 1e-12), g["l2_y0"])
+    bad += differs(l2norm(lib, "orc", g["l2_x"], g["l2_w"], 1e-12), g["l2_y1"])
+    bad += differs(l2norm(lib, "orc", g["l2_x"], g["l2_w"], 0.5), g["l2_y2"])
+    for n in ("gn", "gn2", "gn3"):
+        bad += differs(groupnorm(lib, "orc", g[f"{n}_x"], g[f"{n}_w"], g[f"{n}_b"]), g[f"{n}_y"])
+    for key, wtype in (("f16", F16), ("bf16", BF16), ("f32", F32), ("q8_0", Q8_0), ("q5_K", Q5_K), ("q6_K", Q6_K)):
+        want = g[f"dec_{key}_y"]
+        bad += differs(decode_f32(lib, "orc", g[f"dec_{key}"], wtype, want.size), want)
+    bad += differs(gather(lib, "orc", g["rows_src"], g["gather_rows"]), g["gather_y"])
+    bad += differs(scatter(lib, "orc", g["scatter_dst"], g["rows_src"], g["scatter_rows"]), g["scatter_y"])
+    bad += differs(layout(lib, OP_UPSAMPLE, g["up_x"], 6, 4, 8), g["up_y"])
+    for i, (wd, ht, cin, ch, t, up, sp) in enumerate(g["sc_cases"]):
+        bad += differs(shortcut(lib, "orc", g[f"sc_x{i}"], int(wd), int(ht), int(ch), int(t), int(up), int(sp)), g[f"sc_y{i}"])
+    return bad
+
+
+def surface_mismatches(lib):
+    """The ops the reference keeps static or inline, which cannot be linked
+    here (z_residual, src/inference.cpp:279-291; the VAE and sampler affine
+    steps as vulkan_pointwise runs them, :474-476, :612-631; qwen_image_euler
+    and qwen_image_modulate, src/qwen_image.cpp:149-169, :347-361; the DiT patch
+    loops, src/inference.cpp:374-390, :438-455), against what fixes them:
+      residual: gate 0 leaves x; gate 20 (tanhf(20) = 1 in fp32) gives fl(x + o);
+        no gate gives fl(x + o);
+      affine, scale 2 and bias 1: fl(2x + 1) (2x is exact);
+      euler, scale 0.5: fl(x + o/2) (o/2 is exact);
+      qwen modulation, parameter row 0 = 0 and row 1 = s: target rows unchanged,
+        rows before them x * fl(1 + s) rounded once; with a residual and row 0
+        = 20, row 1 = 0: fl(x + r) on target rows, x before them;
+      patch: the reshape of pixels [H, W, C] into [H/p, p, W/p, p, C], axes
+        (0, 2, 1, 3, 4), then tokens; unpatch inverts it.
+    Sums of two fp32 values are formed in float64 (exact here: operands of
+    similar magnitude) and rounded once."""
+    bad = 0
+    rng = np.random.default_rng(29)
+    x = (rng.standard_normal((5, 48)) + 0.5).astype(np.float32)
+    o = rng.standard_normal((5, 48)).astype(np.float32)
+    xd, od = x.astype(np.float64), o.astype(np.float64)
+
+    def same(a, b):
+        return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+    bad += int(not same(channel_op(lib, OP_RESIDUAL, x, o, np.zeros(48, np.float32)), x))
+    bad += int(not same(channel_op(lib, OP_RESIDUAL, x, o, np.full(48, 20.0, np.float32)), (xd + od).astype(np.float32)))
+    bad += int(not same(channel_op(lib, OP_RESIDUAL, x, o, None), (xd + od).astype(np.float32)))
+    bad += int(not same(channel_op(lib, OP_AFFINE, x, scale=2.0, bias=1.0), (2.0 * xd + 1.0).astype(np.float32)))
+    bad += int(not same(channel_op(lib, OP_EULER, x, o, scale=0.5), (xd + 0.5 * od).astype(np.float32)))
+    s = (rng.standard_normal(48) * 0.3).astype(np.float32)
+    params = np.zeros((2, 96), np.float32)
+    params[1, 48:] = s
+    got = qwen_modulate(lib, x, params, 3, 1)
+    one_plus = (1.0 + s.astype(np.float64)).astype(np.float32).astype(np.float64)
+    want = np.concatenate([(xd[:3] * one_plus).astype(np.float32), x[3:]])
+    bad += int(got is None or not same(got, want))
+    params[0, :48], params[1, :48] = 20.0, 0.0
+    got = qwen_modulate(lib, x, params, 2, 0, residual=o)
+    want = np.concatenate([x[:2], (xd[2:] + od[2:]).astype(np.float32)])
+    bad += int(got is None or not same(got, want))
+    bad += int(qwen_modulate(lib, x, params, 2, 2) is not None)  # (part + 1) * channels > parameter channels
+    h, w, c, p = 6, 8, 4, 2
+    img = rng.standard_normal((h * w, c)).astype(np.float32)
+    tokens = img.reshape(h // p, p, w // p, p, c).transpose(0, 2, 1, 3, 4).reshape(h * w // (p * p), p * p * c)
+    got = layout(lib, OP_PATCH, img, w, h, c, p)
+    bad += int(not same(got, tokens))
+    bad += int(not same(layout(lib, OP_UNPATCH, tokens, w, h, c, p), img))
     return bad
 
 
@@ -432,6 +524,10 @@ def test_modulation_closed_forms():
     assert modulation_mismatches(oracle()) == 0
 
 
+def test_surface_closed_forms():
+    assert surface_mismatches(oracle()) == 0
+
+
 @pytest.mark.parametrize("mutant", sorted(MUTANTS))
 def test_golden_vectors_catch_planted_mistake(mutant, tmp_path):
     so = tmp_path / f"liboracle_m{mutant}.so"
@@ -439,4 +535,4 @@ def test_golden_vectors_catch_planted_mistake(mutant, tmp_path):
                     f"-DORC_MUTANT={mutant}", os.path.join(ORACLE_DIR, "pix_oracle.c"), "-o", str(so), "-lm"],
                    check=True, capture_output=True)
     lib = load_oracle(str(so))
-    assert golden_mismatches(lib) + modulation_mismatches(lib) > 0, MUTANTS[mutant]
+    assert golden_mismatches(lib) + modulation_mismatches(lib) + surface_mismatches(lib) > 0, MUTANTS[mutant]

@@ -1,0 +1,164 @@
+"""The oracle's restatement of the rest of the backend op surface
+(oracle/pix_oracle.c: orc_l2norm, orc_groupnorm, orc_decode_f32, orc_rows,
+orc_layout, orc_shortcut, orc_channel_op, orc_qwen_modulate) against the
+reference's own outputs (tests/golden/g10_tensor_ops, written by the compiled
+src/tensor.cpp and src/backend_cpu.cpp), against that compiled code directly on
+fresh random inputs where oracle/_ref was built, and against what the
+mathematics fixes (unit root mean square, per-group zero mean and unit
+variance, the decoders' closed forms from a second numpy decoder)."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle_lib import (BF16, F16, F32, Q5_K, Q6_K, Q8_0, decode_f32, gather, groupnorm, l2norm, oracle, reference, scatter,
+                        shortcut, upsample_ref, layout, OP_UPSAMPLE)
+from test_oracle_pins import q5_K_ints, q6_K_ints, surface_mismatches, tensor_ops_mismatches
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+needs_ref = pytest.mark.skipif(reference() is None, reason="oracle/_ref not built here")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def test_tensor_ops_match_reference_vectors():
+    assert tensor_ops_mismatches(oracle()) == 0
+
+
+def test_unlinkable_ops_closed_forms():
+    assert surface_mismatches(oracle()) == 0
+
+
+def test_l2norm_properties():
+    """y = x * sqrt(C) / |x|: mean square 1 (to fp32 rounding), exact scale
+    invariance by powers of two, the weight applied last, epsilon taking over
+    for rows shorter than it, and epsilon <= 0 rejected."""
+    o = oracle()
+    rng = np.random.default_rng(61)
+    x = (rng.standard_normal((12, 96)) * rng.choice([1e-3, 1.0, 40.0], (12, 1))).astype(np.float32)
+    y = l2norm(o, "orc", x, None, 1e-12).astype(np.float64)
+    assert np.allclose((y * y).mean(axis=1), 1.0, rtol=0, atol=3e-6)
+    assert np.array_equal(bits(l2norm(o, "orc", x * np.float32(8.0), None, 1e-12)), bits(y.astype(np.float32)))
+    w = (1.0 + 0.2 * rng.standard_normal(96)).astype(np.float32)
+    assert np.array_equal(bits(l2norm(o, "orc", x, w, 1e-12)), bits(y.astype(np.float32) * w))
+    tiny = np.full((1, 16), 1e-3, np.float32)  # |x| = 4e-3 < epsilon 0.5: y = x * 4 / 0.5
+    assert np.allclose(l2norm(o, "orc", tiny, None, 0.5), 1e-3 * 4 / 0.5, rtol=1e-6)
+    assert l2norm(o, "orc", x, None, 0.0) is None and l2norm(o, "orc", x, None, -1.0) is None
+
+
+def test_groupnorm_properties():
+    """With weight 1 and bias 0 each of the 32 groups (over all rows) has mean 0
+    and variance 1 - eps/(var + eps) to fp32 rounding; weight and bias act per
+    channel after it; a constant group maps to zero."""
+    o = oracle()
+    rng = np.random.default_rng(62)
+    rows, ch = 50, 128
+    x = (rng.standard_normal((rows, ch)) * rng.uniform(0.5, 3.0, ch) + rng.uniform(-2, 2, ch)).astype(np.float32)
+    x[:, 8:12] = 1.25  # group 2 constant
+    ones, zeros = np.ones(ch, np.float32), np.zeros(ch, np.float32)
+    y = groupnorm(o, "orc", x, ones, zeros).astype(np.float64)
+    for g in range(32):
+        yg = y[:, 4 * g:4 * g + 4]
+        if g == 2:
+            assert not yg.any()
+            continue
+        xg = x[:, 4 * g:4 * g + 4].astype(np.float64)
+        var = xg.var()
+        assert abs(yg.mean()) < 1e-6 and abs(yg.var() - var / (var + 1e-6)) < 2e-6, g
+    w = (1.0 + 0.3 * rng.standard_normal(ch)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(ch)).astype(np.float32)
+    yw = groupnorm(o, "orc", x, w, b)
+    assert np.array_equal(bits(yw), bits(y.astype(np.float32) * w + b))
+
+
+def test_decode_second_decoder():
+    """cpu_decode's values against a numpy decoder of the block formats in
+    float64 (exact: every quantized value is a product of at most 24 bits), and
+    F16 / BF16 against numpy's own conversions (NaN canonical)."""
+    o = oracle()
+    rng = np.random.default_rng(63)
+    g = np.load(os.path.join(GOLDEN, "g10_tensor_ops.npz"))
+    d, dm, sc, mn, q = q5_K_ints(g["dec_q5_K"])
+    want = (d[:, None] * np.repeat(sc, 32, 1) * q - dm[:, None] * np.repeat(mn, 32, 1)).reshape(-1)
+    assert np.array_equal(bits(decode_f32(o, "orc", g["dec_q5_K"], Q5_K, want.size)), bits(want.astype(np.float32)))
+    d6, sc6, q6 = q6_K_ints(g["dec_q6_K"])
+    want = (d6[:, None] * np.repeat(sc6, 16, 1) * q6).reshape(-1)
+    assert np.array_equal(bits(decode_f32(o, "orc", g["dec_q6_K"], Q6_K, want.size)), bits(want.astype(np.float32)))
+    b8 = g["dec_q8_0"].reshape(-1, 34)
+    want = (b8[:, 0:2].copy().view(np.float16).astype(np.float64) * b8[:, 2:].view(np.int8)).reshape(-1)
+    assert np.array_equal(bits(decode_f32(o, "orc", g["dec_q8_0"], Q8_0, want.size)), bits(want.astype(np.float32)))
+    h = rng.integers(0, 65536, 4096, dtype=np.uint64).astype(np.uint16)
+    got = decode_f32(o, "orc", h.view(np.uint8), F16, h.size)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(bits(got[~nan]), bits(ref[~nan]))
+    assert np.array_equal(bits(got[nan]), np.where(h[nan] & 0x8000, 0xffc00000, 0x7fc00000).astype(np.uint32))
+    got = decode_f32(o, "orc", h.view(np.uint8), BF16, h.size)
+    assert np.array_equal(bits(got), h.astype(np.uint32) << 16)
+    f = rng.standard_normal(100).astype(np.float32)
+    assert np.array_equal(bits(decode_f32(o, "orc", f.view(np.uint8), F32, 100)), bits(f))
+
+
+def test_rows_and_layouts_by_indexing():
+    """Gather, scatter (the last copy of a repeated row wins) and upsample
+    against numpy indexing, and the shortcut's two directions against each
+    other: going up and then down again averages `group` copies of one value."""
+    o = oracle()
+    rng = np.random.default_rng(64)
+    x = rng.standard_normal((10, 6)).astype(np.float32)
+    rows = np.array([9, 0, 4, 4, 1], np.uint64)
+    assert np.array_equal(gather(o, "orc", x, rows), x[rows.astype(np.int64)])
+    d = np.zeros((7, 6), np.float32)
+    src = rng.standard_normal((4, 6)).astype(np.float32)
+    got = scatter(o, "orc", d, src, np.array([2, 5, 2, 0], np.uint64))
+    want = d.copy()
+    want[5], want[2], want[0] = src[1], src[2], src[3]
+    assert np.array_equal(got, want)
+    assert gather(o, "orc", x, np.array([10], np.uint64)) is None
+    img = rng.standard_normal((3 * 5, 4)).astype(np.float32)
+    up = layout(o, OP_UPSAMPLE, img, 5, 3, 4).reshape(6, 10, 4)
+    assert np.array_equal(up, img.reshape(3, 5, 4).repeat(2, 0).repeat(2, 1))
+    # 8 -> 32 channels up (2 time steps, 2x2): output channel c of pixel (x, y)
+    # copies input channel (8c + 4 + 2(y % 2) + x % 2) / 32; going down again,
+    # output channel c averages 32 items of which the 16 of the last time step
+    # are all copies of input channel c: exactly half of it
+    small = rng.integers(-8, 8, (2 * 2, 8)).astype(np.float32)
+    wide = shortcut(o, "orc", small, 2, 2, 32, 2, 1, 1)
+    back = shortcut(o, "orc", wide, 4, 4, 8, 2, 0, 1)
+    assert np.array_equal(back, small * np.float32(0.5))
+    assert shortcut(o, "orc", small, 2, 2, 3, 1, 1, 1) is None   # 3 * 4 not a multiple of 8 channels
+    assert shortcut(o, "orc", img, 5, 3, 4, 1, 0, 1) is None      # odd width cannot go down
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [1, 2])
+def test_tensor_ops_equal_compiled_reference(seed):
+    o, r = oracle(), reference()
+    rng = np.random.default_rng(700 + seed)
+    x = (rng.standard_normal((33, 160)) * rng.choice([1e-2, 1.0, 20.0], (33, 1))).astype(np.float32)
+    w = (1.0 + 0.2 * rng.standard_normal(160)).astype(np.float32)
+    for eps, wt in ((1e-12, None), (1e-12, w), (0.3, w)):
+        assert np.array_equal(bits(l2norm(o, "orc", x, wt, eps)), bits(l2norm(r, "ref", x, wt, eps)))
+    for rows, ch in ((33, 160), (300, 128), (7, 32)):
+        xg = (rng.standard_normal((rows, ch)) * 2 + 1).astype(np.float32)
+        wg = rng.standard_normal(ch).astype(np.float32)
+        bg = rng.standard_normal(ch).astype(np.float32)
+        assert np.array_equal(bits(groupnorm(o, "orc", xg, wg, bg)), bits(groupnorm(r, "ref", xg, wg, bg)))
+    from test_oracle_pins import weights
+    from pixelina_amd import synth
+    wq = weights(rng, 3, 512)
+    for wtype, blocks in ((Q5_K, synth.pack_q5_K(wq)), (Q6_K, synth.pack_q6_K(wq))):
+        assert np.array_equal(bits(decode_f32(o, "orc", blocks, wtype, 1536)), bits(decode_f32(r, "ref", blocks, wtype, 1536)))
+    rows = rng.integers(0, 33, 50).astype(np.uint64)
+    assert np.array_equal(gather(o, "orc", x, rows), gather(r, "ref", x, rows))
+    dst = rng.standard_normal((40, 160)).astype(np.float32)
+    rows = rng.integers(0, 40, 33).astype(np.uint64)
+    assert np.array_equal(scatter(o, "orc", dst, x, rows), scatter(r, "ref", dst, x, rows))
+    img = rng.standard_normal((4 * 6, 12)).astype(np.float32)
+    assert np.array_equal(layout(o, OP_UPSAMPLE, img, 6, 4, 12), upsample_ref(r, img, 6, 4))
+    for wd, ht, cin, ch, t, up, sp in ((4, 6, 12, 24, 2, 1, 1), (4, 6, 24, 12, 2, 0, 1), (6, 4, 16, 8, 1, 0, 1), (5, 3, 8, 8, 2, 1, 0)):
+        xi = rng.standard_normal((wd * ht, cin)).astype(np.float32)
+        a, b = shortcut(o, "orc", xi, wd, ht, ch, t, up, sp), shortcut(r, "ref", xi, wd, ht, ch, t, up, sp)
+        assert a is not None and b is not None and np.array_equal(bits(a), bits(b)), (wd, ht, cin, ch, t, up, sp)
