@@ -15,7 +15,9 @@ workloads (`workloads`: a single Q8_0 linear [256, 3840] x [3840, 3840], every
 linear of a Z-Image DiT block at M = 4608 and of a Qwen-Image edit block at
 M = 8448, each linear and the block back to back), the same step with host
 (pinned) operands staged over PCIe, self-attention at the DiT block's shape
-(30 heads of 128 over 4608 tokens), and the reference CPU path
+(30 heads of 128 over 4608 tokens), the rest of the op surface (`surface`:
+norms, layouts and row moves at the models' shapes, against the HBM peak), and
+the reference CPU path
 (cpu_quant_matmul, tensor_attention) timed on this host on the same inputs.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-blocks]
@@ -429,6 +431,75 @@ def cpu_attention(cpu, rec, data):
     log(f"CPU attention: {sec * 1e3:.0f} ms (scaled); GPU vs CPU rel err {err:.2e}")
 
 
+# The rest of the op surface at the models' shapes: (name, workload text).
+# Every case rotates over enough buffer copies (>= 1 GiB) that the 256 MB
+# Infinity Cache cannot serve a repeat, and is priced by its algorithmic HBM
+# bytes (each input read once, each output written once) against 8 TB/s.
+SURFACE_ROTATE_BYTES = 1 << 30
+
+
+def bench_surface(sess, _lib):
+    rng = np.random.default_rng(55)
+    out = {}
+
+    def case(name, text, nbytes, make, min_reps=20):
+        copies = max(1, int(np.ceil(SURFACE_ROTATE_BYTES / nbytes)))
+        sets = [make() for _ in range(copies)]
+        state = {"i": 0}
+
+        def run():
+            bufs, fn = sets[state["i"] % copies]
+            state["i"] += 1
+            fn(bufs)
+
+        ms, n = timed_series(sess, run, min_reps)
+        for bufs, _ in sets:
+            for b in bufs:
+                b.free()
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"workload": text, "us": round(ms * 1e3, 2), "value": round(gbs, 1), "unit": "GB/s", "reps": n,
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / PEAK_HBM_GBS, 4), "work_per_launch": f"{nbytes} bytes"}}
+        log(f"{name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of HBM peak)")
+
+    block = rng.standard_normal(1 << 20).astype(np.float32)
+
+    def dev(shape, scale=1.0):
+        return sess.to_device(np.resize(block * np.float32(scale), shape))
+
+    # z_residual with the gate, DiT activations [4608, 3840]
+    r, c = 4608, 3840
+    case("residual_gated", f"z_residual x[{r},{c}] += o * tanh(gate part 2)", 3 * r * c * 4 + c * 4,
+         lambda: ((dev((r, c)), dev((r, c)), dev((6 * c,), 0.3)),
+                  lambda b: _lib.check(sess.pointwise_ex(9, b[0].ptr, b[1].ptr, b[2].ptr, r, c, 2), "residual")))
+    # qwen_image_modulate, scale form, Qwen-Image edit stream [8448, 3072]
+    r, c = 8448, 3072
+    case("qwen_modulate", f"qwen_image_modulate x[{r},{c}] *= 1 + p (256 text rows on parameter row 1)", 2 * r * c * 4 + 2 * c * 4,
+         lambda: ((dev((r, c)), dev((2, 6 * c), 0.3)),
+                  lambda b: _lib.check(sess.qwen_modulate(b[0].ptr, r, c, b[1].ptr, 6 * c, 256, 1), "qwen modulate")))
+    # tensor_l2norm over the Qwen VAE decoder's full-resolution pixels
+    r, c = 1024 * 1024, 96
+    case("l2norm", f"tensor_l2norm [{r},{c}] (Qwen VAE, 1024x1024 pixels)", 2 * r * c * 4 + c * 4,
+         lambda: ((dev((r, c)), dev((c,)), sess.alloc(r * c * 4)),
+                  lambda b: _lib.check(sess.l2norm(b[0].ptr, r, c, b[1].ptr, 1e-12, b[2].ptr), "l2norm")), min_reps=10)
+    # tensor_groupnorm over the Flux VAE decoder's full-resolution pixels
+    r, c = 1024 * 1024, 128
+    case("groupnorm", f"tensor_groupnorm(32) [{r},{c}] (VAE, 1024x1024 pixels; 3 passes: 2 reads + 1 write)", 2 * r * c * 4 + 2 * c * 4,
+         lambda: ((dev((r, c)), dev((c,)), dev((c,)), sess.alloc(r * c * 4)),
+                  lambda b: _lib.check(sess.groupnorm(b[0].ptr, r, c, b[1].ptr, b[2].ptr, b[3].ptr), "groupnorm")), min_reps=10)
+    # tensor_upsample of the VAE's 512x512 x 128 stage to 1024x1024
+    w, c = 512, 128
+    case("upsample", f"tensor_upsample [{w}x{w},{c}] -> [{2 * w}x{2 * w},{c}]", 5 * w * w * c * 4,
+         lambda: ((dev((w * w, c)), sess.alloc(4 * w * w * c * 4)),
+                  lambda b: _lib.check(sess.layout(17, b[0].ptr, w * w, c, b[1].ptr, 4 * w * w, c, w), "upsample")), min_reps=10)
+    # the DiT's q / k / v split of the fused projection
+    r, c = 4608, 3840
+    case("copy_rows", f"vulkan_copy_rows: k = qkv[{r},{3 * c}][:, {c}:{2 * c}]", 2 * r * c * 4,
+         lambda: ((dev((r, 3 * c)), sess.alloc(r * c * 4)),
+                  lambda b: _lib.check(sess.copy_rows(b[0].ptr, r, 3 * c, b[1].ptr, r, c, r, 0, c, 0), "copy rows")))
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -443,6 +514,7 @@ def main():
     ap.add_argument("--no-blocks", action="store_true", help="skip the single Q8_0 linear and the block workloads")
     ap.add_argument("--no-pcie", action="store_true", help="skip the host-operand (PCIe-inclusive) step")
     ap.add_argument("--no-attention", action="store_true", help="skip the DiT-shape attention")
+    ap.add_argument("--no-surface", action="store_true", help="skip the norms, layouts and row moves")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one plain 512 MiB device copy (the calibration kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -516,6 +588,7 @@ def main():
             yvb.free()
         fused = {} if args.no_fused else bench_fused(sess, synth, _lib, Q5_K, Q8_0, args.steps)
         attention, attn_data = (None, None) if args.no_attention else bench_attention(sess, synth, _lib, args.steps)
+        surface = None if args.no_surface else bench_surface(sess, _lib)
         if args.calibrate_copy:
             src, dst = sess.alloc(COPY_BYTES), sess.alloc(COPY_BYTES)
             sess.copy_device(dst.ptr, src.ptr, COPY_BYTES)
@@ -566,6 +639,8 @@ def main():
         line["fused"] = fused
     if attention:
         line["attention"] = attention
+    if surface:
+        line["surface"] = surface
     if workloads:
         line["workloads"] = workloads
     if pcie:

@@ -36,6 +36,17 @@ unsigned grid_for(size_t work, size_t per_block = 256)
     return (unsigned)std::min<size_t>((work + per_block - 1) / per_block,(size_t)1 << 20);
 }
 
+// Copy-like kernels move kUnroll values per thread per pass, their loads
+// issued together: a block's pass covers kUnroll * 256 consecutive values
+// (value base + u * 256 + thread), so each wave keeps several KB in flight
+// while the block still walks memory in order.
+constexpr int kUnroll = 4;
+
+unsigned grid_unrolled(size_t work)
+{
+    return grid_for((work + kUnroll - 1) / kUnroll);
+}
+
 bool aligned16(const void* p)
 {
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
@@ -104,24 +115,33 @@ __global__ __launch_bounds__(256) void channel_kernel(ChanArgs a)
             f1[j] = tanh_value(a.p1[c0 + j]);
         }
     }
-    const size_t r0 = (size_t)blockIdx.y * kChanRows, r1 = std::min(r0 + kChanRows,a.rows);
-    for (size_t r = r0; r < r1; r++) {
-        const size_t i = r * a.channels + c0;
-        T v = *reinterpret_cast<const T*>(a.x + i);
-        T o{};
-        if constexpr (OP == kOpResidual || OP == kOpEuler || OP == kOpQwenResidual) o = *reinterpret_cast<const T*>(a.other + i);
+    constexpr bool kOther = OP == kOpResidual || OP == kOpEuler || OP == kOpQwenResidual;
+    const size_t r0 = (size_t)blockIdx.y * kChanRows;
+    // every row's loads first (rows past the end re-read the last row), then
+    // the arithmetic and the stores of the rows that exist
+    T v[kChanRows], o[kChanRows];
+#pragma unroll
+    for (int k = 0; k < kChanRows; k++) {
+        const size_t i = std::min(r0 + k,a.rows - 1) * a.channels + c0;
+        v[k] = *reinterpret_cast<const T*>(a.x + i);
+        if constexpr (kOther) o[k] = *reinterpret_cast<const T*>(a.other + i);
+    }
+#pragma unroll
+    for (int k = 0; k < kChanRows; k++) {
+        const size_t r = r0 + k;
+        if (r >= a.rows) break;
         const bool first = r >= a.split;
 #pragma unroll
         for (int j = 0; j < VEC; j++) {
-            const float x = Vec<VEC>::get(v,j), f = first? f0[j] : f1[j];
+            const float x = Vec<VEC>::get(v[k],j), f = first? f0[j] : f1[j];
             float y;
             if constexpr (OP == kOpModulate || OP == kOpQwenScale) y = __fmul_rn(x,f);
-            else if constexpr (OP == kOpResidual || OP == kOpQwenResidual) y = __fadd_rn(x,__fmul_rn(Vec<VEC>::get(o,j),f));
+            else if constexpr (OP == kOpResidual || OP == kOpQwenResidual) y = __fadd_rn(x,__fmul_rn(Vec<VEC>::get(o[k],j),f));
             else if constexpr (OP == kOpAffine) y = __fadd_rn(__fmul_rn(x,a.scale),a.bias);
-            else y = __fadd_rn(x,__fmul_rn(Vec<VEC>::get(o,j),a.scale));
-            Vec<VEC>::set(v,j,y);
+            else y = __fadd_rn(x,__fmul_rn(Vec<VEC>::get(o[k],j),a.scale));
+            Vec<VEC>::set(v[k],j,y);
         }
-        *reinterpret_cast<T*>(a.x + i) = v;
+        *reinterpret_cast<T*>(a.x + r * a.channels + c0) = v[k];
     }
 }
 
@@ -156,50 +176,115 @@ hipError_t launch_channel_op(int op, float* x, const float* other, const float* 
 
 // ---- l2norm ---------------------------------------------------------------
 //
-// One wave per row, four rows per block:
+// A row per segment of L lanes (L a power of two, 64 / L rows per wave, four
+// waves per block), so that short rows (the VAE's 96 channels) keep every
+// lane loading:
 //   square  = sum of (double)x * x
 //   inverse = (float)(sqrt((double)channels) / max(sqrt(square), (double)eps))
 //   y       = x * inverse * w[c]      (fp32, left to right; w NULL: * 1)
-// The second pass re-reads the row, which the first has just brought into L2.
-template <int VEC>
+// Rows of up to kL2Cache units per lane stay in registers between the two
+// passes; longer rows are re-read (from L2, which the first pass filled).
+constexpr int kL2Cache = 8;
+
+template <int VEC, int L>
 __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
                                                      size_t rows, size_t channels, float eps)
 {
     typedef typename Vec<VEC>::T T;
-    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;  // whole waves leave together
-    const int lane = threadIdx.x & 63;
-    const float* in = x + row * channels;
+    const int lane = threadIdx.x & 63, sl = lane % L;
+    const size_t row = ((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / L) + lane / L;
+    const bool valid = row < rows;
+    const size_t units = channels / VEC;
+    // rows past the end read the last row (in bounds) and write nothing: every
+    // lane stays in the segment sums
+    const float* in = x + (valid? row : rows - 1) * channels;
     float* out = y + row * channels;
+    const double floor = (double)eps;
     double sq = 0.0;
-    for (size_t c = (size_t)lane * VEC; c < channels; c += 64 * VEC) {
-        const T v = *reinterpret_cast<const T*>(in + c);
+    if (units <= (size_t)L * kL2Cache) {
+        // the row's units held in registers: loads issued together, one read
+        T v[kL2Cache];
+#pragma unroll
+        for (int k = 0; k < kL2Cache; k++) {
+            const size_t u = sl + (size_t)k * L;
+            if (u < units) {
+                v[k] = *reinterpret_cast<const T*>(in + u * VEC);
+#pragma unroll
+                for (int j = 0; j < VEC; j++) {
+                    const double d = Vec<VEC>::get(v[k],j);
+                    sq += d * d;
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < L; m <<= 1) sq += __shfl_xor(sq,m,64);
+        if (!valid) return;
+        const double root = sqrt(sq);
+        const float inverse = (float)(sqrt((double)channels) / (root < floor? floor : root));
+#pragma unroll
+        for (int k = 0; k < kL2Cache; k++) {
+            const size_t u = sl + (size_t)k * L;
+            if (u < units) {
+#pragma unroll
+                for (int j = 0; j < VEC; j++)
+                    Vec<VEC>::set(v[k],j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v[k],j),inverse),w? w[u * VEC + j] : 1.0f));
+                *reinterpret_cast<T*>(out + u * VEC) = v[k];
+            }
+        }
+        return;
+    }
+#pragma unroll 4
+    for (size_t u = sl; u < units; u += L) {
+        const T v = *reinterpret_cast<const T*>(in + u * VEC);
 #pragma unroll
         for (int j = 0; j < VEC; j++) {
             const double d = Vec<VEC>::get(v,j);
             sq += d * d;
         }
     }
-    sq = wave_sum_f64(sq);
-    const double root = sqrt(sq), floor = (double)eps;
+#pragma unroll
+    for (int m = 1; m < L; m <<= 1) sq += __shfl_xor(sq,m,64);
+    if (!valid) return;
+    const double root = sqrt(sq);
     const float inverse = (float)(sqrt((double)channels) / (root < floor? floor : root));
-    for (size_t c = (size_t)lane * VEC; c < channels; c += 64 * VEC) {
-        T v = *reinterpret_cast<const T*>(in + c);
+#pragma unroll 4
+    for (size_t u = sl; u < units; u += L) {
+        T v = *reinterpret_cast<const T*>(in + u * VEC);
 #pragma unroll
         for (int j = 0; j < VEC; j++)
-            Vec<VEC>::set(v,j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v,j),inverse),w? w[c + j] : 1.0f));
-        *reinterpret_cast<T*>(out + c) = v;
+            Vec<VEC>::set(v,j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v,j),inverse),w? w[u * VEC + j] : 1.0f));
+        *reinterpret_cast<T*>(out + u * VEC) = v;
     }
+}
+
+template <int VEC>
+static hipError_t l2norm_launch(const float* x, const float* w, float* y, size_t rows, size_t channels, float eps, hipStream_t s)
+{
+    // lanes per row: all 64 for long rows, else about four units per lane
+    const size_t units = channels / VEC;
+    int lanes = 64;
+    if (units < 256)
+        for (lanes = 1; lanes * 2 <= 64 && (size_t)lanes * 2 * 4 <= units;) lanes *= 2;
+    const size_t per_block = 4 * (64 / lanes), blocks = (rows + per_block - 1) / per_block;
+    if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+    const dim3 g((unsigned)blocks), b(256);
+    switch (lanes) {
+    case 1: l2norm_kernel<VEC,1><<<g,b,0,s>>>(x,w,y,rows,channels,eps); break;
+    case 2: l2norm_kernel<VEC,2><<<g,b,0,s>>>(x,w,y,rows,channels,eps); break;
+    case 4: l2norm_kernel<VEC,4><<<g,b,0,s>>>(x,w,y,rows,channels,eps); break;
+    case 8: l2norm_kernel<VEC,8><<<g,b,0,s>>>(x,w,y,rows,channels,eps); break;
+    case 16: l2norm_kernel<VEC,16><<<g,b,0,s>>>(x,w,y,rows,channels,eps); break;
+    case 32: l2norm_kernel<VEC,32><<<g,b,0,s>>>(x,w,y,rows,channels,eps); break;
+    default: l2norm_kernel<VEC,64><<<g,b,0,s>>>(x,w,y,rows,channels,eps); break;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_l2norm(const float* x, const float* w, float* y, size_t rows, size_t channels, float eps, hipStream_t s)
 {
     if (!rows || !channels) return hipSuccess;
-    if ((rows + 3) / 4 > 0x7fffffffu) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    if (channels % 4 == 0 && aligned16(x) && aligned16(y)) l2norm_kernel<4><<<grid,block,0,s>>>(x,w,y,rows,channels,eps);
-    else l2norm_kernel<1><<<grid,block,0,s>>>(x,w,y,rows,channels,eps);
-    return hipGetLastError();
+    if (channels % 4 == 0 && aligned16(x) && aligned16(y)) return l2norm_launch<4>(x,w,y,rows,channels,eps,s);
+    return l2norm_launch<1>(x,w,y,rows,channels,eps,s);
 }
 
 // ---- groupnorm ------------------------------------------------------------
@@ -216,13 +301,14 @@ hipError_t launch_l2norm(const float* x, const float* w, float* y, size_t rows, 
 //            no group straddles two tiles) and writes each group's chunk mean
 //            and sum of squared deviations from it (two passes over the
 //            registers, double);
-//   merge    one block per group combines the chunks in a fixed order with the
-//            pairwise update (Chan, Golub and LeVeque): n = na + nb,
-//            d = mb - ma, mean = ma + d * nb / n, M2 = M2a + M2b + d^2 na nb / n;
+//   merge    up to 64 blocks per group, then one, combine the chunks in a
+//            fixed order with the pairwise update (Chan, Golub and LeVeque):
+//            n = na + nb, d = mb - ma, mean = ma + d * nb / n,
+//            M2 = M2a + M2b + d^2 na nb / n;
 //   apply    one pass over x and the output.
 // HBM traffic is two reads and one write of the tensor.
 constexpr int kGroups = 32;
-constexpr int kGnRows = 8;
+constexpr int kGnRows = 16;
 
 // rows x channels in columns of VEC channels (cvec of them); a partial block
 // covers a tile of `lanes` columns and rp * kGnRows rows (one chunk).
@@ -254,15 +340,18 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict
     const size_t valid = std::min<size_t>(sh.rows - row0,(size_t)sh.rp * kGnRows);
     T v[kGnRows];
     double sum = 0.0;
+    if (active) {
+        // all loads first (rows past the end re-read the last row), then the sums
 #pragma unroll
-    for (int k = 0; k < kGnRows; k++) {
-        const size_t r = row0 + ro + (size_t)k * sh.rp;
-        v[k] = T{};
-        if (active && r < sh.rows) {
+        for (int k = 0; k < kGnRows; k++) {
+            const size_t r = std::min<size_t>(row0 + ro + (size_t)k * sh.rp,sh.rows - 1);
             v[k] = *reinterpret_cast<const T*>(x + r * sh.channels + cv * VEC);
-#pragma unroll
-            for (int j = 0; j < VEC; j++) sum += (double)Vec<VEC>::get(v[k],j);
         }
+#pragma unroll
+        for (int k = 0; k < kGnRows; k++)
+            if (row0 + ro + (size_t)k * sh.rp < sh.rows)
+#pragma unroll
+                for (int j = 0; j < VEC; j++) sum += (double)Vec<VEC>::get(v[k],j);
     }
     const int groups = tile_cols / q;
     const double n = (double)valid * (double)sh.gs;
@@ -309,24 +398,46 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict
     }
 }
 
-__global__ __launch_bounds__(256) void gn_merge_kernel(const double* __restrict__ part, GnShape sh, float eps, GnStat* __restrict__ stat)
+// The pairwise update of (n, mean, M2) by another part (nb, mb, qb).
+__device__ __forceinline__ void chan_merge(double& n, double& mean, double& m2, double nb, double mb, double qb)
+{
+    if (nb == 0.0) return;
+    if (n == 0.0) {
+        n = nb;
+        mean = mb;
+        m2 = qb;
+        return;
+    }
+    const double total = n + nb, d = mb - mean;
+    mean += d * (nb / total);
+    m2 += qb + d * d * (n * nb / total);
+    n = total;
+}
+
+// Block (g, s) merges entries [s * per, (s + 1) * per) of group g in a fixed
+// order (each thread a strided run, then a tree over the block): with
+// FROM_CHUNKS the partial kernel's (mean, M2) pairs, n of chunk c being its
+// row count * gs; else (n, mean, M2) triples [32][count] of a first level.
+// With several blocks per group (gridDim.y > 1) the result is a triple in
+// `level`, else the group's statistics.
+constexpr int kGnSplit = 64;  // most first-level merge blocks per group
+
+template <bool FROM_CHUNKS>
+__global__ __launch_bounds__(256) void gn_merge_kernel(const double* __restrict__ in, size_t count, GnShape sh, float eps,
+                                                       double* __restrict__ level, GnStat* __restrict__ stat)
 {
     __shared__ double sn[256], sm[256], s2[256];
     const int g = blockIdx.x, t = threadIdx.x;
+    const size_t per = (count + gridDim.y - 1) / gridDim.y, begin = blockIdx.y * per, end = std::min(begin + per,count);
     const size_t per_chunk = (size_t)sh.rp * kGnRows;
     double n = 0.0, mean = 0.0, m2 = 0.0;
-    for (size_t c = t; c < sh.chunks; c += 256) {
-        const double nb = (double)std::min<size_t>(sh.rows - c * per_chunk,per_chunk) * (double)sh.gs;
-        const double mb = part[(c * kGroups + g) * 2], qb = part[(c * kGroups + g) * 2 + 1];
-        if (n == 0.0) {
-            n = nb;
-            mean = mb;
-            m2 = qb;
+    for (size_t e = begin + t; e < end; e += 256) {
+        if constexpr (FROM_CHUNKS) {
+            const double nb = (double)std::min<size_t>(sh.rows - e * per_chunk,per_chunk) * (double)sh.gs;
+            chan_merge(n,mean,m2,nb,in[(e * kGroups + g) * 2],in[(e * kGroups + g) * 2 + 1]);
         } else {
-            const double total = n + nb, d = mb - mean;
-            mean += d * (nb / total);
-            m2 += qb + d * d * (n * nb / total);
-            n = total;
+            const double* r = in + ((size_t)g * count + e) * 3;
+            chan_merge(n,mean,m2,r[0],r[1],r[2]);
         }
     }
     sn[t] = n;
@@ -334,26 +445,27 @@ __global__ __launch_bounds__(256) void gn_merge_kernel(const double* __restrict_
     s2[t] = m2;
     __syncthreads();
     for (int stride = 128; stride > 0; stride >>= 1) {
-        if (t < stride && sn[t + stride] != 0.0) {
-            const double na = sn[t], nb = sn[t + stride];
-            if (na == 0.0) {
-                sn[t] = nb;
-                sm[t] = sm[t + stride];
-                s2[t] = s2[t + stride];
-            } else {
-                const double total = na + nb, d = sm[t + stride] - sm[t];
-                sm[t] += d * (nb / total);
-                s2[t] += s2[t + stride] + d * d * (na * nb / total);
-                sn[t] = total;
-            }
+        if (t < stride) {
+            double a = sn[t], b = sm[t], c = s2[t];
+            chan_merge(a,b,c,sn[t + stride],sm[t + stride],s2[t + stride]);
+            sn[t] = a;
+            sm[t] = b;
+            s2[t] = c;
         }
         __syncthreads();
     }
     if (t == 0) {
-        const double count = (double)sh.rows * (double)sh.gs;
-        stat[g].mean = sm[0];
-        stat[g].inverse = (float)(1.0 / sqrt(s2[0] / count + (double)eps));
-        stat[g].pad = 0.0f;
+        if (gridDim.y > 1) {
+            double* r = level + ((size_t)g * gridDim.y + blockIdx.y) * 3;
+            r[0] = sn[0];
+            r[1] = sm[0];
+            r[2] = s2[0];
+        } else {
+            const double total = (double)sh.rows * (double)sh.gs;
+            stat[g].mean = sm[0];
+            stat[g].inverse = (float)(1.0 / sqrt(s2[0] / total + (double)eps));
+            stat[g].pad = 0.0f;
+        }
     }
 }
 
@@ -365,17 +477,25 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(const float* __restrict__
     __shared__ GnStat st[kGroups];
     if (threadIdx.x < kGroups) st[threadIdx.x] = stat[threadIdx.x];
     __syncthreads();
-    const size_t total = sh.rows * sh.cvec, stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        const size_t cv = e % sh.cvec, c = cv * VEC;
-        const GnStat gs = st[c / sh.gs];
-        T v = *reinterpret_cast<const T*>(x + e * VEC);
+    const size_t total = sh.rows * sh.cvec;
+    for (size_t base = (size_t)blockIdx.x * blockDim.x * kUnroll + threadIdx.x; base < total; base += (size_t)gridDim.x * blockDim.x * kUnroll) {
+        T v[kUnroll];
 #pragma unroll
-        for (int j = 0; j < VEC; j++) {
-            const float d = (float)((double)Vec<VEC>::get(v,j) - gs.mean);
-            Vec<VEC>::set(v,j,__fadd_rn(__fmul_rn(__fmul_rn(d,gs.inverse),w[c + j]),b[c + j]));
+        for (int k = 0; k < kUnroll; k++)
+            if (base + k * (size_t)blockDim.x < total) v[k] = *reinterpret_cast<const T*>(x + (base + k * (size_t)blockDim.x) * VEC);
+#pragma unroll
+        for (int k = 0; k < kUnroll; k++) {
+            const size_t e = base + k * (size_t)blockDim.x;
+            if (e >= total) break;
+            const size_t c = (e % sh.cvec) * VEC;
+            const GnStat gs = st[c / sh.gs];
+#pragma unroll
+            for (int j = 0; j < VEC; j++) {
+                const float d = (float)((double)Vec<VEC>::get(v[k],j) - gs.mean);
+                Vec<VEC>::set(v[k],j,__fadd_rn(__fmul_rn(__fmul_rn(d,gs.inverse),w[c + j]),b[c + j]));
+            }
+            *reinterpret_cast<T*>(y + e * VEC) = v[k];
         }
-        *reinterpret_cast<T*>(y + e * VEC) = v;
     }
 }
 
@@ -397,15 +517,16 @@ bool groupnorm_shape(size_t rows, size_t channels, bool vec, GnShape* sh)
     return sh->chunks <= 0x7fffffffu && sh->tiles <= 65535;
 }
 
-// Workspace: the 32 group statistics, then [chunks][32] (mean, M2) pairs for
-// the larger chunk count of the two column widths.
+// Workspace: the 32 group statistics, the first merge level's [32][64]
+// triples, then [chunks][32] (mean, M2) pairs for the larger chunk count of
+// the two column widths.
 size_t groupnorm_workspace_bytes(size_t rows, size_t channels)
 {
     GnShape scalar{}, vec{};
     if (!groupnorm_shape(rows,channels,false,&scalar)) return 0;
     size_t chunks = scalar.chunks;
     if (groupnorm_shape(rows,channels,true,&vec)) chunks = std::max(chunks,vec.chunks);
-    return kGroups * sizeof(GnStat) + chunks * kGroups * 2 * sizeof(double);
+    return kGroups * sizeof(GnStat) + (kGroups * kGnSplit * 3 + chunks * kGroups * 2) * sizeof(double);
 }
 
 hipError_t launch_groupnorm(const float* x, const float* w, const float* b, float* y, size_t rows, size_t channels, float eps,
@@ -415,12 +536,16 @@ hipError_t launch_groupnorm(const float* x, const float* w, const float* b, floa
     GnShape sh{};
     if (!groupnorm_shape(rows,channels,vec,&sh)) return hipErrorInvalidValue;
     GnStat* stat = static_cast<GnStat*>(workspace);
-    double* part = reinterpret_cast<double*>(stat + kGroups);
+    double* level = reinterpret_cast<double*>(stat + kGroups);
+    double* part = level + kGroups * kGnSplit * 3;
     const dim3 pgrid((unsigned)sh.chunks,(unsigned)sh.tiles), block(256);
     if (vec) gn_partial_kernel<4><<<pgrid,block,0,s>>>(x,sh,part);
     else gn_partial_kernel<1><<<pgrid,block,0,s>>>(x,sh,part);
-    gn_merge_kernel<<<dim3(kGroups),block,0,s>>>(part,sh,eps,stat);
-    const unsigned agrid = grid_for(rows * sh.cvec);
+    // at least 1024 chunks per first-level block
+    const unsigned split = (unsigned)std::min<size_t>(kGnSplit,std::max<size_t>(1,(sh.chunks + 1023) / 1024));
+    gn_merge_kernel<true><<<dim3(kGroups,split),block,0,s>>>(part,sh.chunks,sh,eps,level,stat);
+    if (split > 1) gn_merge_kernel<false><<<dim3(kGroups,1),block,0,s>>>(level,split,sh,eps,nullptr,stat);
+    const unsigned agrid = grid_unrolled(rows * sh.cvec);
     if (vec) gn_apply_kernel<4><<<dim3(agrid),block,0,s>>>(x,sh,stat,w,b,y);
     else gn_apply_kernel<1><<<dim3(agrid),block,0,s>>>(x,sh,stat,w,b,y);
     return hipGetLastError();
@@ -521,55 +646,59 @@ hipError_t launch_decode_rows(const void* table, uint32_t type, size_t stride, c
 
 // ---- row moves ------------------------------------------------------------
 //
-// rows: destination row dst_rows[k] (NULL: k) = source row src_rows[k] (NULL:
-// k), k < n, `cvec` columns of VEC floats.  copy2d: `rows` rows of cvec
-// columns between two row strides (in floats).
+// Destination row dst_rows[k] (NULL: k) = source row src_rows[k] (NULL: k),
+// k < n, `cvec` columns of VEC floats, rows `src_stride` / `dst_stride` floats
+// apart.  A block moves kMoveRows rows of 256 columns (column blockIdx.x * 256
+// + thread), all its loads issued before the stores, and strides over the
+// rows in y.
+constexpr int kMoveRows = 4;
+
 template <int VEC>
-__global__ __launch_bounds__(256) void rows_kernel(const float* __restrict__ src, float* __restrict__ dst, const uint64_t* __restrict__ src_rows,
-                                                   const uint64_t* __restrict__ dst_rows, size_t n, size_t cvec)
+__global__ __launch_bounds__(256) void move_rows_kernel(const float* __restrict__ src, size_t src_stride, float* __restrict__ dst,
+                                                        size_t dst_stride, const uint64_t* __restrict__ src_rows,
+                                                        const uint64_t* __restrict__ dst_rows, size_t n, size_t cvec)
 {
     typedef typename Vec<VEC>::T T;
-    const size_t total = n * cvec, step = (size_t)gridDim.x * blockDim.x;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
-        const size_t k = e / cvec, j = e % cvec;
-        const size_t sr = src_rows? src_rows[k] : k, dr = dst_rows? dst_rows[k] : k;
-        reinterpret_cast<T*>(dst)[dr * cvec + j] = reinterpret_cast<const T*>(src)[sr * cvec + j];
+    const size_t j = ((size_t)blockIdx.x * 256 + threadIdx.x) * VEC;
+    if (j >= cvec * VEC) return;
+    for (size_t r0 = (size_t)blockIdx.y * kMoveRows; r0 < n; r0 += (size_t)gridDim.y * kMoveRows) {
+        T v[kMoveRows];
+#pragma unroll
+        for (int u = 0; u < kMoveRows; u++) {
+            const size_t k = std::min(r0 + u,n - 1);
+            v[u] = *reinterpret_cast<const T*>(src + (src_rows? src_rows[k] : k) * src_stride + j);
+        }
+#pragma unroll
+        for (int u = 0; u < kMoveRows; u++) {
+            const size_t k = r0 + u;
+            if (k >= n) break;
+            *reinterpret_cast<T*>(dst + (dst_rows? dst_rows[k] : k) * dst_stride + j) = v[u];
+        }
     }
+}
+
+static hipError_t move_rows(const float* src, size_t src_stride, float* dst, size_t dst_stride, const uint64_t* src_rows,
+                            const uint64_t* dst_rows, size_t n, size_t columns, hipStream_t s)
+{
+    if (!n || !columns) return hipSuccess;
+    const bool vec = columns % 4 == 0 && src_stride % 4 == 0 && dst_stride % 4 == 0 && aligned16(src) && aligned16(dst);
+    const size_t cvec = vec? columns / 4 : columns;
+    if ((cvec + 255) / 256 > 0x7fffffffu) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((cvec + 255) / 256),(unsigned)std::min<size_t>((n + kMoveRows - 1) / kMoveRows,65535)), b(256);
+    if (vec) move_rows_kernel<4><<<g,b,0,s>>>(src,src_stride,dst,dst_stride,src_rows,dst_rows,n,cvec);
+    else move_rows_kernel<1><<<g,b,0,s>>>(src,src_stride,dst,dst_stride,src_rows,dst_rows,n,cvec);
+    return hipGetLastError();
 }
 
 hipError_t launch_rows(const float* src, float* dst, const uint64_t* src_rows, const uint64_t* dst_rows, size_t n, size_t channels,
                        hipStream_t s)
 {
-    if (!n || !channels) return hipSuccess;
-    const bool vec = channels % 4 == 0 && aligned16(src) && aligned16(dst);
-    const size_t cvec = vec? channels / 4 : channels;
-    const dim3 g(grid_for(n * cvec)), b(256);
-    if (vec) rows_kernel<4><<<g,b,0,s>>>(src,dst,src_rows,dst_rows,n,cvec);
-    else rows_kernel<1><<<g,b,0,s>>>(src,dst,src_rows,dst_rows,n,cvec);
-    return hipGetLastError();
-}
-
-template <int VEC>
-__global__ __launch_bounds__(256) void copy2d_kernel(const float* __restrict__ src, size_t src_stride, float* __restrict__ dst,
-                                                     size_t dst_stride, size_t rows, size_t cvec)
-{
-    typedef typename Vec<VEC>::T T;
-    const size_t total = rows * cvec, step = (size_t)gridDim.x * blockDim.x;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
-        const size_t r = e / cvec, j = e % cvec;
-        *reinterpret_cast<T*>(dst + r * dst_stride + j * VEC) = *reinterpret_cast<const T*>(src + r * src_stride + j * VEC);
-    }
+    return move_rows(src,channels,dst,channels,src_rows,dst_rows,n,channels,s);
 }
 
 hipError_t launch_copy2d(const float* src, size_t src_stride, float* dst, size_t dst_stride, size_t rows, size_t columns, hipStream_t s)
 {
-    if (!rows || !columns) return hipSuccess;
-    const bool vec = columns % 4 == 0 && src_stride % 4 == 0 && dst_stride % 4 == 0 && aligned16(src) && aligned16(dst);
-    const size_t cvec = vec? columns / 4 : columns;
-    const dim3 g(grid_for(rows * cvec)), b(256);
-    if (vec) copy2d_kernel<4><<<g,b,0,s>>>(src,src_stride,dst,dst_stride,rows,cvec);
-    else copy2d_kernel<1><<<g,b,0,s>>>(src,src_stride,dst,dst_stride,rows,cvec);
-    return hipGetLastError();
+    return move_rows(src,src_stride,dst,dst_stride,nullptr,nullptr,rows,columns,s);
 }
 
 // ---- layout ---------------------------------------------------------------
@@ -584,28 +713,28 @@ hipError_t launch_copy2d(const float* src, size_t src_stride, float* dst, size_t
 //            (y/p)*(W/p) + x/p, feature ((y % p)*p + x % p)*C + c
 //   UPSAMPLE dst [ 4*W*H ][ C ]: pixel (x, y) of width 2W -> (x/2, y/2)
 // (W the source width for PATCH and UPSAMPLE, the destination width for UNPATCH.)
-template <int OP, int VEC>
-__global__ __launch_bounds__(256) void layout_kernel(const float* __restrict__ src, float* __restrict__ dst, size_t rows, size_t channels,
-                                                     size_t width, size_t src_channels, size_t patch)
+template <int OP, int VEC, typename I>
+__global__ __launch_bounds__(256) void layout_kernel(const float* __restrict__ src, float* __restrict__ dst, I rows, I channels, I width,
+                                                     I src_channels, I patch)
 {
     typedef typename Vec<VEC>::T T;
-    const size_t cvec = channels / VEC, total = rows * cvec, step = (size_t)gridDim.x * blockDim.x;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
-        const size_t row = e / cvec, f = (e % cvec) * VEC;
-        size_t from;
+    const I cvec = channels / VEC, total = rows * cvec, step = (I)gridDim.x * blockDim.x;
+    for (I e = (I)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
+        const I row = e / cvec, f = (e % cvec) * VEC;
+        I from;
         if constexpr (OP == kLayoutPatch) {
-            const size_t pw = width / patch, pixel = f / src_channels;
-            const size_t x = (row % pw) * patch + pixel % patch, y = (row / pw) * patch + pixel / patch;
+            const I pw = width / patch, pixel = f / src_channels;
+            const I x = (row % pw) * patch + pixel % patch, y = (row / pw) * patch + pixel / patch;
             from = (y * width + x) * src_channels + f % src_channels;
         } else if constexpr (OP == kLayoutUnpatch) {
-            const size_t x = row % width, y = row / width;
-            const size_t token = (y / patch) * (width / patch) + x / patch;
+            const I x = row % width, y = row / width;
+            const I token = (y / patch) * (width / patch) + x / patch;
             from = token * src_channels + ((y % patch) * patch + x % patch) * channels + f;
         } else {
-            const size_t x = row % (width * 2), y = row / (width * 2);
+            const I x = row % (width * 2), y = row / (width * 2);
             from = ((y / 2) * width + x / 2) * channels + f;
         }
-        *reinterpret_cast<T*>(dst + row * channels + f) = *reinterpret_cast<const T*>(src + from);
+        *reinterpret_cast<T*>(dst + (size_t)e * VEC) = *reinterpret_cast<const T*>(src + from);
     }
 }
 
@@ -614,8 +743,20 @@ static hipError_t layout_launch(const float* src, float* dst, size_t rows, size_
                                 bool vec, hipStream_t s)
 {
     const dim3 g(grid_for(rows * (vec? channels / 4 : channels))), b(256);
-    if (vec) layout_kernel<OP,4><<<g,b,0,s>>>(src,dst,rows,channels,width,src_channels,patch);
-    else layout_kernel<OP,1><<<g,b,0,s>>>(src,dst,rows,channels,width,src_channels,patch);
+    // 32-bit index arithmetic when every index fits, the loop's last step
+    // included (the grid is at most 2^28 threads): the destination holds the
+    // most values (the source as many, or a quarter for UPSAMPLE)
+    const bool narrow = rows * channels < (1ull << 31);
+    if (vec && narrow)
+        layout_kernel<OP,4,uint32_t><<<g,b,0,s>>>(src,dst,(uint32_t)rows,(uint32_t)channels,(uint32_t)width,(uint32_t)src_channels,
+                                                  (uint32_t)patch);
+    else if (vec)
+        layout_kernel<OP,4,size_t><<<g,b,0,s>>>(src,dst,rows,channels,width,src_channels,patch);
+    else if (narrow)
+        layout_kernel<OP,1,uint32_t><<<g,b,0,s>>>(src,dst,(uint32_t)rows,(uint32_t)channels,(uint32_t)width,(uint32_t)src_channels,
+                                                  (uint32_t)patch);
+    else
+        layout_kernel<OP,1,size_t><<<g,b,0,s>>>(src,dst,rows,channels,width,src_channels,patch);
     return hipGetLastError();
 }
 
