@@ -265,6 +265,75 @@ bool hip_attention(const float* q, size_t rows, const float* k, const float* v, 
     return s && pixhip_attention_ranges(s,q,rows,k,v,keys,heads,kv_heads,channels,ranges,count,query_offset,output) == PIXHIP_OK;
 }
 
+bool hip_pointwise_ex(unsigned operation, float* destination, const float* second, const float* third, size_t rows, size_t channels,
+                      unsigned part, float scale, float bias)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_pointwise_ex(s,operation,destination,second,third,rows,channels,part,scale,bias) == PIXHIP_OK;
+}
+
+bool hip_qwen_modulate(float* destination, size_t rows, size_t channels, const float* parameters, size_t parameter_channels,
+                       size_t target_begin, size_t part, const float* residual)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_qwen_modulate(s,destination,rows,channels,parameters,parameter_channels,target_begin,part,residual) == PIXHIP_OK;
+}
+
+bool hip_l2norm(const float* input, size_t rows, size_t channels, const float* weight, float epsilon, float* output)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_l2norm(s,input,rows,channels,weight,epsilon,output) == PIXHIP_OK;
+}
+
+bool hip_groupnorm(const float* input, size_t rows, size_t channels, const float* weight, const float* bias, float* output)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_groupnorm(s,input,rows,channels,weight,bias,output) == PIXHIP_OK;
+}
+
+bool hip_embedding(const void* table, uint32_t type, uint64_t inner, uint64_t table_rows, const int32_t* ids, size_t count, float* output)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_embedding(s,table,type,inner,table_rows,ids,count,output) == PIXHIP_OK;
+}
+
+bool hip_rows(const float* source, size_t source_rows, float* destination, size_t destination_rows, size_t channels, const size_t* rows,
+              size_t count, bool scatter)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_rows(s,source,source_rows,destination,destination_rows,channels,rows,count,scatter? 1 : 0) == PIXHIP_OK;
+}
+
+bool hip_copy_rows(const float* source, size_t source_rows, size_t source_channels, float* destination, size_t destination_rows,
+                   size_t destination_channels, size_t rows, size_t source_row, size_t source_feature, size_t destination_row)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_copy_rows(s,source,source_rows,source_channels,destination,destination_rows,destination_channels,rows,source_row,
+                                 source_feature,destination_row) == PIXHIP_OK;
+}
+
+bool hip_copy_features(const float* source, size_t source_channels, float* destination, size_t destination_channels,
+                       size_t destination_feature)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_copy_features(s,source,source_channels,destination,destination_channels,destination_feature) == PIXHIP_OK;
+}
+
+bool hip_layout(unsigned operation, const float* source, size_t source_rows, size_t source_channels, float* destination,
+                size_t destination_rows, size_t destination_channels, size_t width, size_t patch)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_layout(s,operation,source,source_rows,source_channels,destination,destination_rows,destination_channels,width,
+                              patch) == PIXHIP_OK;
+}
+
+bool hip_shortcut(const float* source, size_t width, size_t height, size_t source_channels, float* destination, size_t channels,
+                  size_t temporal, bool up, bool spatial)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && pixhip_shortcut(s,source,width,height,source_channels,destination,channels,temporal,up? 1 : 0,spatial? 1 : 0) == PIXHIP_OK;
+}
+
 bool hip_available(std::string &description)
 {
     HipSession session;

@@ -156,6 +156,30 @@ bool hip_attention(const float* q, size_t rows, const float* k, const float* v, 
 bool hip_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
                    size_t channels, const pixhip_attention_range* ranges, size_t count, size_t query_offset, float* output);
 
+// The rest of vulkan_*'s op surface (src/backend_vulkan.h:141-156) on the
+// active session, each the pixhip_ entry point of the same name over the
+// tensors' value pointers (PixTensorVals under a session; pageable vectors are
+// staged).  False (with pixhip_last_error) on what the backend rejects, so the
+// caller falls back to its CPU code.
+bool hip_pointwise_ex(unsigned operation, float* destination, const float* second, const float* third, size_t rows, size_t channels,
+                      unsigned part, float scale, float bias);
+bool hip_qwen_modulate(float* destination, size_t rows, size_t channels, const float* parameters, size_t parameter_channels,
+                       size_t target_begin, size_t part, const float* residual);
+bool hip_l2norm(const float* input, size_t rows, size_t channels, const float* weight, float epsilon, float* output);
+bool hip_groupnorm(const float* input, size_t rows, size_t channels, const float* weight, const float* bias, float* output);
+bool hip_embedding(const void* table, uint32_t type, uint64_t inner, uint64_t table_rows, const int32_t* ids, size_t count,
+                   float* output);
+bool hip_rows(const float* source, size_t source_rows, float* destination, size_t destination_rows, size_t channels, const size_t* rows,
+              size_t count, bool scatter);
+bool hip_copy_rows(const float* source, size_t source_rows, size_t source_channels, float* destination, size_t destination_rows,
+                   size_t destination_channels, size_t rows, size_t source_row, size_t source_feature, size_t destination_row);
+bool hip_copy_features(const float* source, size_t source_channels, float* destination, size_t destination_channels,
+                       size_t destination_feature);
+bool hip_layout(unsigned operation, const float* source, size_t source_rows, size_t source_channels, float* destination,
+                size_t destination_rows, size_t destination_channels, size_t width, size_t patch);
+bool hip_shortcut(const float* source, size_t width, size_t height, size_t source_channels, float* destination, size_t channels,
+                  size_t temporal, bool up, bool spatial);
+
 bool hip_available(std::string &description);
 
 #endif /* PIXELINA_BACKEND_HIP_H */

@@ -20,7 +20,11 @@
 // the gated product [M][F]; RoPE of X with K/64 heads of 64 (hip_rope, split
 // halves) [M][K]; Y + bias (hip_pointwise BIAS) [M][N]; self-attention of X
 // with K/64 heads of 64 (hip_attention), causal [M][K], then in the ranges form
-// with rows [0, M/2) seeing every key and [M/2, M) causal [M][K].
+// with rows [0, M/2) seeing every key and [M/2, M) causal [M][K]; tensor_l2norm
+// of X with the norm weight (hip_l2norm, epsilon 1e-12) [M][K];
+// tensor_groupnorm of X with the norm weight and the modulation as bias
+// (hip_groupnorm) [M][K]; the rows of X in reverse order gathered from the
+// std::vector<size_t> (hip_rows) [M][K].
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -128,13 +132,21 @@ int main(int argc, char** argv)
         if (!hip_attention(x.data(),M,x.data(),x.data(),M,K / 64,K / 64,K,true,att.data())) return fail("hip_attention");
         const pixhip_attention_range ranges[2] = {{0,M / 2,M,0},{M / 2,M,M,1}};
         if (!hip_attention(x.data(),M,x.data(),x.data(),M,K / 64,K / 64,K,ranges,2,0,att2.data())) return fail("hip_attention(ranges)");
+        // tensor_l2norm / tensor_groupnorm / tensor_gather with the reference's vectors
+        Vals<float> l2(M * K), gn(M * K), gathered(M * K);
+        if (!hip_l2norm(x.data(),M,K,norm_weight.data(),1e-12f,l2.data())) return fail("hip_l2norm");
+        if (!hip_groupnorm(x.data(),M,K,norm_weight.data(),modulation.data(),gn.data())) return fail("hip_groupnorm");
+        std::vector<size_t> reversed(M);
+        for (size_t i = 0; i < M; i++) reversed[i] = M - 1 - i;
+        if (!hip_rows(x.data(),M,gathered.data(),M,K,reversed.data(),M,false)) return fail("hip_rows");
         if (!hip_synchronize()) return fail("hip_synchronize");
 
         FILE* out = std::fopen(argv[2],"wb");
         if (!out) return fail("cannot open output");
         const bool ok = write_floats(out,y) && write_floats(out,y1) && write_floats(out,y2) && write_floats(out,normalized) &&
                         write_floats(out,d) && write_floats(out,gated) && write_floats(out,roped) && write_floats(out,biased) &&
-                        write_floats(out,att) && write_floats(out,att2);
+                        write_floats(out,att) && write_floats(out,att2) && write_floats(out,l2) && write_floats(out,gn) &&
+                        write_floats(out,gathered);
         std::fclose(out);
         if (!ok) return fail("short write");
     }

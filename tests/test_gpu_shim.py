@@ -6,7 +6,8 @@ model-file / weight pair shaped like PixModelFile / PixWeight, and the calls of
 tensor_linear (hip_matmul), of the DiT block's FFN (hip_norm_multiply for
 the gate and up linears, hip_silu_gate_multiply for the down linear), and of
 tensor_rope / tensor_bias (hip_rope, hip_pointwise) with their tables in
-pageable std::vector memory, which the library stages to the device.
+pageable std::vector memory, which the library stages to the device, and of
+tensor_attention, tensor_l2norm, tensor_groupnorm and tensor_gather.
 
 Against the oracle: the normalized input bit-exact; the SiLU product within 4
 ulps (the reference's glibc expf is not correctly rounded; this one is); every
@@ -19,7 +20,8 @@ import numpy as np
 import pytest
 
 from gpu_helpers import TOL, row_rel_error
-from oracle_lib import Q5_K, Q8_0, attention, bias, modulate_rows, norm_rows, oracle, quant_matmul, quantize, rope, silu_gate
+from oracle_lib import (Q5_K, Q8_0, attention, bias, groupnorm, l2norm, modulate_rows, norm_rows, oracle, quant_matmul, quantize, rope,
+                        silu_gate)
 from pixelina_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -56,9 +58,14 @@ def test_shim_matmul_norm_and_gate(tmp_path):
     proc = subprocess.run([SHIM_CHECK, str(src), str(dst)], capture_output=True, text=True, timeout=120)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     out = np.fromfile(dst, np.float32)
-    sizes = [m * n, m * n, m * n, m * k, m * k, m * f, m * k, m * n, m * k, m * k]
+    sizes = [m * n, m * n, m * n, m * k, m * k, m * f, m * k, m * n, m * k, m * k, m * k, m * k, m * k]
     assert out.size == sum(sizes)
-    y, y1, y2, normalized, d, gated, roped, biased, att, att2 = np.split(out, np.cumsum(sizes)[:-1])
+    y, y1, y2, normalized, d, gated, roped, biased, att, att2, l2, gn, gathered = np.split(out, np.cumsum(sizes)[:-1])
+
+    # hip_l2norm / hip_groupnorm / hip_rows with pageable vectors: bit-exact
+    assert np.array_equal(l2.reshape(m, k).view(np.uint32), l2norm(o, "orc", x, nw, 1e-12).view(np.uint32))
+    assert np.array_equal(gn.reshape(m, k).view(np.uint32), groupnorm(o, "orc", x, nw, mod).view(np.uint32))
+    assert np.array_equal(gathered.reshape(m, k), x[::-1])
 
     # hip_attention, both forms, against the oracle's tensor_attention
     h = k // 64
