@@ -32,6 +32,8 @@ extern "C" {
 #define PIXHIP_ERR_MEMORY (-3)      /* device allocation failed or exceeds the budget (src/backend_vulkan.cpp:689, :718-720) */
 #define PIXHIP_ERR_DEVICE (-4)      /* HIP runtime failure: no device, launch or synchronisation error */
 #define PIXHIP_ERR_STATE (-5)       /* missing session, MULTIPLY without matching activations, or an evicted weight without host bytes */
+#define PIXHIP_ERR_OPEN (-6)        /* the model file cannot be opened or mapped (MODEL_ERROR_OPEN, src/model.h:16) */
+#define PIXHIP_ERR_FORMAT (-7)      /* not a GGUF v3 / safetensors file the reader accepts (MODEL_ERROR_FORMAT, src/model.h:17) */
 
 #define PIXHIP_TYPE_Q8_0 8
 #define PIXHIP_TYPE_Q5_K 13
@@ -124,6 +126,55 @@ int pixhip_weight_residency(pixhip_session* session, uint64_t* gguf_bytes, uint6
 /* The type and shape a handle was created with (PixWeight::type and shape
  * {inner, rows}, src/model.h:33-39). */
 int pixhip_weight_shape(const pixhip_weight* weight, uint32_t* type, uint64_t* inner, uint64_t* rows);
+
+/* ---- model files: PixModelFile (src/model.h:41-56, src/model.cpp:87-250) ---- */
+
+typedef struct pixhip_model pixhip_model;
+
+/* One PixWeight (src/model.h:33-39). */
+typedef struct pixhip_tensor_info {
+    const char* name;   /* valid while the model is open; NUL-terminated */
+    uint64_t name_length; /* bytes of the name (GGUF names may hold NUL bytes) */
+    uint32_t type;      /* GGML type: F32 0, F16 1, Q8_0 8, Q5_K 13, Q6_K 14, BF16 30 */
+    uint32_t rank;      /* 1..5 */
+    uint64_t shape[5];  /* GGML order, first dimension contiguous; unused dimensions 0 */
+    uint64_t offset;    /* absolute byte offset in the mapping */
+    uint64_t bytes;     /* weight_bytes(shape, type) */
+} pixhip_tensor_info;
+
+/* PixModelFile::open (src/model.cpp:138-160) and read (:162-243): maps `path`
+ * read-only and parses it as GGUF version 3 (safetensors = 0) or safetensors,
+ * with the reference's acceptance rules (header within the first 64 MiB, at most
+ * 1e6 tensors / metadata pairs / array items, rank 1..5, types F32 / F16 / BF16 /
+ * Q8_0 / Q5_K / Q6_K with whole blocks, offsets aligned to general.alignment
+ * (default 32) and inside the file, no duplicate names or keys, no overlapping
+ * tensors).  PIXHIP_ERR_OPEN when the file cannot be opened or mapped,
+ * PIXHIP_ERR_FORMAT when it is not accepted (MODEL_ERROR_OPEN / _FORMAT). */
+int pixhip_model_open(const char* path, int safetensors, pixhip_model** out);
+/* PixModelFile::close (src/model.cpp:128-136): unmaps the file. */
+void pixhip_model_close(pixhip_model* model);
+/* PixModelFile::data and size: the mapping. */
+const unsigned char* pixhip_model_data(const pixhip_model* model, uint64_t* size);
+/* PixModelFile::weights, in name order (std::map). */
+uint64_t pixhip_model_tensor_count(const pixhip_model* model);
+int pixhip_model_tensor_at(const pixhip_model* model, uint64_t index, pixhip_tensor_info* info);
+/* PixModelFile::tensor (src/model.cpp:245-249); PIXHIP_ERR_ARGUMENT when absent. */
+int pixhip_model_tensor(const pixhip_model* model, const char* name, pixhip_tensor_info* info);
+/* PixModelFile::metadata, in key order: entry `index`'s key, and its value as
+ * JSON text (numbers in the reference's textual form, e.g. float32 as
+ * std::to_string prints it).  Each copies at most length - 1 bytes and a NUL
+ * and returns the full length (call with length 0 to size a buffer), or
+ * PIXHIP_ERR_ARGUMENT. */
+uint64_t pixhip_model_metadata_count(const pixhip_model* model);
+int64_t pixhip_model_metadata_key(const pixhip_model* model, uint64_t index, char* key, size_t length);
+int64_t pixhip_model_metadata_value(const pixhip_model* model, uint64_t index, char* value, size_t length);
+/* The metadata value of `key` as JSON text, as above; PIXHIP_ERR_ARGUMENT when absent. */
+int64_t pixhip_model_metadata(const pixhip_model* model, const char* key, char* value, size_t length);
+/* VulkanState::weight (src/backend_vulkan.cpp:742-758) for tensor `name` of an
+ * open model: pixhip_weight_get with the key "file:name:offset:bytes" and the
+ * mapping's bytes (a 2-D Q8_0 / Q5_K / Q6_K tensor; the model must stay open
+ * while the handle is used). */
+int pixhip_model_weight(pixhip_session* session, const pixhip_model* model, const char* name, pixhip_weight** out);
 
 /* ---- the op: vulkan_matmul / VulkanState::multiply ---- */
 

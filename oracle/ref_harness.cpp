@@ -286,4 +286,83 @@ size_t ref_shortcut(const float* x, size_t width, size_t height, size_t in_chann
     return o.values.size();
 }
 
+/* PixModelFile::open (src/model.cpp:138-243) on `path`, rendered as text for
+ * comparison with another reader: "open <code>\n", then per tensor in name
+ * order "T <name> <type> <d0,d1,...> <offset> <bytes>\n", then per metadata key
+ * "M <key> <value as JSON>\n" (strings with '"', '\\' and control characters
+ * escaped, numbers and booleans in PixJson's text).  Writes at most
+ * `capacity` bytes; returns the full length. */
+static void ref_json(const PixJson &v, std::string &out)
+{
+    static const char hex[] = "0123456789abcdef";
+    auto quote = [&](const std::string &s) {
+        out += '"';
+        for (unsigned char c : s) {
+            if (c == '"' || c == '\\') {
+                out += '\\';
+                out += char(c);
+            } else if (c < 0x20) {
+                out += "\\u00";
+                out += hex[c >> 4];
+                out += hex[c & 15];
+            } else out += char(c);
+        }
+        out += '"';
+    };
+    switch (v.type) {
+    case PixJson::Null: out += "null"; break;
+    case PixJson::Boolean:
+    case PixJson::Number: out += v.scalar; break;
+    case PixJson::String: quote(v.scalar); break;
+    case PixJson::Array:
+        out += '[';
+        for (size_t i = 0; i < v.array.size(); i++) {
+            if (i) out += ',';
+            ref_json(v.array[i],out);
+        }
+        out += ']';
+        break;
+    case PixJson::Object: {
+        out += '{';
+        bool first = true;
+        for (const auto &m : v.object) {
+            if (!first) out += ',';
+            first = false;
+            quote(m.first);
+            out += ':';
+            ref_json(m.second,out);
+        }
+        out += '}';
+        break;
+    }
+    default: out += "?"; break;
+    }
+}
+
+size_t ref_model_probe(const char* path, int safetensors, char* out, size_t capacity)
+{
+    PixModelFile model;
+    const int code = model.open(path,safetensors != 0);
+    std::string text = "open " + std::to_string(code) + "\n";
+    if (!code) {
+        for (const auto &e : model.weights) {
+            const PixWeight &w = e.second;
+            text += "T " + w.name + " " + std::to_string(w.type) + " ";
+            for (size_t i = 0; i < w.shape.size(); i++) text += (i? "," : "") + std::to_string(w.shape[i]);
+            text += " " + std::to_string(w.offset) + " " + std::to_string(w.bytes) + "\n";
+        }
+        for (const auto &m : model.metadata) {
+            text += "M " + m.first + " ";
+            ref_json(m.second,text);
+            text += "\n";
+        }
+    }
+    if (capacity) {
+        const size_t n = std::min(text.size(),capacity - 1);
+        std::memcpy(out,text.data(),n);
+        out[n] = 0;
+    }
+    return text.size();
+}
+
 }

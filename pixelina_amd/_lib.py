@@ -15,6 +15,8 @@ ERR_UNSUPPORTED = -2
 ERR_MEMORY = -3
 ERR_DEVICE = -4
 ERR_STATE = -5
+ERR_OPEN = -6
+ERR_FORMAT = -7
 
 Q8_0 = 8
 Q5_K = 13
@@ -63,6 +65,17 @@ SIGNATURES = {
     "pixhip_rope": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
     "pixhip_attention": (_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _int, _vp]),
     "pixhip_attention_ranges": (_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _vp]),
+    "pixhip_model_open": (_int, [ctypes.c_char_p, _int, ctypes.POINTER(_vp)]),
+    "pixhip_model_close": (None, [_vp]),
+    "pixhip_model_data": (_vp, [_vp, ctypes.POINTER(_u64)]),
+    "pixhip_model_tensor_count": (_u64, [_vp]),
+    "pixhip_model_tensor_at": (_int, [_vp, _u64, _vp]),
+    "pixhip_model_tensor": (_int, [_vp, ctypes.c_char_p, _vp]),
+    "pixhip_model_metadata_count": (_u64, [_vp]),
+    "pixhip_model_metadata_key": (ctypes.c_int64, [_vp, _u64, ctypes.c_char_p, _sz]),
+    "pixhip_model_metadata_value": (ctypes.c_int64, [_vp, _u64, ctypes.c_char_p, _sz]),
+    "pixhip_model_metadata": (ctypes.c_int64, [_vp, ctypes.c_char_p, ctypes.c_char_p, _sz]),
+    "pixhip_model_weight": (_int, [_vp, _vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "pixhip_pointwise_ex": (_int, [_vp, ctypes.c_uint, _vp, _vp, _vp, _sz, _sz, ctypes.c_uint, ctypes.c_float, ctypes.c_float]),
     "pixhip_qwen_modulate": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _sz, _sz, _vp]),
     "pixhip_l2norm": (_int, [_vp, _vp, _sz, _sz, _vp, ctypes.c_float, _vp]),

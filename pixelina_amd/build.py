@@ -25,6 +25,7 @@ SOURCES = [
     "csrc/attention.hip",
     "csrc/tensor_ops.hip",
     "csrc/api.cpp",
+    "csrc/model_file.cpp",
     "host/backend_hip.cpp",
 ]
 

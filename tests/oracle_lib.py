@@ -107,6 +107,7 @@ def reference():
             "ref_scatter": (_int, [_vp, _sz, _sz, _vp, _vp, _sz]),
             "ref_upsample": (_int, [_vp, _sz, _sz, _sz, _vp]),
             "ref_shortcut": (_sz, [_vp, _sz, _sz, _sz, _sz, _sz, _int, _int, _vp, _sz]),
+            "ref_model_probe": (_sz, [ctypes.c_char_p, _int, ctypes.c_char_p, _sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
