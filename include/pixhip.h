@@ -175,6 +175,10 @@ int64_t pixhip_model_metadata(const pixhip_model* model, const char* key, char* 
  * mapping's bytes (a 2-D Q8_0 / Q5_K / Q6_K tensor; the model must stay open
  * while the handle is used). */
 int pixhip_model_weight(pixhip_session* session, const pixhip_model* model, const char* name, pixhip_weight** out);
+/* The same for a convolution weight (pixhip_conv_weight_get): tensor `name`
+ * of rank 4 [kx, ky, cin, cout] or rank 5 [kx, ky, 1, cin, cout] (the checks
+ * of src/convolution.cpp:60-62), type F32 / F16 / BF16. */
+int pixhip_model_conv_weight(pixhip_session* session, const pixhip_model* model, const char* name, pixhip_weight** out);
 
 /* ---- the op: vulkan_matmul / VulkanState::multiply ---- */
 
@@ -460,6 +464,38 @@ int pixhip_layout(pixhip_session* session, unsigned operation, const float* sour
  * / group).  The reference's shape checks apply. */
 int pixhip_shortcut(pixhip_session* session, const float* source, size_t width, size_t height, size_t source_channels,
                     float* destination, size_t channels, size_t temporal, int up, int spatial);
+
+/* ---- convolution: vulkan_conv (src/backend_vulkan.h:146-147) ---- */
+
+/* PixConv2D (src/tensor.h:65-68). */
+typedef struct pixhip_conv_geometry {
+    size_t stride_x, stride_y;
+    size_t left, right, top, bottom;  /* zero padding */
+} pixhip_conv_geometry;
+
+/* The cache entry of a convolution weight (VulkanState::weight of the
+ * flattened tensor, src/backend_vulkan.cpp:1195, :1388): `bytes` of a float
+ * tensor (F32 0, F16 1, BF16 30) of GGML shape [kernel_x, kernel_y,
+ * in_channels, out_channels] (a rank-5 [kx, ky, 1, cin, cout] tensor is the
+ * same bytes), keyed like pixhip_weight_get.  On first use it is made resident
+ * as two bf16 planes (hi, lo = w - hi) with the inner index reordered to
+ * (ky, kx, c); F16 and BF16 weights are exact in them.  Quantized convolution
+ * weights are PIXHIP_ERR_UNSUPPORTED. */
+int pixhip_conv_weight_get(pixhip_session* session, const char* key, const void* host_bytes, uint64_t bytes, uint32_t type,
+                           uint64_t kernel_x, uint64_t kernel_y, uint64_t in_channels, uint64_t out_channels, pixhip_weight** out);
+
+/* tensor_conv (src/convolution.cpp:34-100; vulkan_conv, src/backend_vulkan.cpp:
+ * 1177-1209, :1359-1402): `output` [out_width * out_height][out_channels] =
+ * the convolution of `input` [width * height][in_channels] (pixels row-major,
+ * channels innermost) with the weight, plus bias[o] when `bias` is not NULL.
+ * `geometry` NULL is tensor_conv's first form (stride 1, the kernel centred at
+ * offset kernel / 2, out = in); otherwise out_width = (width + left + right -
+ * kernel_x) / stride_x + 1 (and likewise in y), with the reference's checks.
+ * Within 1e-4 of the fp32 reference per output row (split-bf16 MFMA products,
+ * fp32 accumulation).  Tensors are device or pinned host memory (input and
+ * bias may be pageable), 4-byte aligned. */
+int pixhip_conv2d(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t width, size_t height,
+                  const pixhip_conv_geometry* geometry, const float* bias, float* output);
 
 /* ---- integer parity gate ---- */
 

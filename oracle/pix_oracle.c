@@ -52,6 +52,8 @@
  *  28 qwen modulation with the two parameter rows swapped
  *  29 residual gate without tanh
  *  30 affine adding the bias before the scale
+ *  31 convolution patches with the kernel's x and y swapped
+ *  32 convolution padding taken from the right instead of the left
  */
 #ifndef ORC_MUTANT
 #define ORC_MUTANT 0
@@ -969,5 +971,50 @@ int orc_shortcut(const float* input, size_t width, size_t height, size_t input_c
                 }
                 out[(y * ow + x) * channels + c] = value;
             }
+    return 1;
+}
+
+/* tensor_conv's geometry form, src/convolution.cpp:56-100 (the first form,
+ * :34-54, is the geometry {1, 1, k/2, k-1-k/2, k/2, k-1-k/2}): each output
+ * pixel (ox, oy) reads input (ox*sx - left + kx, oy*sy - top + ky), zero
+ * outside the image, patch index (c * kernel_y + ky) * kernel_x + kx, times
+ * weight [cout][patch], plus bias[o] (NULL: none).  The sums are taken in
+ * double (the reference's fp32 FMA tiles round differently; comparisons are
+ * held to a tolerance).  `out` [out_w * out_h][cout]; returns 0 on the
+ * reference's rejections. */
+int orc_conv2d(const float* x, size_t width, size_t height, size_t cin, const float* weight, size_t kx_n, size_t ky_n, size_t cout,
+               const float* bias, size_t sx, size_t sy, size_t left, size_t right, size_t top, size_t bottom, float* out)
+{
+    if (!width || !height || !sx || !sy || width + left + right < kx_n || height + top + bottom < ky_n) return 0;
+    const size_t ow = (width + left + right - kx_n) / sx + 1, oh = (height + top + bottom - ky_n) / sy + 1;
+    const size_t inner = cin * kx_n * ky_n;
+    double* patch = (double*)malloc(inner * sizeof(double));
+    if (!patch) return 0;
+    for (size_t oy = 0; oy < oh; oy++)
+        for (size_t ox = 0; ox < ow; ox++) {
+#if ORC_MUTANT == 32
+            const int64_t x0 = (int64_t)(ox * sx) - (int64_t)right, y0 = (int64_t)(oy * sy) - (int64_t)bottom;
+#else
+            const int64_t x0 = (int64_t)(ox * sx) - (int64_t)left, y0 = (int64_t)(oy * sy) - (int64_t)top;
+#endif
+            for (size_t c = 0; c < cin; c++)
+                for (size_t ky = 0; ky < ky_n; ky++)
+                    for (size_t kx = 0; kx < kx_n; kx++) {
+                        const int64_t ix = x0 + (int64_t)kx, iy = y0 + (int64_t)ky;
+#if ORC_MUTANT == 31
+                        const size_t to = (c * kx_n + kx) * ky_n + ky;
+#else
+                        const size_t to = (c * ky_n + ky) * kx_n + kx;
+#endif
+                        patch[to] = (ix < 0 || iy < 0 || ix >= (int64_t)width || iy >= (int64_t)height)? 0.0
+                                    : (double)x[((size_t)iy * width + (size_t)ix) * cin + c];
+                    }
+            for (size_t o = 0; o < cout; o++) {
+                double acc = 0.0;
+                for (size_t k = 0; k < inner; k++) acc += patch[k] * (double)weight[o * inner + k];
+                out[(oy * ow + ox) * cout + o] = (float)acc + (bias? bias[o] : 0.0f);
+            }
+        }
+    free(patch);
     return 1;
 }

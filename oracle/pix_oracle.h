@@ -68,6 +68,8 @@ void orc_decode_f32(const void* data, uint32_t type, size_t count, float* out);
 int orc_rows(const float* source, size_t source_rows, float* destination, size_t destination_rows, size_t channels,
              const uint64_t* rows, size_t count, int scatter);
 void orc_layout(int op, const float* source, float* destination, size_t width, size_t height, size_t channels, size_t patch);
+int orc_conv2d(const float* x, size_t width, size_t height, size_t cin, const float* weight, size_t kx_n, size_t ky_n, size_t cout,
+               const float* bias, size_t sx, size_t sy, size_t left, size_t right, size_t top, size_t bottom, float* out);
 int orc_shortcut(const float* input, size_t width, size_t height, size_t input_channels, size_t channels, size_t temporal, int up,
                  int spatial, float* out);
 

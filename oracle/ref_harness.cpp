@@ -365,4 +365,45 @@ size_t ref_model_probe(const char* path, int safetensors, char* out, size_t capa
     return text.size();
 }
 
+/* tensor_conv (src/convolution.cpp:34-100) with the weight `c.weight` (raw
+ * bytes of `type`, GGML shape [kx, ky, cin, cout]) and bias `c.bias` (F32
+ * [cout], NULL: none) in a PixModelFile whose mapping is a buffer.  form 0:
+ * the first form (square kernel, bias required); form 1: the geometry form.
+ * Returns the number of output values written (0: rejected). */
+size_t ref_conv(const float* x, size_t width, size_t height, size_t cin, const void* weight, uint32_t type, size_t kx, size_t ky,
+                size_t cout, const float* bias, int form, size_t sx, size_t sy, size_t left, size_t right, size_t top, size_t bottom,
+                float* out, size_t capacity)
+{
+    const uint64_t wbytes = weight_bytes({uint64_t(kx),uint64_t(ky),uint64_t(cin),uint64_t(cout)},type);
+    std::vector<unsigned char> blob(size_t(wbytes) + cout * 4);
+    std::memcpy(blob.data(),weight,size_t(wbytes));
+    if (bias) std::memcpy(blob.data() + wbytes,bias,cout * 4);
+    PixModelFile model;
+    model.data = blob.data();
+    model.size = blob.size();
+    model.filename = "conv";
+    model.weights["c" WEIGHT_SUFFIX] = PixWeight{"c" WEIGHT_SUFFIX,{uint64_t(kx),uint64_t(ky),uint64_t(cin),uint64_t(cout)},type,0,wbytes};
+    if (bias) model.weights["c" BIAS_SUFFIX] = PixWeight{"c" BIAS_SUFFIX,{uint64_t(cout)},MODEL_F32,wbytes,uint64_t(cout) * 4};
+    PixTensor in(width * height,cin);
+    std::copy(x,x + width * height * cin,in.values.begin());
+    PixTensor o;
+    if (form == 0) {
+        o = tensor_conv(model,"c",in,width,height);
+    } else {
+        PixConv2D g;
+        g.stride_x = sx;
+        g.stride_y = sy;
+        g.left = left;
+        g.right = right;
+        g.top = top;
+        g.bottom = bottom;
+        o = tensor_conv(model,"c",in,width,height,g,bias != nullptr);
+    }
+    model.data = nullptr;
+    model.size = 0;
+    if (o.values.empty() || o.values.size() > capacity) return 0;
+    std::copy(o.values.begin(),o.values.end(),out);
+    return o.values.size();
+}
+
 }

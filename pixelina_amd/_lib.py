@@ -76,6 +76,9 @@ SIGNATURES = {
     "pixhip_model_metadata_value": (ctypes.c_int64, [_vp, _u64, ctypes.c_char_p, _sz]),
     "pixhip_model_metadata": (ctypes.c_int64, [_vp, ctypes.c_char_p, ctypes.c_char_p, _sz]),
     "pixhip_model_weight": (_int, [_vp, _vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "pixhip_conv_weight_get": (_int, [_vp, ctypes.c_char_p, _vp, _u64, _u32, _u64, _u64, _u64, _u64, ctypes.POINTER(_vp)]),
+    "pixhip_conv2d": (_int, [_vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
+    "pixhip_model_conv_weight": (_int, [_vp, _vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "pixhip_pointwise_ex": (_int, [_vp, ctypes.c_uint, _vp, _vp, _vp, _sz, _sz, ctypes.c_uint, ctypes.c_float, ctypes.c_float]),
     "pixhip_qwen_modulate": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _sz, _sz, _vp]),
     "pixhip_l2norm": (_int, [_vp, _vp, _sz, _sz, _vp, ctypes.c_float, _vp]),
@@ -117,6 +120,12 @@ class PixhipError(RuntimeError):
         msg = load().pixhip_last_error().decode(errors="replace")
         super().__init__(f"{what} failed ({code}): {msg}")
         self.code = code
+
+
+class ConvGeometry(ctypes.Structure):
+    """pixhip_conv_geometry (PixConv2D, src/tensor.h:65-68)."""
+    _fields_ = [("stride_x", ctypes.c_size_t), ("stride_y", ctypes.c_size_t), ("left", ctypes.c_size_t),
+                ("right", ctypes.c_size_t), ("top", ctypes.c_size_t), ("bottom", ctypes.c_size_t)]
 
 
 def check(code, what):

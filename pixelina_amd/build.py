@@ -24,6 +24,7 @@ SOURCES = [
     "csrc/ops.hip",
     "csrc/attention.hip",
     "csrc/tensor_ops.hip",
+    "csrc/conv.hip",
     "csrc/api.cpp",
     "csrc/model_file.cpp",
     "host/backend_hip.cpp",

@@ -115,6 +115,12 @@ struct pixhip_weight {
     pixhip::PlanarQ6K q6p{};
     size_t resident = 0;
     uint64_t used = 0;
+    // convolution weights (F32 / F16 / BF16, [cout][cin * ky * kx]): the
+    // split-bf16 planes the implicit GEMM reads, built on first use
+    bool conv = false;
+    uint32_t kernel_x = 0, kernel_y = 0, cin = 0;
+    void* conv_planes = nullptr;
+    size_t conv_kp = 0, conv_npad = 0;
 };
 
 struct pixhip_session {
@@ -171,7 +177,8 @@ void release_forms(pixhip_session* s, pixhip_weight* w)
     if (w->raw) (void)hipFree(w->raw);
     if (w->planes) (void)hipFree(w->planes);
     if (w->planar) (void)hipFree(w->planar);
-    w->raw = w->planes = w->planar = nullptr;
+    if (w->conv_planes) (void)hipFree(w->conv_planes);
+    w->raw = w->planes = w->planar = w->conv_planes = nullptr;
     w->q5 = {};
     w->q6 = {};
     w->q80 = {};
@@ -564,6 +571,7 @@ int run(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t c
     if (rc) return rc;
     pixhip_weight* w = const_cast<pixhip_weight*>(wc);
     if (!w) return fail(PIXHIP_ERR_ARGUMENT,"null weight handle");
+    if (w->conv) return fail(PIXHIP_ERR_UNSUPPORTED,"a convolution weight: use pixhip_conv2d");
     if (!columns || (stages & PIXHIP_STAGE_MULTIPLY && !output) || (stages & PIXHIP_STAGE_QUANTIZE && !input))
         return fail(PIXHIP_ERR_ARGUMENT,"null pointer or zero columns");
     if (!stages || stages > (PIXHIP_STAGE_QUANTIZE | PIXHIP_STAGE_MULTIPLY)) return fail(PIXHIP_ERR_ARGUMENT,"bad stage flags");
@@ -846,7 +854,8 @@ int pixhip_weight_get(pixhip_session* s, const char* key, const void* host_bytes
     auto it = s->weights.find(key);
     if (it != s->weights.end()) {
         pixhip_weight* w = it->second;
-        if (w->type != type || w->inner != inner || w->rows != rows) return fail(PIXHIP_ERR_ARGUMENT,"cached key with another shape");
+        if (w->conv || w->type != type || w->inner != inner || w->rows != rows)
+            return fail(PIXHIP_ERR_ARGUMENT,"cached key with another shape");
         if (host_bytes) {
             if (bytes < expect) return fail(PIXHIP_ERR_ARGUMENT,"weight bytes shorter than rows*row_bytes");
             w->host = host_bytes;  // the caller's current mapping of the same bytes
@@ -934,6 +943,7 @@ int pixhip_matmul_ex_noalloc(pixhip_session* s, const pixhip_weight* wc, const f
     if (rc) return rc;
     pixhip_weight* w = const_cast<pixhip_weight*>(wc);
     if (!w) return fail(PIXHIP_ERR_ARGUMENT,"null weight handle");
+    if (w->conv) return fail(PIXHIP_ERR_UNSUPPORTED,"a convolution weight: use pixhip_conv2d");
     if (!columns || !input || !output) return fail(PIXHIP_ERR_ARGUMENT,"null pointer or zero columns");
     if (!ldy) ldy = w->rows;
     if (ldy < w->rows) return fail(PIXHIP_ERR_ARGUMENT,"output stride smaller than rows");
@@ -1243,6 +1253,7 @@ int pixhip_block_sums(pixhip_session* s, const pixhip_weight* wc, const float* i
     if (rc) return rc;
     pixhip_weight* w = const_cast<pixhip_weight*>(wc);
     if (!w || !input || !sums || !columns || (w->type == PIX_Q5_K && !mins)) return fail(PIXHIP_ERR_ARGUMENT,"null pointer");
+    if (w->conv) return fail(PIXHIP_ERR_UNSUPPORTED,"a convolution weight");
     if (reinterpret_cast<uintptr_t>(input) % 16) return fail(PIXHIP_ERR_ARGUMENT,"input must be 16-byte aligned");
     if ((rc = quantize_stage(s,w,input,columns))) return rc;
     if ((rc = ensure_gemm_form(s,w))) return rc;
@@ -1660,6 +1671,154 @@ int pixhip_shortcut(pixhip_session* s, const float* source, size_t width, size_t
     hipError_t e = pixhip::launch_shortcut(static_cast<const float*>(src),static_cast<float*>(dst),out_width * out_height,channels,
                                            source_channels,width,side,temporal,up != 0,s->stream);
     PIX_HIP(e,"shortcut");
+    return PIXHIP_OK;
+}
+
+}  // extern "C"
+
+/* ---- convolution ---- */
+
+namespace {
+
+// The split-bf16 planes of a convolution weight, built from its file bytes.
+int ensure_conv_form(pixhip_session* s, pixhip_weight* w)
+{
+    if (w->conv_planes) return PIXHIP_OK;
+    int rc = ensure_raw(s,w);
+    if (rc) return rc;
+    const size_t plane = w->conv_npad * w->conv_kp * sizeof(uint16_t);
+    if ((rc = weight_alloc(s,w,2 * plane,&w->conv_planes))) return rc;
+    uint16_t* hi = static_cast<uint16_t*>(w->conv_planes);
+    PIX_HIP(pixhip::launch_conv_form(w->raw,w->type,(int)w->kernel_x,(int)w->kernel_y,(int)w->cin,(int)w->rows,(int)w->conv_kp,
+                                     (int)w->conv_npad,hi,hi + plane / sizeof(uint16_t),s->stream),
+            "convolution weight form");
+    return release_raw(s,w);
+}
+
+size_t float_type_bytes(uint32_t type)
+{
+    return type == PIX_F32? 4 : (type == PIX_F16 || type == PIX_BF16)? 2 : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pixhip_conv_weight_get(pixhip_session* s, const char* key, const void* host_bytes, uint64_t bytes, uint32_t type,
+                           uint64_t kernel_x, uint64_t kernel_y, uint64_t in_channels, uint64_t out_channels, pixhip_weight** out)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    if (!key || !out) return fail(PIXHIP_ERR_ARGUMENT,"null key or output");
+    *out = nullptr;
+    const size_t elem = float_type_bytes(type);
+    if (!elem) return fail(PIXHIP_ERR_UNSUPPORTED,"convolution weights are F32, F16 or BF16 (type " + std::to_string(type) + ")");
+    if (!kernel_x || !kernel_y || !in_channels || !out_channels || kernel_x > 64 || kernel_y > 64 || in_channels > (1u << 20) ||
+        out_channels > (1u << 20) || in_channels * kernel_x * kernel_y > INT32_MAX / 2)
+        return fail(PIXHIP_ERR_ARGUMENT,"bad convolution weight shape");
+    const uint64_t inner = in_channels * kernel_x * kernel_y, expect = out_channels * inner * elem;
+    auto it = s->weights.find(key);
+    if (it != s->weights.end()) {
+        pixhip_weight* w = it->second;
+        if (!w->conv || w->type != type || w->kernel_x != kernel_x || w->kernel_y != kernel_y || w->cin != in_channels ||
+            w->rows != out_channels)
+            return fail(PIXHIP_ERR_ARGUMENT,"cached key with another shape");
+        if (host_bytes) {
+            if (bytes < expect) return fail(PIXHIP_ERR_ARGUMENT,"weight bytes shorter than the tensor");
+            w->host = host_bytes;
+        }
+        w->used = ++s->uses;
+        *out = w;
+        return PIXHIP_OK;
+    }
+    if (!host_bytes || bytes < expect) return fail(PIXHIP_ERR_ARGUMENT,"weight bytes missing or shorter than the tensor");
+    pixhip_weight* w = new (std::nothrow) pixhip_weight();
+    if (!w) return fail(PIXHIP_ERR_MEMORY,"host allocation failed");
+    w->key = key;
+    w->type = type;
+    w->inner = inner;
+    w->rows = out_channels;
+    w->gguf_bytes = expect;
+    w->host = host_bytes;
+    w->used = ++s->uses;
+    w->conv = true;
+    w->kernel_x = (uint32_t)kernel_x;
+    w->kernel_y = (uint32_t)kernel_y;
+    w->cin = (uint32_t)in_channels;
+    w->conv_kp = round_up(inner,pixhip::kConvTileK);
+    w->conv_npad = round_up(out_channels,pixhip::kConvTileN);
+    if ((rc = ensure_raw(s,w))) {
+        release_forms(s,w);
+        delete w;
+        return rc;
+    }
+    s->weights.emplace(w->key,w);
+    *out = w;
+    return PIXHIP_OK;
+}
+
+int pixhip_conv2d(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t width, size_t height,
+                  const pixhip_conv_geometry* geometry, const float* bias, float* output)
+{
+    int rc = use_device(s);
+    if (rc) return rc;
+    pixhip_weight* w = const_cast<pixhip_weight*>(wc);
+    if (!w || !w->conv) return fail(PIXHIP_ERR_ARGUMENT,"not a convolution weight (pixhip_conv_weight_get)");
+    if (!input || !output || !width || !height || width > SIZE_MAX / height) return fail(PIXHIP_ERR_ARGUMENT,"null pointer or empty image");
+    // tensor_conv's "same" form (src/convolution.cpp:34-54): stride 1, the
+    // kernel centred (offset kernel / 2), as many output pixels as input ones
+    pixhip_conv_geometry g{1,1,w->kernel_x / 2,w->kernel_x - 1 - w->kernel_x / 2,w->kernel_y / 2,w->kernel_y - 1 - w->kernel_y / 2};
+    if (geometry) g = *geometry;
+    // the geometry form's checks (src/convolution.cpp:58-69)
+    if (!g.stride_x || !g.stride_y || g.left > SIZE_MAX - width || g.right > SIZE_MAX - width - g.left || g.top > SIZE_MAX - height ||
+        g.bottom > SIZE_MAX - height - g.top)
+        return fail(PIXHIP_ERR_ARGUMENT,"bad convolution geometry");
+    const size_t pw = width + g.left + g.right, ph = height + g.top + g.bottom;
+    if (pw < w->kernel_x || ph < w->kernel_y) return fail(PIXHIP_ERR_ARGUMENT,"the padded image is smaller than the kernel");
+    const size_t ow = (pw - w->kernel_x) / g.stride_x + 1, oh = (ph - w->kernel_y) / g.stride_y + 1;
+    if (width > INT32_MAX / 2 || height > INT32_MAX / 2 || pw > INT32_MAX / 2 || ph > INT32_MAX / 2 || g.stride_x > INT32_MAX ||
+        g.stride_y > INT32_MAX || ow > SIZE_MAX / oh)
+        return fail(PIXHIP_ERR_ARGUMENT,"image too large");
+    size_t in_bytes = 0, out_bytes = 0;
+    if (width * height > SIZE_MAX / w->cin / 4 || ow * oh > SIZE_MAX / w->rows / 4) return fail(PIXHIP_ERR_ARGUMENT,"image too large");
+    in_bytes = width * height * w->cin * 4;
+    out_bytes = ow * oh * w->rows * 4;
+    (void)out_bytes;
+    if (reinterpret_cast<uintptr_t>(input) % 4 || reinterpret_cast<uintptr_t>(output) % 4 || reinterpret_cast<uintptr_t>(bias) % 4)
+        return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
+    w->used = ++s->uses;
+    if ((rc = ensure_conv_form(s,w))) return rc;
+    void* out = nullptr;
+    if ((rc = write_operand(s,output,&out))) return rc;
+    Staged st(s);
+    const void *in = nullptr, *b = nullptr;
+    if ((rc = st.read(input,in_bytes,&in))) return rc;
+    if (bias && (rc = st.read(bias,w->rows * sizeof(float),&b))) return rc;
+    pixhip::ConvArgs a{};
+    a.x = static_cast<const float*>(in);
+    a.wh = static_cast<const uint16_t*>(w->conv_planes);
+    a.wl = a.wh + w->conv_npad * w->conv_kp;
+    a.bias = static_cast<const float*>(b);
+    a.y = static_cast<float*>(out);
+    a.W = (int)width;
+    a.H = (int)height;
+    a.C = (int)w->cin;
+    a.KX = (int)w->kernel_x;
+    a.KY = (int)w->kernel_y;
+    a.SX = (int)g.stride_x;
+    a.SY = (int)g.stride_y;
+    a.PL = (int)g.left;
+    a.PT = (int)g.top;
+    a.OW = (int)ow;
+    a.OH = (int)oh;
+    a.K = (int)w->inner;
+    a.Kp = (int)w->conv_kp;
+    a.N = (int)w->rows;
+    a.Npad = (int)w->conv_npad;
+    a.M = (long long)(ow * oh);
+    hipError_t e = pixhip::launch_conv(a,s->stream);
+    if (e == hipErrorInvalidValue) return fail(PIXHIP_ERR_ARGUMENT,"convolution grid too large");
+    PIX_HIP(e,"convolution");
     return PIXHIP_OK;
 }
 

@@ -1,0 +1,260 @@
+// Convolution: tensor_conv (src/convolution.cpp:34-100) and vulkan_conv
+// (src/backend_vulkan.cpp:1177-1209, :1359-1402) as an implicit GEMM on bf16
+// MFMA (gfx950).
+//
+// The reference forms the im2col patches of every output pixel (inner index
+// (c * kernel_y + ky) * kernel_x + kx, zero outside the image), multiplies them
+// by the float weight [out][inner] in fp32 (cpu_gemm's FMA tiles, or the
+// Vulkan matmul shader) and adds the bias.  Here the patches are never written
+// out: a workgroup gathers its 128 pixels x 32 inner values straight from the
+// image into LDS, with the inner dimension ordered (ky, kx, c) so that a stage
+// of 32 is one kernel tap over 32 consecutive channels (one 128-byte run per
+// pixel) whenever channels % 32 == 0 -- the weight is stored in that order
+// when it is made resident.  Products run as attention's do: every fp32
+// operand split into bf16 halves (hi = bf16(x), lo = bf16(x - hi)) and
+// a*b = hi*hi + hi*lo + lo*hi on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation, about 2^-16 relative per product (the weight halves are made
+// once, at upload; F16 and BF16 weights are exact in them).
+//
+// Tile: 128 pixels x 128 output channels x 32 inner per stage, 4 waves of
+// 64 x 64 (2 x 2 MFMA tiles), two LDS buffers of four planes (A hi / lo,
+// B hi / lo, rows padded to 80 bytes), the next stage's global loads held in
+// registers while the current one is multiplied.
+#include <algorithm>
+
+#include "pixhip_device.h"
+#include "pixhip_internal.h"
+
+namespace pixhip {
+
+namespace {
+
+typedef __bf16 cbf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t cu32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kCM = 128, kCN = 128, kCK = 32;   // workgroup tile
+constexpr int kCRow = 40;                        // LDS row: 32 bf16 + 8 padding (80 B)
+constexpr int kCPlane = kCM * kCRow;             // bf16 per plane
+constexpr int kCStage = 4 * kCPlane;             // A hi, A lo, B hi, B lo
+
+__device__ __forceinline__ uint32_t rne16(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ void halves(float x, uint32_t& hi, uint32_t& lo)
+{
+    hi = rne16(x);
+    lo = rne16(x - __uint_as_float(hi << 16));
+}
+
+__device__ __forceinline__ float weight_value(const uint8_t* raw, uint32_t type, size_t index)
+{
+    if (type == PIX_F32) {
+        const uint8_t* p = raw + 4 * index;
+        return __uint_as_float((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24));
+    }
+    const uint8_t* p = raw + 2 * index;
+    const uint16_t h = (uint16_t)(p[0] | (p[1] << 8));
+    return type == PIX_F16? half_bits_to_float(h) : __uint_as_float((uint32_t)h << 16);
+}
+
+}  // namespace
+
+// Weight form: planes [npad][kp] of bf16 (hi, lo); row n, column k' = (ky *
+// kernel_x + kx) * cin + c holds weight[n][(c * kernel_y + ky) * kernel_x + kx]
+// of the GGUF / safetensors tensor; zero past cout and inner.
+__global__ __launch_bounds__(256) void conv_form_kernel(const uint8_t* __restrict__ raw, uint32_t type, int kx_n, int ky_n, int cin,
+                                                        int cout, int kp, int npad, uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
+{
+    const size_t inner = (size_t)cin * kx_n * ky_n, total = (size_t)npad * kp, step = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
+        const int n = (int)(e / kp), k = (int)(e % kp);
+        float w = 0.0f;
+        if (n < cout && (size_t)k < inner) {
+            const int c = k % cin, tap = k / cin, kx = tap % kx_n, ky = tap / kx_n;
+            w = weight_value(raw,type,(size_t)n * inner + ((size_t)c * ky_n + ky) * kx_n + kx);
+        }
+        uint32_t h, l;
+        halves(w,h,l);
+        hi[e] = (uint16_t)h;
+        lo[e] = (uint16_t)l;
+    }
+}
+
+hipError_t launch_conv_form(const void* raw, uint32_t type, int kernel_x, int kernel_y, int cin, int cout, int kp, int npad,
+                            uint16_t* hi, uint16_t* lo, hipStream_t s)
+{
+    const size_t total = (size_t)npad * kp;
+    const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256,(size_t)1 << 20);
+    conv_form_kernel<<<dim3(grid),dim3(256),0,s>>>(static_cast<const uint8_t*>(raw),type,kernel_x,kernel_y,cin,cout,kp,npad,hi,lo);
+    return hipGetLastError();
+}
+
+// FAST: cin % 32 == 0 and the image 16-byte aligned (a stage is one tap of 32
+// consecutive channels, read as float4); else each inner value is gathered on
+// its own (the first layer's 3 or 16 channels).
+template <bool FAST>
+__global__ __launch_bounds__(256) void conv_kernel(ConvArgs a)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kCStage];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, lr = lane & 31, hh = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1;
+    const long long m0 = (long long)blockIdx.x * kCM;
+    const int n0 = blockIdx.y * kCN;
+
+    // the pixels this thread loads: rows t/8 + 32i (FAST), rows t/32 + 8i (gather)
+    constexpr int kRowsA = FAST? 4 : 16;
+    int iy0[kRowsA], ix0[kRowsA];
+#pragma unroll
+    for (int i = 0; i < kRowsA; i++) {
+        const long long m = m0 + (FAST? t / 8 + 32 * i : t / 32 + 8 * i);
+        if (m < a.M) {
+            const int oy = (int)(m / a.OW), ox = (int)(m % a.OW);
+            iy0[i] = oy * a.SY - a.PT;
+            ix0[i] = ox * a.SX - a.PL;
+        } else {
+            iy0[i] = -(1 << 30);  // never inside the image
+            ix0[i] = 0;
+        }
+    }
+
+    float4 ra[FAST? 4 : 1];
+    float rs[FAST? 1 : 16];
+    cu32x4 rb[4];
+    auto fetch = [&](int stage) {
+        const int k0 = stage * kCK;
+        if constexpr (FAST) {
+            const int tap = k0 / a.C, c = k0 % a.C + (t % 8) * 4;
+            const int ky = tap / a.KX, kx = tap % a.KX;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int iy = iy0[i] + ky, ix = ix0[i] + kx;
+                ra[i] = make_float4(0.0f,0.0f,0.0f,0.0f);
+                if (iy >= 0 && iy < a.H && ix >= 0 && ix < a.W && k0 < a.K)
+                    ra[i] = *reinterpret_cast<const float4*>(a.x + ((size_t)iy * a.W + ix) * a.C + c);
+            }
+        } else {
+            const int k = k0 + t % 32;
+            const int c = k % a.C, tap = k / a.C, ky = tap / a.KX, kx = tap % a.KX;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int iy = iy0[i] + ky, ix = ix0[i] + kx;
+                rs[i] = (k < a.K && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W) ? a.x[((size_t)iy * a.W + ix) * a.C + c] : 0.0f;
+            }
+        }
+        // B: 128 rows x 64 bytes per plane, two 16-byte pieces per thread per plane
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
+            const uint16_t* plane = (j < 2)? a.wh : a.wl;
+            rb[j] = *reinterpret_cast<const cu32x4*>(plane + (size_t)(n0 + row) * a.Kp + k0 + part * 8);
+        }
+    };
+    auto store = [&](int buf) {
+        uint16_t* st = lds + buf * kCStage;
+        if constexpr (FAST) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = t / 8 + 32 * i, col = (t % 8) * 4;
+                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+                halves(ra[i].x,h0,l0);
+                halves(ra[i].y,h1,l1);
+                halves(ra[i].z,h2,l2);
+                halves(ra[i].w,h3,l3);
+                *reinterpret_cast<uint2*>(st + row * kCRow + col) = make_uint2(h0 | (h1 << 16),h2 | (h3 << 16));
+                *reinterpret_cast<uint2*>(st + kCPlane + row * kCRow + col) = make_uint2(l0 | (l1 << 16),l2 | (l3 << 16));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = t / 32 + 8 * i, col = t % 32;
+                uint32_t h, l;
+                halves(rs[i],h,l);
+                st[row * kCRow + col] = (uint16_t)h;
+                st[kCPlane + row * kCRow + col] = (uint16_t)l;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
+            *reinterpret_cast<cu32x4*>(st + (2 + (j >> 1)) * kCPlane + row * kCRow + part * 8) = rb[j];
+        }
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v16f{};
+
+    const int stages = a.Kp / kCK;
+    fetch(0);
+    store(0);
+    __syncthreads();
+    for (int s = 0; s < stages; s++) {
+        const int buf = s & 1;
+        if (s + 1 < stages) fetch(s + 1);
+        const uint16_t* st = lds + buf * kCStage;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const int col = ks * 16 + 8 * hh;
+            cbf16x8 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int row = wm * 64 + i * 32 + lr;
+                ah[i] = *reinterpret_cast<const cbf16x8*>(st + row * kCRow + col);
+                al[i] = *reinterpret_cast<const cbf16x8*>(st + kCPlane + row * kCRow + col);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int row = wn * 64 + j * 32 + lr;
+                bh[j] = *reinterpret_cast<const cbf16x8*>(st + 2 * kCPlane + row * kCRow + col);
+                bl[j] = *reinterpret_cast<const cbf16x8*>(st + 3 * kCPlane + row * kCRow + col);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i],bh[j],acc[i][j],0,0,0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i],bl[j],acc[i][j],0,0,0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i],bh[j],acc[i][j],0,0,0);
+                }
+        }
+        if (s + 1 < stages) {
+            store(buf ^ 1);  // the other buffer: its last readers finished before the previous barrier
+            __syncthreads();
+        }
+    }
+
+    // acc[i][j] lane: output channel n0 + wn*64 + 32j + lr, pixels
+    // m0 + wm*64 + 32i + 8(r/4) + 4hh + r%4
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int n = n0 + wn * 64 + 32 * j + lr;
+        if (n >= a.N) continue;
+        const float b = a.bias? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const long long m = m0 + wm * 64 + 32 * i + 8 * (r / 4) + 4 * hh + r % 4;
+                if (m < a.M) a.y[(size_t)m * a.N + n] = a.bias? __fadd_rn(acc[i][j][r],b) : acc[i][j][r];
+            }
+    }
+}
+
+hipError_t launch_conv(const ConvArgs& a, hipStream_t s)
+{
+    if (!a.M || !a.N) return hipSuccess;
+    const long long mt = (a.M + kCM - 1) / kCM;
+    if (mt > 0x7fffffffLL || a.Npad / kCN > 65535) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)mt,(unsigned)(a.Npad / kCN)), block(256);
+    const bool fast = a.C % kCK == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
+    if (fast) conv_kernel<true><<<grid,block,0,s>>>(a);
+    else conv_kernel<false><<<grid,block,0,s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace pixhip

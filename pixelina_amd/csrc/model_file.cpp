@@ -658,4 +658,17 @@ int pixhip_model_weight(pixhip_session* session, const pixhip_model* model, cons
     return pixhip_weight_get(session,key.c_str(),model->data + t.offset,t.bytes,t.type,t.shape[0],t.shape[1],out);
 }
 
+int pixhip_model_conv_weight(pixhip_session* session, const pixhip_model* model, const char* name, pixhip_weight** out)
+{
+    if (!session || !model || !name || !out) return PIXHIP_ERR_ARGUMENT;
+    auto it = model->tensors.find(name);
+    if (it == model->tensors.end()) return PIXHIP_ERR_ARGUMENT;
+    const Tensor& t = it->second;
+    const size_t rank = t.shape.size();
+    if ((rank != 4 && rank != 5) || (rank == 5 && t.shape[2] != 1)) return PIXHIP_ERR_ARGUMENT;
+    const std::string key = model->filename + ":" + t.name + ":" + std::to_string(t.offset) + ":" + std::to_string(t.bytes);
+    return pixhip_conv_weight_get(session,key.c_str(),model->data + t.offset,t.bytes,t.type,t.shape[0],t.shape[1],t.shape[rank - 2],
+                                  t.shape[rank - 1],out);
+}
+
 }  // extern "C"

@@ -191,6 +191,22 @@ hipError_t launch_layout(int op, const float* src, float* dst, size_t rows, size
 hipError_t launch_shortcut(const float* src, float* dst, size_t out_rows, size_t channels, size_t src_channels, size_t width, size_t side,
                            size_t temporal, bool up, hipStream_t s);
 
+// conv.hip: implicit-GEMM convolution on split-bf16 MFMA.  The weight form is
+// two bf16 planes [Npad][Kp] (hi, lo) with the inner index in (ky, kx, c)
+// order; x [H*W][C], y [OH*OW][N] (+ bias[n] when bias is not null).
+struct ConvArgs {
+    const float* x;
+    const uint16_t *wh, *wl;
+    const float* bias;
+    float* y;
+    int W, H, C, KX, KY, SX, SY, PL, PT, OW, OH, K, Kp, N, Npad;
+    long long M;
+};
+constexpr int kConvTileN = 128, kConvTileK = 32;
+hipError_t launch_conv_form(const void* raw, uint32_t type, int kernel_x, int kernel_y, int cin, int cout, int kp, int npad,
+                            uint16_t* hi, uint16_t* lo, hipStream_t s);
+hipError_t launch_conv(const ConvArgs& a, hipStream_t s);
+
 // repack.hip
 hipError_t launch_repack_q5_K(const uint8_t* raw, size_t rows, size_t inner, size_t npad, int8_t* hi, int8_t* lo, float* d,
                               float* dm, _Float16* mn, hipStream_t s);

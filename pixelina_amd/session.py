@@ -207,6 +207,20 @@ class Session:
         return self.lib.pixhip_shortcut(self.handle, src_ptr, width, height, src_channels, dst_ptr, channels, temporal, int(up),
                                         int(spatial))
 
+    def conv_weight(self, key, raw_bytes, wtype, kx, ky, cin, cout):
+        """pixhip_conv_weight_get over a float tensor's bytes [kx, ky, cin, cout] (GGML order)."""
+        b = np.ascontiguousarray(raw_bytes, dtype=np.uint8)
+        h = ctypes.c_void_p()
+        check(self.lib.pixhip_conv_weight_get(self.handle, key.encode(), b.ctypes.data, b.nbytes, wtype, kx, ky, cin, cout,
+                                              ctypes.byref(h)), "pixhip_conv_weight_get")
+        self._host_weights[key] = b
+        return h.value
+
+    def conv2d(self, weight, x_ptr, width, height, out_ptr, geometry=None, bias_ptr=None):
+        """tensor_conv (src/convolution.cpp:34-100); geometry (sx, sy, left, right, top, bottom) or None."""
+        g = None if geometry is None else ctypes.byref(_lib.ConvGeometry(*geometry))
+        return self.lib.pixhip_conv2d(self.handle, weight, x_ptr, width, height, g, bias_ptr, out_ptr)
+
     def block_sums(self, weight, x_ptr, columns, sums_ptr, mins_ptr=None):
         return self.lib.pixhip_block_sums(self.handle, weight, x_ptr, columns, sums_ptr, mins_ptr)
 

@@ -25,6 +25,9 @@ Fixtures (numpy .npz, data only):
                         blocks), tensor_gather / tensor_scatter (repeated rows),
                         tensor_slice, tensor_upsample, tensor_resample_shortcut
                         (up and down, spatial or not, one or two time steps)
+  g11_conv.npz          tensor_conv, both forms: 3x3 and 1x1 kernels, stride 2
+                        with one-sided padding, a 3x1 kernel, 3 input channels,
+                        F32 / F16 / BF16 weights, with and without a bias
 
     python tests/golden/make_golden.py g5 g6 g7   # only the named fixtures
 """
@@ -40,7 +43,7 @@ sys.path.insert(0, os.path.dirname(HERE))
 
 from oracle_lib import (BF16, F16, F32, Q5_K, Q6_K, Q8_0, add, attention, bias, decode_f32, dot, gather,  # noqa: E402
                         gelu, groupnorm, l2norm, norm_rows, quant_matmul, quantize, reference, rope, scatter, shortcut,
-                        silu_gate, upsample_ref)
+                        silu_gate, upsample_ref, conv2d_ref)
 from pixelina_amd import synth  # noqa: E402
 
 
@@ -260,6 +263,39 @@ def write_g10(ref):
     np.savez_compressed(os.path.join(HERE, "g10_tensor_ops.npz"), **g)
 
 
+# (width, height, cin, cout, kx, ky, weight type, bias, geometry or None)
+G11_CASES = [
+    (12, 10, 32, 40, 3, 3, F32, True, None),
+    (9, 7, 16, 48, 1, 1, F16, True, None),
+    (11, 9, 8, 16, 3, 3, BF16, False, (2, 2, 0, 1, 0, 1)),
+    (8, 6, 12, 20, 3, 1, F32, True, (1, 1, 1, 1, 0, 0)),
+    (10, 10, 3, 24, 3, 3, F16, True, None),
+]
+
+
+def write_g11(ref):
+    rng = np.random.default_rng(1111)
+    g = {"count": np.array(len(G11_CASES))}
+    for c, (wd, ht, cin, cout, kx, ky, wtype, has_bias, geom) in enumerate(G11_CASES):
+        x = rng.standard_normal((wd * ht, cin)).astype(np.float32)
+        w = (rng.standard_normal((cout, cin * ky * kx)) / np.sqrt(cin * kx * ky)).astype(np.float32)
+        if wtype == F16:
+            wb = w.astype(np.float16).view(np.uint8)
+        elif wtype == BF16:
+            wb = (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+        else:
+            wb = w.view(np.uint8)
+        b = rng.standard_normal(cout).astype(np.float32) if has_bias else None
+        y = conv2d_ref(ref, x, wd, ht, wb, wtype, kx, ky, cin, cout, b, geom)
+        assert y is not None, G11_CASES[c]
+        g[f"c{c}_shape"] = np.array([wd, ht, cin, cout, kx, ky, wtype, int(has_bias)])
+        g[f"c{c}_geometry"] = np.array(geom if geom else [], np.int64)
+        g[f"c{c}_x"], g[f"c{c}_w"], g[f"c{c}_y"] = x, np.ascontiguousarray(wb).reshape(-1), y
+        if has_bias:
+            g[f"c{c}_b"] = b
+    np.savez_compressed(os.path.join(HERE, "g11_conv.npz"), **g)
+
+
 def main():
     ref = reference()
     if ref is None:
@@ -276,6 +312,8 @@ def main():
             write_g9(ref)
         if "g10" in only:
             write_g10(ref)
+        if "g11" in only:
+            write_g11(ref)
         return
     rng = np.random.default_rng(20260101)
 
@@ -342,6 +380,7 @@ def main():
     write_g7(ref)
     write_g9(ref)
     write_g10(ref)
+    write_g11(ref)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

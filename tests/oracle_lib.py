@@ -56,6 +56,7 @@ def load_oracle(path):
         "orc_rows": (_int, [_vp, _sz, _vp, _sz, _sz, _vp, _sz, _int]),
         "orc_layout": (None, [_int, _vp, _vp, _sz, _sz, _sz, _sz]),
         "orc_shortcut": (_int, [_vp, _sz, _sz, _sz, _sz, _sz, _int, _int, _vp]),
+        "orc_conv2d": (_int, [_vp, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -108,6 +109,7 @@ def reference():
             "ref_upsample": (_int, [_vp, _sz, _sz, _sz, _vp]),
             "ref_shortcut": (_sz, [_vp, _sz, _sz, _sz, _sz, _sz, _int, _int, _vp, _sz]),
             "ref_model_probe": (_sz, [ctypes.c_char_p, _int, ctypes.c_char_p, _sz]),
+            "ref_conv": (_sz, [_vp, _sz, _sz, _sz, _vp, _u32, _sz, _sz, _sz, _vp, _int, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -367,3 +369,42 @@ def shortcut(lib, prefix, x, width, height, channels, temporal, up, spatial):
         return out if n == out.size else None
     ok = lib.orc_shortcut(ptr(x), width, height, x.shape[1], channels, temporal, int(up), int(spatial), ptr(out))
     return out if ok else None
+
+
+def conv_out_size(width, height, kx, ky, geometry):
+    sx, sy, left, right, top, bottom = geometry
+    return (width + left + right - kx) // sx + 1, (height + top + bottom - ky) // sy + 1
+
+
+def same_geometry(kx, ky):
+    """tensor_conv's first form as a geometry: stride 1, the kernel centred."""
+    return (1, 1, kx // 2, kx - 1 - kx // 2, ky // 2, ky - 1 - ky // 2)
+
+
+def conv2d(lib, x, width, height, weight, kx, ky, bias=None, geometry=None):
+    """orc_conv2d: x [width*height][cin], weight fp32 [cout][cin*ky*kx] (the
+    GGUF [kx, ky, cin, cout] order), geometry (sx, sy, left, right, top,
+    bottom) or None for the first form."""
+    x = _f32(x)
+    w = _f32(weight)
+    cout = w.shape[0]
+    g = geometry or same_geometry(kx, ky)
+    ow, oh = conv_out_size(width, height, kx, ky, g)
+    out = np.full((ow * oh, cout), np.nan, np.float32)
+    b = None if bias is None else _f32(bias)
+    ok = lib.orc_conv2d(ptr(x), width, height, x.shape[1], ptr(w), kx, ky, cout, None if b is None else ptr(b), *g, ptr(out))
+    return out if ok else None
+
+
+def conv2d_ref(ref, x, width, height, wbytes, wtype, kx, ky, cin, cout, bias=None, geometry=None):
+    """The reference's tensor_conv (first form when geometry is None, then
+    with the bias it requires), through oracle/_ref."""
+    x = _f32(x)
+    wb = np.ascontiguousarray(wbytes, dtype=np.uint8)
+    g = geometry or same_geometry(kx, ky)
+    ow, oh = conv_out_size(width, height, kx, ky, g)
+    out = np.full((ow * oh, cout), np.nan, np.float32)
+    b = None if bias is None else _f32(bias)
+    n = ref.ref_conv(ptr(x), width, height, cin, ptr(wb), wtype, kx, ky, cout, None if b is None else ptr(b), 0 if geometry is None else 1,
+                     *g, ptr(out), out.size)
+    return out if n == out.size else None

@@ -12,7 +12,7 @@ import pytest
 from oracle_lib import (BF16, F16, F32, OP_AFFINE, OP_EULER, OP_PATCH, OP_RESIDUAL, OP_UNPATCH, OP_UPSAMPLE, ORACLE_DIR, Q5_K,
                         Q6_K, Q8_0, add, attention, bias, channel_op, decode_f32, dot, gather, gelu, groupnorm, l2norm, layout,
                         load_oracle, modulate_rows, norm_rows, oracle, ptr, quant_matmul, quantize, qwen_modulate, rope, scatter,
-                        shortcut, silu_gate)
+                        shortcut, silu_gate, conv2d)
 from pixelina_amd import synth
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -368,6 +368,8 @@ MUTANTS = {
     28: "qwen modulation with the two parameter rows swapped",
     29: "residual gate without tanh",
     30: "affine adding the bias before the scale",
+    31: "convolution patches with the kernel's x and y swapped",
+    32: "convolution padding taken from the right instead of the left",
 }
 
 
@@ -411,6 +413,39 @@ def golden_mismatches(lib):
         got = attention(lib, "orc", g9[f"c{c}_q"], g9[f"c{c}_k"], g9[f"c{c}_v"], heads, kvh, ranges, offset, causal=bool(causal))
         bad += int(got is None or not np.array_equal(got.view(np.uint32), g9[f"c{c}_y"].view(np.uint32)))
     bad += tensor_ops_mismatches(lib)
+    bad += conv_mismatches(lib)
+    return bad
+
+
+def g11_weight(g, c):
+    """The fp32 values of case c's weight [cout][cin*ky*kx] (F32, F16 or BF16 bytes)."""
+    wd, ht, cin, cout, kx, ky, wtype, _ = (int(v) for v in g[f"c{c}_shape"])
+    raw = g[f"c{c}_w"]
+    if wtype == 1:
+        w = raw.view(np.float16).astype(np.float32)
+    elif wtype == 30:
+        w = (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        w = raw.view(np.float32)
+    return w.reshape(cout, cin * ky * kx)
+
+
+def conv_mismatches(lib, tol=1e-5):
+    """How many g11 cases (the reference's tensor_conv) the oracle's
+    orc_conv2d misses by more than `tol` of an output row's largest value
+    (the oracle sums in double, the reference in fp32 FMA tiles)."""
+    g = np.load(os.path.join(GOLDEN, "g11_conv.npz"))
+    bad = 0
+    for c in range(int(g["count"])):
+        wd, ht, cin, cout, kx, ky, wtype, has_bias = (int(v) for v in g[f"c{c}_shape"])
+        geom = tuple(int(v) for v in g[f"c{c}_geometry"]) or None
+        y = conv2d(lib, g[f"c{c}_x"], wd, ht, g11_weight(g, c), kx, ky, g[f"c{c}_b"] if has_bias else None, geom)
+        want = g[f"c{c}_y"]
+        if y is None or y.shape != want.shape:
+            bad += 1
+            continue
+        err = np.abs(y.astype(np.float64) - want).max(axis=1) / np.maximum(np.abs(want).max(axis=1), 1e-30)
+        bad += int(err.max() > tol)
     return bad
 
 

@@ -13,7 +13,8 @@ import pytest
 
 from oracle_lib import (BF16, F16, F32, Q5_K, Q6_K, Q8_0, decode_f32, gather, groupnorm, l2norm, oracle, reference, scatter,
                         shortcut, upsample_ref, layout, OP_UPSAMPLE)
-from test_oracle_pins import q5_K_ints, q6_K_ints, surface_mismatches, tensor_ops_mismatches
+from oracle_lib import conv2d, conv2d_ref
+from test_oracle_pins import conv_mismatches, q5_K_ints, q6_K_ints, surface_mismatches, tensor_ops_mismatches
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 needs_ref = pytest.mark.skipif(reference() is None, reason="oracle/_ref not built here")
@@ -162,3 +163,51 @@ def test_tensor_ops_equal_compiled_reference(seed):
         xi = rng.standard_normal((wd * ht, cin)).astype(np.float32)
         a, b = shortcut(o, "orc", xi, wd, ht, ch, t, up, sp), shortcut(r, "ref", xi, wd, ht, ch, t, up, sp)
         assert a is not None and b is not None and np.array_equal(bits(a), bits(b)), (wd, ht, cin, ch, t, up, sp)
+
+
+def test_conv_matches_reference_vectors():
+    assert conv_mismatches(oracle()) == 0
+
+
+def test_conv_closed_forms():
+    """A 1x1 identity kernel copies the image; a 3x3 kernel with one tap at
+    (kx, ky) shifts it by (kx - 1, ky - 1) with zeros past the border; stride 2
+    with padding (0, 1, 0, 1) keeps the even pixels of a 1x1-kernel image;
+    the bias is added per output channel."""
+    o = oracle()
+    rng = np.random.default_rng(65)
+    w_, h_, c = 7, 5, 4
+    x = rng.standard_normal((w_ * h_, c)).astype(np.float32)
+    y = conv2d(o, x, w_, h_, np.eye(c, dtype=np.float32), 1, 1)
+    assert np.array_equal(y, x)
+    img = x.reshape(h_, w_, c)
+    for kx, ky in ((0, 0), (2, 1), (1, 2)):
+        wt = np.zeros((c, c, 3, 3), np.float32)  # [cout][cin][ky][kx]
+        for i in range(c):
+            wt[i, i, ky, kx] = 1.0
+        y = conv2d(o, x, w_, h_, wt.reshape(c, -1), 3, 3).reshape(h_, w_, c)
+        want = np.zeros_like(img)
+        dy, dx = ky - 1, kx - 1
+        ys, xs = slice(max(0, -dy), min(h_, h_ - dy)), slice(max(0, -dx), min(w_, w_ - dx))
+        want[ys, xs] = img[max(0, dy):h_ + min(0, dy), max(0, dx):w_ + min(0, dx)]
+        assert np.array_equal(y, want), (kx, ky)
+    y = conv2d(o, x, w_, h_, np.eye(c, dtype=np.float32), 1, 1, None, (2, 2, 0, 1, 0, 1)).reshape(3, 4, c)
+    assert np.array_equal(y[:, :, :], np.pad(img, ((0, 1), (0, 1), (0, 0)))[0::2, 0::2][:3, :4])
+    b = rng.standard_normal(c).astype(np.float32)
+    assert np.array_equal(conv2d(o, x, w_, h_, np.eye(c, dtype=np.float32), 1, 1, b), x + b)
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [1, 2])
+def test_conv_equals_compiled_reference(seed):
+    o, r = oracle(), reference()
+    rng = np.random.default_rng(800 + seed)
+    for wd, ht, cin, cout, kx, ky, geom in ((13, 9, 32, 24, 3, 3, None), (10, 8, 5, 7, 3, 3, (2, 1, 1, 0, 2, 1)),
+                                           (6, 6, 16, 16, 1, 1, None), (9, 11, 8, 12, 1, 3, (1, 2, 0, 0, 1, 1))):
+        x = rng.standard_normal((wd * ht, cin)).astype(np.float32)
+        w = (rng.standard_normal((cout, cin * kx * ky)) * 0.2).astype(np.float32)
+        b = rng.standard_normal(cout).astype(np.float32)
+        a = conv2d(o, x, wd, ht, w, kx, ky, b, geom)
+        c = conv2d_ref(r, x, wd, ht, w.view(np.uint8), 0, kx, ky, cin, cout, b, geom)
+        assert a is not None and c is not None
+        assert np.abs(a.astype(np.float64) - c).max() <= 1e-5 * np.abs(c).max()
