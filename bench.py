@@ -16,8 +16,8 @@ linear of a Z-Image DiT block at M = 4608 and of a Qwen-Image edit block at
 M = 8448, each linear and the block back to back), the same step with host
 (pinned) operands staged over PCIe, self-attention at the DiT block's shape
 (30 heads of 128 over 4608 tokens), the rest of the op surface (`surface`:
-norms, layouts and row moves at the models' shapes, against the HBM peak), and
-the reference CPU path
+norms, layouts and row moves at the models' shapes, against the HBM peak), VAE
+convolutions (`conv`, against the bf16 MFMA peak), and the reference CPU path
 (cpu_quant_matmul, tensor_attention) timed on this host on the same inputs.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-blocks]
@@ -500,6 +500,44 @@ def bench_surface(sess, _lib):
     return out
 
 
+# VAE convolutions (implicit GEMM on split-bf16 MFMA): (width, height, cin, cout, kernel)
+CONV_CASES = [(256, 256, 512, 512, 3), (1024, 1024, 128, 128, 3), (128, 128, 16, 512, 3)]
+
+
+def bench_conv(sess, _lib):
+    """tensor_conv at VAE decoder shapes with F16 weights.  Algorithmic work
+    2 * pixels * cout * cin * k^2; the kernel runs each product as three bf16
+    MFMA terms, so its matrix-core work is 3x that, priced against the dense
+    bf16 peak."""
+    rng = np.random.default_rng(66)
+    out = {}
+    for wd, ht, cin, cout, k in CONV_CASES:
+        w = (rng.standard_normal((cout, cin * k * k)) / np.sqrt(cin * k * k)).astype(np.float16)
+        h = sess.conv_weight(f"bench:conv:{wd}:{cin}:{cout}", w.view(np.uint8), 1, k, k, cin, cout)
+        xb = sess.to_device(np.resize(rng.standard_normal(1 << 20).astype(np.float32), (wd * ht, cin)))
+        bb = sess.to_device(rng.standard_normal(cout).astype(np.float32))
+        yb = sess.alloc(wd * ht * cout * 4)
+
+        def run():
+            _lib.check(sess.conv2d(h, xb.ptr, wd, ht, yb.ptr, None, bb.ptr), "conv2d")
+
+        ms, n = timed_series(sess, run, 5)
+        for b in (xb, bb, yb):
+            b.free()
+        flops = 2.0 * wd * ht * cout * cin * k * k
+        tf = flops / (ms * 1e-3) / 1e12
+        name = f"conv{k}x{k}_{wd}x{ht}_{cin}to{cout}"
+        out[name] = {"workload": f"VAE conv {k}x{k}, {wd}x{ht} pixels, {cin} -> {cout} channels, F16 weights, bias",
+                     "us": round(ms * 1e3, 1), "tflops": round(tf, 1), "reps": n,
+                     "roofline": {"kernel": "conv_kernel<%s>" % ("true" if cin % 32 == 0 else "false"), "bound": "mfma",
+                                  "achieved": round(3 * tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": round(3 * tf / PEAK_BF16_TFLOPS, 4),
+                                  "work_per_launch": f"3 x 2*pixels*cout*cin*k^2 = {3 * flops:.4e} bf16 MFMA flops"}}
+        log(f"{name}: {ms * 1e3:.0f} us, {tf:.1f} TFLOP/s ({3 * tf:.0f} TFLOP/s of bf16 MFMA work, "
+            f"{3 * tf / PEAK_BF16_TFLOPS:.1%} of peak)")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -515,6 +553,7 @@ def main():
     ap.add_argument("--no-pcie", action="store_true", help="skip the host-operand (PCIe-inclusive) step")
     ap.add_argument("--no-attention", action="store_true", help="skip the DiT-shape attention")
     ap.add_argument("--no-surface", action="store_true", help="skip the norms, layouts and row moves")
+    ap.add_argument("--no-conv", action="store_true", help="skip the VAE convolutions")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one plain 512 MiB device copy (the calibration kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -589,6 +628,7 @@ def main():
         fused = {} if args.no_fused else bench_fused(sess, synth, _lib, Q5_K, Q8_0, args.steps)
         attention, attn_data = (None, None) if args.no_attention else bench_attention(sess, synth, _lib, args.steps)
         surface = None if args.no_surface else bench_surface(sess, _lib)
+        conv = None if args.no_conv else bench_conv(sess, _lib)
         if args.calibrate_copy:
             src, dst = sess.alloc(COPY_BYTES), sess.alloc(COPY_BYTES)
             sess.copy_device(dst.ptr, src.ptr, COPY_BYTES)
@@ -641,6 +681,8 @@ def main():
         line["attention"] = attention
     if surface:
         line["surface"] = surface
+    if conv:
+        line["conv"] = conv
     if workloads:
         line["workloads"] = workloads
     if pcie:

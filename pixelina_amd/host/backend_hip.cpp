@@ -334,6 +334,23 @@ bool hip_shortcut(const float* source, size_t width, size_t height, size_t sourc
     return s && pixhip_shortcut(s,source,width,height,source_channels,destination,channels,temporal,up? 1 : 0,spatial? 1 : 0) == PIXHIP_OK;
 }
 
+pixhip_weight* hip_conv_weight(const std::string &key, const void* host_bytes, uint64_t bytes, uint32_t type, uint64_t kernel_x,
+                               uint64_t kernel_y, uint64_t in_channels, uint64_t out_channels)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    pixhip_weight* w = nullptr;
+    if (!s || pixhip_conv_weight_get(s,key.c_str(),host_bytes,bytes,type,kernel_x,kernel_y,in_channels,out_channels,&w) != PIXHIP_OK)
+        return nullptr;
+    return w;
+}
+
+bool hip_conv2d(pixhip_weight* weight, const float* input, size_t width, size_t height, const pixhip_conv_geometry* geometry,
+                const float* bias, float* output)
+{
+    pixhip_session* s = hip_state_session(active_state);
+    return s && weight && pixhip_conv2d(s,weight,input,width,height,geometry,bias,output) == PIXHIP_OK;
+}
+
 bool hip_available(std::string &description)
 {
     HipSession session;

@@ -180,6 +180,25 @@ bool hip_layout(unsigned operation, const float* source, size_t source_rows, siz
 bool hip_shortcut(const float* source, size_t width, size_t height, size_t source_channels, float* destination, size_t channels,
                   size_t temporal, bool up, bool spatial);
 
+// vulkan_conv (src/backend_vulkan.h:146-147): the cached convolution weight of
+// a model file's float tensor [kx, ky, cin, cout] (rank 5 with a unit third
+// dimension accepted), keyed as hip_weight_of keys linear weights, and the
+// convolution itself (geometry NULL: tensor_conv's first form).
+pixhip_weight* hip_conv_weight(const std::string &key, const void* host_bytes, uint64_t bytes, uint32_t type, uint64_t kernel_x,
+                               uint64_t kernel_y, uint64_t in_channels, uint64_t out_channels);
+bool hip_conv2d(pixhip_weight* weight, const float* input, size_t width, size_t height, const pixhip_conv_geometry* geometry,
+                const float* bias, float* output);
+
+template <class File, class Weight>
+pixhip_weight* hip_conv_weight_of(const File &file, const Weight &weight)
+{
+    const size_t rank = weight.shape.size();
+    if ((rank != 4 && rank != 5) || (rank == 5 && weight.shape[2] != 1)) return nullptr;
+    const std::string key = file.filename + ":" + weight.name + ":" + std::to_string(weight.offset) + ":" + std::to_string(weight.bytes);
+    return hip_conv_weight(key,file.data + weight.offset,weight.bytes,weight.type,weight.shape[0],weight.shape[1],weight.shape[rank - 2],
+                           weight.shape[rank - 1]);
+}
+
 bool hip_available(std::string &description);
 
 #endif /* PIXELINA_BACKEND_HIP_H */
