@@ -529,7 +529,7 @@ def bench_conv(sess, _lib):
         name = f"conv{k}x{k}_{wd}x{ht}_{cin}to{cout}"
         out[name] = {"workload": f"VAE conv {k}x{k}, {wd}x{ht} pixels, {cin} -> {cout} channels, F16 weights, bias",
                      "us": round(ms * 1e3, 1), "tflops": round(tf, 1), "reps": n,
-                     "roofline": {"kernel": "conv_kernel<%s>" % ("true" if cin % 32 == 0 else "false"), "bound": "mfma",
+                     "roofline": {"kernel": "conv_image_kernel" if cin % 32 == 0 else "conv_gather_kernel", "bound": "mfma",
                                   "achieved": round(3 * tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                                   "frac": round(3 * tf / PEAK_BF16_TFLOPS, 4),
                                   "work_per_launch": f"3 x 2*pixels*cout*cin*k^2 = {3 * flops:.4e} bf16 MFMA flops"}}

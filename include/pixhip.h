@@ -493,7 +493,8 @@ int pixhip_conv_weight_get(pixhip_session* session, const char* key, const void*
  * kernel_x) / stride_x + 1 (and likewise in y), with the reference's checks.
  * Within 1e-4 of the fp32 reference per output row (split-bf16 MFMA products,
  * fp32 accumulation).  Tensors are device or pinned host memory (input and
- * bias may be pageable), 4-byte aligned. */
+ * bias may be pageable), 4-byte aligned.  Images of more than 2^32 - 1 pixels
+ * are PIXHIP_ERR_ARGUMENT. */
 int pixhip_conv2d(pixhip_session* session, const pixhip_weight* weight, const float* input, size_t width, size_t height,
                   const pixhip_conv_geometry* geometry, const float* bias, float* output);
 

@@ -1777,8 +1777,8 @@ int pixhip_conv2d(pixhip_session* s, const pixhip_weight* wc, const float* input
     if (pw < w->kernel_x || ph < w->kernel_y) return fail(PIXHIP_ERR_ARGUMENT,"the padded image is smaller than the kernel");
     const size_t ow = (pw - w->kernel_x) / g.stride_x + 1, oh = (ph - w->kernel_y) / g.stride_y + 1;
     if (width > INT32_MAX / 2 || height > INT32_MAX / 2 || pw > INT32_MAX / 2 || ph > INT32_MAX / 2 || g.stride_x > INT32_MAX ||
-        g.stride_y > INT32_MAX || ow > SIZE_MAX / oh)
-        return fail(PIXHIP_ERR_ARGUMENT,"image too large");
+        g.stride_y > INT32_MAX || ow > SIZE_MAX / oh || width * height > UINT32_MAX)
+        return fail(PIXHIP_ERR_ARGUMENT,"image too large");  // pixel indices are 32-bit in the kernel
     size_t in_bytes = 0, out_bytes = 0;
     if (width * height > SIZE_MAX / w->cin / 4 || ow * oh > SIZE_MAX / w->rows / 4) return fail(PIXHIP_ERR_ARGUMENT,"image too large");
     in_bytes = width * height * w->cin * 4;

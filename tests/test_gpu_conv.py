@@ -159,6 +159,7 @@ def test_errors(sess):
     x, y = sess.alloc(16 * 8 * 4), sess.alloc(64 * 4 * 4)
     assert sess.conv2d(w, x.ptr, 4, 4, y.ptr, (0, 1, 1, 1, 1, 1)) == arg         # stride 0
     assert sess.conv2d(w, x.ptr, 1, 1, y.ptr, (1, 1, 0, 0, 0, 0)) == arg         # padded image smaller than the kernel
+    assert sess.conv2d(w, x.ptr, 1 << 16, 1 << 16, y.ptr) == arg                  # 2^32 pixels (indices are 32-bit)
     assert sess.matmul(w, x.ptr, 2, y.ptr) == uns                                # not a linear weight
     x.free()
     y.free()
