@@ -59,6 +59,16 @@ __device__ __forceinline__ void split2(float x, uint32_t& hi, uint32_t& lo)
     lo = bf16_rne(x - __uint_as_float(hi << 16));
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two values rounded to bf16 (nearest even) by v_cvt_pk_bf16_f32, a in the
+// low half.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b)
+{
+    const bf16x2 h = {(__bf16)a,(__bf16)b};
+    return __builtin_bit_cast(uint32_t,h);
+}
+
 // ---------------------------------------------------------------- split pass
 
 // src [n][stride] fp32, head h's values at h*dim; planes [heads][npad][D] bf16
@@ -304,8 +314,8 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
         }
     };
     // Online softmax of one half (keys key0 + 8(r/4) + 4hh + r%4) -> P^T as
-    // bf16 pairs for its two k-steps: hi = the top half of p, lo = p - hi
-    // rounded to nearest even.
+    // bf16 pairs for its two k-steps: hi = p rounded to nearest even, lo =
+    // p - hi rounded likewise (six vector instructions per pair).
     auto softmax = [&](v16f& sv, int key0, uint32_t (&ph)[2][4], uint32_t (&pl)[2][4]) {
         const bool edge = key0 + 32 > wave_limit;
         float mx = -INFINITY;
@@ -335,12 +345,10 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
             const float p1 = __builtin_amdgcn_exp2f(sv[r + 1] - m_ref);
             l_run += p0;
             l_run += p1;
-            const uint32_t u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
-            const uint32_t r0 = __float_as_uint(p0 - __uint_as_float(u0 & 0xFFFF0000u));
-            const uint32_t r1 = __float_as_uint(p1 - __uint_as_float(u1 & 0xFFFF0000u));
+            const uint32_t h = pack_bf16(p0,p1);
             const int t = r / 8, w = (r % 8) / 2;
-            ph[t][w] = __builtin_amdgcn_perm(u1,u0,0x07060302u);
-            pl[t][w] = __builtin_amdgcn_perm(r1 + 0x7FFFu + ((r1 >> 16) & 1u),r0 + 0x7FFFu + ((r0 >> 16) & 1u),0x07060302u);
+            ph[t][w] = h;
+            pl[t][w] = pack_bf16(p0 - __uint_as_float(h << 16),p1 - __uint_as_float(h & 0xFFFF0000u));
         }
     };
     // O^T += V^T * P^T over the half's two 16-key k-steps

@@ -51,6 +51,24 @@ __device__ __forceinline__ void halves(float x, uint32_t& hi, uint32_t& lo)
     lo = rne16(x - __uint_as_float(hi << 16));
 }
 
+typedef __bf16 cbf16x2 __attribute__((ext_vector_type(2)));
+
+// Two values rounded to bf16 (nearest even) by v_cvt_pk_bf16_f32; a in the
+// low half.  For finite values the same bits as rne16.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b)
+{
+    const cbf16x2 h = {(__bf16)a,(__bf16)b};
+    return __builtin_bit_cast(uint32_t,h);
+}
+
+// The split of a pair: hi = both values rounded to bf16, lo = the remainders
+// rounded to bf16 (six vector instructions for two values).
+__device__ __forceinline__ void halves2(float a, float b, uint32_t& hi, uint32_t& lo)
+{
+    hi = pack_bf16(a,b);
+    lo = pack_bf16(a - __uint_as_float(hi << 16),b - __uint_as_float(hi & 0xFFFF0000u));
+}
+
 __device__ __forceinline__ float weight_value(const uint8_t* raw, uint32_t type, size_t index)
 {
     if (type == PIX_F32) {
@@ -170,13 +188,11 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
             for (int i = 0; i < AV; i++) {
                 const int row = t / 8 + 32 * i, col = (t % 8) * 4;
                 const float4 v = ain[i]? ra[i] : make_float4(0.0f,0.0f,0.0f,0.0f);
-                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-                halves(v.x,h0,l0);
-                halves(v.y,h1,l1);
-                halves(v.z,h2,l2);
-                halves(v.w,h3,l3);
-                *reinterpret_cast<uint2*>(st + row * kCRow + col) = make_uint2(h0 | (h1 << 16),h2 | (h3 << 16));
-                *reinterpret_cast<uint2*>(st + PA + row * kCRow + col) = make_uint2(l0 | (l1 << 16),l2 | (l3 << 16));
+                uint32_t h01, l01, h23, l23;
+                halves2(v.x,v.y,h01,l01);
+                halves2(v.z,v.w,h23,l23);
+                *reinterpret_cast<uint2*>(st + row * kCRow + col) = make_uint2(h01,h23);
+                *reinterpret_cast<uint2*>(st + PA + row * kCRow + col) = make_uint2(l01,l23);
             }
         } else {
 #pragma unroll
