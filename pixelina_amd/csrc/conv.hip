@@ -52,6 +52,13 @@ __device__ __forceinline__ void halves(float x, uint32_t& hi, uint32_t& lo)
 }
 
 typedef __bf16 cbf16x2 __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t CRsrc;
+
+// Raw buffer of `bytes` bytes (stride 0): loads at or past the end read zeros.
+__device__ __forceinline__ CRsrc conv_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base),(short)0,(int)bytes,0x00020000);
+}
 
 // Two values rounded to bf16 (nearest even) by v_cvt_pk_bf16_f32; a in the
 // low half.  For finite values the same bits as rne16.
@@ -112,14 +119,20 @@ hipError_t launch_conv_form(const void* raw, uint32_t type, int kernel_x, int ke
     return hipGetLastError();
 }
 
-// FAST: cin % 32 == 0 and the image 16-byte aligned (a stage is one tap of 32
-// consecutive channels, read as float4); else each inner value is gathered on
-// its own (the first layer's 3 or 16 channels).  Each wave owns MT = 2 tiles
-// of 32 pixels by 2 of 32 channels (a 256-pixel workgroup tile with 128 x 64
-// per wave ran 27% slower).
-template <bool FAST>
+// MODE 1 and 2: cin % 32 == 0 and the image 16-byte aligned (a stage is one
+// tap of 32 consecutive channels, read as float4); MODE 0: each inner value is
+// gathered on its own (the first layer's 3 or 16 channels).  MODE 2 reads the
+// image and the weight planes with buffer loads at 32-bit offsets (images
+// below 2 GiB): a lane's image offsets are worked out once per kernel tap
+// (every cin / 32 stages), and a tap outside the image gets an offset past the
+// buffer's end, which the hardware reads as zeros.  MODE 1 is the same with
+// 64-bit addresses, for larger images.  Each wave owns MT = 2 tiles of 32
+// pixels by 2 of 32 channels (a 256-pixel workgroup tile with 128 x 64 per
+// wave ran 27% slower).
+template <int MODE>
 __device__ __forceinline__ void conv_body(const ConvArgs& a)
 {
+    constexpr bool FAST = MODE != 0, BUF = MODE == 2;
     constexpr int MT = 2;
     constexpr int BM = 64 * MT;                        // workgroup pixels
     constexpr int PA = BM * kCRow, PB = kCN * kCRow;   // bf16 per A / B plane
@@ -150,9 +163,43 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
     bool ain[FAST? AV : 1];
     float rs[FAST? 1 : AV];
     cu32x4 rb[4];
+    // MODE 2: buffer resources, this lane's weight offsets (bytes, without the
+    // stage's k) and image offsets for the current tap
+    constexpr uint32_t kOut = 0x80000000u;  // past the end of any buffered image
+    const uint32_t wbytes = BUF? (uint32_t)((size_t)a.Npad * a.Kp * 2) : 0u;
+    const CRsrc rx = conv_rsrc(a.x,BUF? (uint32_t)((size_t)a.W * a.H * a.C * 4) : 0u);
+    const CRsrc rwh = conv_rsrc(a.wh,wbytes), rwl = conv_rsrc(a.wl,wbytes);
+    uint32_t woff[4], aoff[AV];
+    int cur_tap = -1;
+    if constexpr (BUF) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
+            woff[j] = ((uint32_t)(n0 + row) * (uint32_t)a.Kp + (uint32_t)part * 8u) * 2u;
+        }
+    }
     auto fetch = [&](int stage) {
         const int k0 = stage * kCK;
-        if constexpr (FAST) {
+        if constexpr (BUF) {
+            const int tap = k0 / a.C;  // (uniform)
+            if (tap != cur_tap) {
+                cur_tap = tap;
+                const int ky = tap / a.KX, kx = tap % a.KX;
+#pragma unroll
+                for (int i = 0; i < AV; i++) {
+                    const int iy = iy0[i] + ky, ix = ix0[i] + kx;
+                    const bool in = iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+                    const uint32_t pix = (uint32_t)iy * (uint32_t)a.W + (uint32_t)ix;
+                    aoff[i] = in? (pix * (uint32_t)a.C + (uint32_t)(t % 8) * 4u) * 4u : kOut;
+                }
+            }
+            const uint32_t cb = (uint32_t)(k0 % a.C) * 4u;
+#pragma unroll
+            for (int i = 0; i < AV; i++) {
+                const cu32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx,aoff[i] + cb,0,0);
+                ra[i] = make_float4(__uint_as_float(v.x),__uint_as_float(v.y),__uint_as_float(v.z),__uint_as_float(v.w));
+            }
+        } else if constexpr (FAST) {
             const int tap = k0 / a.C, c = k0 % a.C + (t % 8) * 4;
             const int ky = tap / a.KX, kx = tap % a.KX;
             // every lane loads: a tap outside the image reads pixel 0 and
@@ -176,9 +223,13 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
         // B: 128 rows x 64 bytes per plane, two 16-byte pieces per thread per plane
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
-            const uint16_t* plane = (j < 2)? a.wh : a.wl;
-            rb[j] = *reinterpret_cast<const cu32x4*>(plane + (size_t)(n0 + row) * a.Kp + k0 + part * 8);
+            if constexpr (BUF) {
+                rb[j] = __builtin_amdgcn_raw_buffer_load_b128(j < 2? rwh : rwl,woff[j] + (uint32_t)k0 * 2u,0,0);
+            } else {
+                const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
+                const uint16_t* plane = (j < 2)? a.wh : a.wl;
+                rb[j] = *reinterpret_cast<const cu32x4*>(plane + (size_t)(n0 + row) * a.Kp + k0 + part * 8);
+            }
         }
     };
     auto store = [&]() {
@@ -187,7 +238,7 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
 #pragma unroll
             for (int i = 0; i < AV; i++) {
                 const int row = t / 8 + 32 * i, col = (t % 8) * 4;
-                const float4 v = ain[i]? ra[i] : make_float4(0.0f,0.0f,0.0f,0.0f);
+                const float4 v = BUF || ain[i]? ra[i] : make_float4(0.0f,0.0f,0.0f,0.0f);
                 uint32_t h01, l01, h23, l23;
                 halves2(v.x,v.y,h01,l01);
                 halves2(v.z,v.w,h23,l23);
@@ -276,12 +327,17 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3,3))) void conv_image_kernel(ConvArgs a)
 {
-    conv_body<true>(a);
+    conv_body<2>(a);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3,3))) void conv_image_wide_kernel(ConvArgs a)
+{
+    conv_body<1>(a);
 }
 
 __global__ __launch_bounds__(256) void conv_gather_kernel(ConvArgs a)
 {
-    conv_body<false>(a);
+    conv_body<0>(a);
 }
 
 hipError_t launch_conv(const ConvArgs& a, hipStream_t s)
@@ -290,9 +346,11 @@ hipError_t launch_conv(const ConvArgs& a, hipStream_t s)
     const long long mt = (a.M + 127) / 128;
     if (mt > 0x7fffffffLL || a.Npad / kCN > 65535) return hipErrorInvalidValue;
     const dim3 grid((unsigned)mt,(unsigned)(a.Npad / kCN));
-    if (a.C % kCK == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0)
-        conv_image_kernel<<<grid,dim3(256),0,s>>>(a);
-    else
+    const bool narrow = (size_t)a.W * a.H * a.C * 4 < ((size_t)1 << 31) && (size_t)a.Npad * a.Kp * 2 < ((size_t)1 << 31);
+    if (a.C % kCK == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0) {
+        if (narrow) conv_image_kernel<<<grid,dim3(256),0,s>>>(a);
+        else conv_image_wide_kernel<<<grid,dim3(256),0,s>>>(a);
+    } else
         conv_gather_kernel<<<grid,dim3(256),0,s>>>(a);
     return hipGetLastError();
 }
