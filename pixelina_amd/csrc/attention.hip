@@ -297,20 +297,40 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
     float m_run = -INFINITY, l_run = 0.0f;
     const float c2 = a.scale * kLog2e;
 
-    // S^T = K * Q^T for the 32-key half u of the tile in `st`
-    auto score = [&](const uint8_t* st, int u, v16f& sv) {
-        sv = v16f{};
-        const int r = 32 * u + lr;
-        const uint8_t* rowh = st + r * (2 * D);
-        const uint8_t* rowl = st + PLANE + r * (2 * D);
+    // S^T = K * Q^T for both 32-key halves of the tile in `st`: the two
+    // halves' MFMA chains interleaved, each k-step's K fragments read while
+    // the previous k-step's MFMAs run.
+    auto score = [&](const uint8_t* st, v16f& s0, v16f& s1) {
+        s0 = v16f{};
+        s1 = v16f{};
+        const int r0 = lr, r1 = 32 + lr;
+        const uint8_t *h0 = st + r0 * (2 * D), *l0 = st + PLANE + r0 * (2 * D);
+        const uint8_t *h1 = st + r1 * (2 * D), *l1 = st + PLANE + r1 * (2 * D);
+        auto frag = [&](const uint8_t* row, int r, int k) { return lds_read<bf16x8>(row + 16 * ((2 * k + hh) ^ swz_k<D>(r))); };
+        bf16x8 a0h = frag(h0,r0,0), a0l = frag(l0,r0,0), a1h = frag(h1,r1,0), a1l = frag(l1,r1,0);
 #pragma unroll
         for (int k = 0; k < KS; k++) {
-            const int piece = (2 * k + hh) ^ swz_k<D>(r);
-            const bf16x8 ah = lds_read<bf16x8>(rowh + 16 * piece);
-            const bf16x8 al = lds_read<bf16x8>(rowl + 16 * piece);
-            sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfh[k],sv,0,0,0);
-            sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfl[k],sv,0,0,0);
-            sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,qfh[k],sv,0,0,0);
+            bf16x8 n0h, n0l, n1h, n1l;
+            if (k + 1 < KS) {
+                n0h = frag(h0,r0,k + 1);
+                n0l = frag(l0,r0,k + 1);
+                n1h = frag(h1,r1,k + 1);
+                n1l = frag(l1,r1,k + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // (the reads stay ahead of this k-step's MFMAs)
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0h,qfh[k],s0,0,0,0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1h,qfh[k],s1,0,0,0);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0h,qfl[k],s0,0,0,0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1h,qfl[k],s1,0,0,0);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0l,qfh[k],s0,0,0,0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1l,qfh[k],s1,0,0,0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + 1 < KS) {
+                a0h = n0h;
+                a0l = n0l;
+                a1h = n1h;
+                a1l = n1l;
+            }
         }
     };
     // Online softmax of one half (keys key0 + 8(r/4) + 4hh + r%4) -> P^T as
@@ -351,22 +371,35 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
             pl[t][w] = pack_bf16(p0 - __uint_as_float(h << 16),p1 - __uint_as_float(h & 0xFFFF0000u));
         }
     };
-    // O^T += V^T * P^T over the half's two 16-key k-steps
+    // O^T += V^T * P^T over the half's two 16-key k-steps; the V^T fragments
+    // of the next (k-step, output tile) are read while the current MFMAs run.
     auto pv = [&](const uint8_t* st, int u, const uint32_t (&ph)[2][4], const uint32_t (&pl)[2][4]) {
+        auto frag = [&](int plane, int j, int td) {
+            const int r = 32 * td + lr;
+            return lds_read<bf16x8>(st + plane * PLANE + r * 128 + 16 * ((2 * (2 * u + j) + hh) ^ swz_v(r)));
+        };
+        bf16x8 ah = frag(2,0,0), al = frag(3,0,0);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int t = 2 * u + j;
             const bf16x8 bh = __builtin_bit_cast(bf16x8,u32x4{ph[j][0],ph[j][1],ph[j][2],ph[j][3]});
             const bf16x8 bl = __builtin_bit_cast(bf16x8,u32x4{pl[j][0],pl[j][1],pl[j][2],pl[j][3]});
 #pragma unroll
             for (int td = 0; td < TD; td++) {
-                const int r = 32 * td + lr;
-                const int piece = (2 * t + hh) ^ swz_v(r);
-                const bf16x8 ah = lds_read<bf16x8>(st + 2 * PLANE + r * 128 + 16 * piece);
-                const bf16x8 al = lds_read<bf16x8>(st + 3 * PLANE + r * 128 + 16 * piece);
+                const int nj = td + 1 < TD? j : j + 1, ntd = td + 1 < TD? td + 1 : 0;
+                bf16x8 nh, nl;
+                if (nj < 2) {
+                    nh = frag(2,nj,ntd);
+                    nl = frag(3,nj,ntd);
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,bh,o[td],0,0,0);
                 o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,bl,o[td],0,0,0);
                 o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,bh,o[td],0,0,0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (nj < 2) {
+                    ah = nh;
+                    al = nl;
+                }
             }
         }
     };
@@ -382,8 +415,7 @@ __global__ __launch_bounds__(kAThreads, 1) void attn_kernel(AttnArgs a)
         const uint8_t* st = lds + (kt & 1) * STAGE;
         v16f s0, s1;
         uint32_t ph[2][4], pl[2][4];
-        score(st,0,s0);
-        score(st,1,s1);
+        score(st,s0,s1);
         __builtin_amdgcn_sched_barrier(0);
         softmax(s0,kt * kAK,ph,pl);
         __builtin_amdgcn_sched_barrier(0);
