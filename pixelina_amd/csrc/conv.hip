@@ -17,12 +17,14 @@
 // once, at upload; F16 and BF16 weights are exact in them).
 //
 // Tile: 128 pixels x 128 output channels x 32 inner per stage, 4 waves of
-// 64 x 64 (2 x 2 MFMA tiles), one 40 KB LDS stage of four planes (A hi / lo,
-// B hi / lo, rows padded to 80 bytes), the next stage's global loads held in
-// registers while the current one is multiplied.  The image kernel is built
-// for three waves per SIMD (at most 168 registers), so three workgroups share
-// a CU and cover each other's barriers and load latency: 1240 -> 1170 us at
-// 256 x 256 x 512 -> 512 against two LDS buffers at two waves per SIMD.
+// 64 x 64 (2 x 2 MFMA tiles).  The image kernel (images below 2 GiB) keeps one
+// LDS stage of the split image (hi / lo planes, 80-byte rows) and a two-slot
+// ring of the weight planes filled by L2 -> LDS transfers, with the image
+// loads two stages ahead in registers; it is built for three waves per SIMD
+// (at most 168 registers), so three workgroups share a CU.  Larger images and
+// channel counts that are not a multiple of 32 take a simpler single-stage
+// form (conv_body).
+
 #include <algorithm>
 
 #include "pixhip_device.h"
@@ -53,6 +55,32 @@ __device__ __forceinline__ void halves(float x, uint32_t& hi, uint32_t& lo)
 
 typedef __bf16 cbf16x2 __attribute__((ext_vector_type(2)));
 typedef __amdgpu_buffer_rsrc_t CRsrc;
+
+// One 1 KB L2 -> LDS transfer (lane l's 16 bytes to lds_dst + 16 l), written
+// as asm: issued through the builtin, the compiler makes every later LDS
+// access wait for all transfers in flight (it cannot tell them apart), which
+// would undo the ring.  The waits for these transfers are the explicit ones
+// before the barriers; the compiler's own counts for the image loads only
+// grow stronger from operations it does not see (the counter is in order).
+// s_nop 0: one wait state between writing M0 and the transfer that reads it.
+__device__ __forceinline__ void conv_dma(CRsrc r, const uint16_t* lds_dst, uint32_t voff, uint32_t soff)
+{
+    const uint32_t m = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)lds_dst;
+    __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :: "s"(__builtin_amdgcn_readfirstlane(m)), "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff))
+                     : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), then s_barrier: the wave's own LDS reads
+// and writes are done and all but its N newest vector-memory operations
+// (loads and L2 -> LDS transfers, counted in issue order) have completed.
+// (__syncthreads would also drain every outstanding load.)
+template <int N> __device__ __forceinline__ void conv_barrier()
+{
+    static_assert(N >= 0 && N < 16, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(N | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
+}
 
 // Raw buffer of `bytes` bytes (stride 0): loads at or past the end read zeros.
 __device__ __forceinline__ CRsrc conv_rsrc(const void* base, uint32_t bytes)
@@ -119,20 +147,17 @@ hipError_t launch_conv_form(const void* raw, uint32_t type, int kernel_x, int ke
     return hipGetLastError();
 }
 
-// MODE 1 and 2: cin % 32 == 0 and the image 16-byte aligned (a stage is one
-// tap of 32 consecutive channels, read as float4); MODE 0: each inner value is
-// gathered on its own (the first layer's 3 or 16 channels).  MODE 2 reads the
-// image and the weight planes with buffer loads at 32-bit offsets (images
-// below 2 GiB): a lane's image offsets are worked out once per kernel tap
-// (every cin / 32 stages), and a tap outside the image gets an offset past the
-// buffer's end, which the hardware reads as zeros.  MODE 1 is the same with
-// 64-bit addresses, for larger images.  Each wave owns MT = 2 tiles of 32
+// MODE 1: cin % 32 == 0 and the image 16-byte aligned (a stage is one tap of
+// 32 consecutive channels, read as float4) at 64-bit addresses, for images of
+// 2 GiB and more; MODE 0: each inner value is gathered on its own (the first
+// layer's 3 or 16 channels).  The next stage's loads are held in registers
+// while the current one is multiplied.  Each wave owns MT = 2 tiles of 32
 // pixels by 2 of 32 channels (a 256-pixel workgroup tile with 128 x 64 per
 // wave ran 27% slower).
 template <int MODE>
 __device__ __forceinline__ void conv_body(const ConvArgs& a)
 {
-    constexpr bool FAST = MODE != 0, BUF = MODE == 2;
+    constexpr bool FAST = MODE != 0;
     constexpr int MT = 2;
     constexpr int BM = 64 * MT;                        // workgroup pixels
     constexpr int PA = BM * kCRow, PB = kCN * kCRow;   // bf16 per A / B plane
@@ -163,43 +188,9 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
     bool ain[FAST? AV : 1];
     float rs[FAST? 1 : AV];
     cu32x4 rb[4];
-    // MODE 2: buffer resources, this lane's weight offsets (bytes, without the
-    // stage's k) and image offsets for the current tap
-    constexpr uint32_t kOut = 0x80000000u;  // past the end of any buffered image
-    const uint32_t wbytes = BUF? (uint32_t)((size_t)a.Npad * a.Kp * 2) : 0u;
-    const CRsrc rx = conv_rsrc(a.x,BUF? (uint32_t)((size_t)a.W * a.H * a.C * 4) : 0u);
-    const CRsrc rwh = conv_rsrc(a.wh,wbytes), rwl = conv_rsrc(a.wl,wbytes);
-    uint32_t woff[4], aoff[AV];
-    int cur_tap = -1;
-    if constexpr (BUF) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
-            woff[j] = ((uint32_t)(n0 + row) * (uint32_t)a.Kp + (uint32_t)part * 8u) * 2u;
-        }
-    }
     auto fetch = [&](int stage) {
         const int k0 = stage * kCK;
-        if constexpr (BUF) {
-            const int tap = k0 / a.C;  // (uniform)
-            if (tap != cur_tap) {
-                cur_tap = tap;
-                const int ky = tap / a.KX, kx = tap % a.KX;
-#pragma unroll
-                for (int i = 0; i < AV; i++) {
-                    const int iy = iy0[i] + ky, ix = ix0[i] + kx;
-                    const bool in = iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
-                    const uint32_t pix = (uint32_t)iy * (uint32_t)a.W + (uint32_t)ix;
-                    aoff[i] = in? (pix * (uint32_t)a.C + (uint32_t)(t % 8) * 4u) * 4u : kOut;
-                }
-            }
-            const uint32_t cb = (uint32_t)(k0 % a.C) * 4u;
-#pragma unroll
-            for (int i = 0; i < AV; i++) {
-                const cu32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx,aoff[i] + cb,0,0);
-                ra[i] = make_float4(__uint_as_float(v.x),__uint_as_float(v.y),__uint_as_float(v.z),__uint_as_float(v.w));
-            }
-        } else if constexpr (FAST) {
+        if constexpr (FAST) {
             const int tap = k0 / a.C, c = k0 % a.C + (t % 8) * 4;
             const int ky = tap / a.KX, kx = tap % a.KX;
             // every lane loads: a tap outside the image reads pixel 0 and
@@ -223,13 +214,9 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
         // B: 128 rows x 64 bytes per plane, two 16-byte pieces per thread per plane
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            if constexpr (BUF) {
-                rb[j] = __builtin_amdgcn_raw_buffer_load_b128(j < 2? rwh : rwl,woff[j] + (uint32_t)k0 * 2u,0,0);
-            } else {
-                const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
-                const uint16_t* plane = (j < 2)? a.wh : a.wl;
-                rb[j] = *reinterpret_cast<const cu32x4*>(plane + (size_t)(n0 + row) * a.Kp + k0 + part * 8);
-            }
+            const int q = t + 256 * (j & 1), row = q / 4, part = q % 4;
+            const uint16_t* plane = (j < 2)? a.wh : a.wl;
+            rb[j] = *reinterpret_cast<const cu32x4*>(plane + (size_t)(n0 + row) * a.Kp + k0 + part * 8);
         }
     };
     auto store = [&]() {
@@ -238,7 +225,7 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
 #pragma unroll
             for (int i = 0; i < AV; i++) {
                 const int row = t / 8 + 32 * i, col = (t % 8) * 4;
-                const float4 v = BUF || ain[i]? ra[i] : make_float4(0.0f,0.0f,0.0f,0.0f);
+                const float4 v = ain[i]? ra[i] : make_float4(0.0f,0.0f,0.0f,0.0f);
                 uint32_t h01, l01, h23, l23;
                 halves2(v.x,v.y,h01,l01);
                 halves2(v.z,v.w,h23,l23);
@@ -325,9 +312,185 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a)
 }
 
 
+// The image kernel for images below 2 GiB, pipelined deeper than conv_body:
+// the weight planes go L2 -> LDS by buffer_load ... lds into a two-slot ring
+// (64-byte rows, piece c of row r at c ^ ((r >> 2) & 3), no registers), and
+// the image loads run two stages ahead in two register sets, so a stage's
+// stores to LDS wait on loads issued a whole stage earlier.  LDS: one A stage
+// (hi, lo: 20 KB) + two B slots (hi, lo: 16 KB each) = 52 KB, three
+// workgroups per CU.
+__device__ __forceinline__ void conv_body_ring(const ConvArgs& a)
+{
+    constexpr int BM = 128, AV = 4;
+    constexpr int PA = BM * kCRow;   // bf16 per A plane (80-byte rows)
+    constexpr int PB = kCN * 32;     // bf16 per B plane (64-byte rows)
+    // (separate arrays: the compiler can then tell the image stores from the
+    // transfers in flight into the ring)
+    __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * PA];
+    __shared__ __attribute__((aligned(1024))) uint16_t bslot0[2 * PB];  // ring slots: planes hi, lo
+    __shared__ __attribute__((aligned(1024))) uint16_t bslot1[2 * PB];
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), lr = lane & 31, hh = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1;
+    const long long m0 = (long long)blockIdx.x * BM;
+    const int n0 = blockIdx.y * kCN;
+
+    int iy0[AV], ix0[AV];
+#pragma unroll
+    for (int i = 0; i < AV; i++) {
+        const long long m = m0 + t / 8 + 32 * i;
+        if (m < a.M) {
+            const int oy = (int)(m / a.OW), ox = (int)(m % a.OW);
+            iy0[i] = oy * a.SY - a.PT;
+            ix0[i] = ox * a.SX - a.PL;
+        } else {
+            iy0[i] = -(1 << 30);
+            ix0[i] = 0;
+        }
+    }
+    const uint32_t wbytes = (uint32_t)((size_t)a.Npad * a.Kp * 2);
+    const CRsrc rx = conv_rsrc(a.x,(uint32_t)((size_t)a.W * a.H * a.C * 4));
+    const CRsrc rwh = conv_rsrc(a.wh,wbytes), rwl = conv_rsrc(a.wl,wbytes);
+    // B DMA: the stage's 16 chunks of 1 KB (plane c / 8, rows 16 (c % 8) ..
+    // +15), chunk c = wave + 4i; lane l lands at row l / 4, physical piece l % 4
+    uint32_t bvo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = wave + 4 * i, row = 16 * (c % 8) + lane / 4, logical = (lane % 4) ^ ((row >> 2) & 3);
+        bvo[i] = ((uint32_t)(n0 + row) * (uint32_t)a.Kp + 8u * (uint32_t)logical) * 2u;
+    }
+    auto issue_b = [&](int stage, int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = wave + 4 * i;
+            uint16_t* dst = (slot? bslot1 : bslot0) + (c / 8) * PB + (c % 8) * 512;
+            conv_dma(c < 8? rwh : rwl,dst,bvo[i],(uint32_t)(stage * kCK * 2));
+        }
+    };
+    constexpr uint32_t kOut = 0x80000000u;
+    uint32_t aoff[AV];
+    int cur_tap = -1;
+    auto fetch_a = [&](int stage, float4 (&ra)[AV]) {
+        const int k0 = stage * kCK, tap = k0 / a.C;
+        if (tap != cur_tap) {
+            cur_tap = tap;
+            const int ky = tap / a.KX, kx = tap % a.KX;
+#pragma unroll
+            for (int i = 0; i < AV; i++) {
+                const int iy = iy0[i] + ky, ix = ix0[i] + kx;
+                const bool in = iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+                const uint32_t pix = (uint32_t)iy * (uint32_t)a.W + (uint32_t)ix;
+                aoff[i] = in? (pix * (uint32_t)a.C + (uint32_t)(t % 8) * 4u) * 4u : kOut;
+            }
+        }
+        const uint32_t cb = (uint32_t)(k0 % a.C) * 4u;
+#pragma unroll
+        for (int i = 0; i < AV; i++) {
+            const cu32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx,aoff[i] + cb,0,0);
+            ra[i] = make_float4(__uint_as_float(v.x),__uint_as_float(v.y),__uint_as_float(v.z),__uint_as_float(v.w));
+        }
+    };
+    auto store_a = [&](const float4 (&ra)[AV]) {
+#pragma unroll
+        for (int i = 0; i < AV; i++) {
+            const int row = t / 8 + 32 * i, col = (t % 8) * 4;
+            uint32_t h01, l01, h23, l23;
+            halves2(ra[i].x,ra[i].y,h01,l01);
+            halves2(ra[i].z,ra[i].w,h23,l23);
+            *reinterpret_cast<uint2*>(lds + row * kCRow + col) = make_uint2(h01,h23);
+            *reinterpret_cast<uint2*>(lds + PA + row * kCRow + col) = make_uint2(l01,l23);
+        }
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v16f{};
+    auto multiply = [&](int slot) {
+        const uint16_t* bs = slot? bslot1 : bslot0;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const int col = ks * 16 + 8 * hh;
+            cbf16x8 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int row = wn * 64 + j * 32 + lr;
+                const int at = row * 32 + (((2 * ks + hh) ^ ((row >> 2) & 3)) << 3);
+                bh[j] = *reinterpret_cast<const cbf16x8*>(bs + at);
+                bl[j] = *reinterpret_cast<const cbf16x8*>(bs + PB + at);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int row = wm * 64 + i * 32 + lr;
+                ah[i] = *reinterpret_cast<const cbf16x8*>(lds + row * kCRow + col);
+                al[i] = *reinterpret_cast<const cbf16x8*>(lds + PA + row * kCRow + col);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i],bh[j],acc[i][j],0,0,0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i],bl[j],acc[i][j],0,0,0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i],bh[j],acc[i][j],0,0,0);
+                }
+        }
+    };
+
+    // Before stage s: A of s in LDS, B of s in slot s % 2, the loads of A of
+    // s + 1 in flight in register set (s + 1) % 2.  Stage s issues B of s + 1
+    // (the other slot, read last in stage s - 1) and A of s + 2 (set s % 2,
+    // stored in stage s - 1), multiplies, and after a barrier waits for all
+    // but the four newest loads (A of s + 2), so B of s + 1 and A of s + 1
+    // have landed, and stores A of s + 1.
+    const int stages = a.Kp / kCK;
+    float4 ra0[AV], ra1[AV];
+    fetch_a(0,ra0);
+    issue_b(0,0);
+    // The image loads are issued unconditionally (past the last stage they
+    // read offsets of a further tap, in range or read as zeros, and are never
+    // stored), so every stage has the same four loads newest in the counter.
+    fetch_a(1,ra1);
+    store_a(ra0);
+    conv_barrier<4>();  // B of 0 landed (A of 1 may be in flight)
+    auto step = [&](int s, float4 (&mine)[AV], float4 (&next)[AV], int slot, bool more) {
+        if (more) issue_b(s + 1,slot ^ 1);
+        fetch_a(s + 2,mine);
+        multiply(slot);
+        if (more) {
+            conv_barrier<15>();  // every wave is done reading A of s and B slot s % 2
+            store_a(next);       // (the compiler waits for the loads of `next`)
+            conv_barrier<4>();   // B of s + 1 landed; A of s + 2 may be in flight
+        }
+    };
+    // Whole pairs in the loop (every step has a next stage, so the loop body
+    // has no path that leaves a register set's loads unwaited), then the
+    // last one or two stages.
+    int s = 0;
+    for (; s + 2 < stages; s += 2) {
+        step(s,ra0,ra1,0,true);
+        step(s + 1,ra1,ra0,1,true);
+    }
+    step(s,ra0,ra1,0,s + 1 < stages);
+    if (s + 1 < stages) step(s + 1,ra1,ra0,1,false);
+
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int n = n0 + wn * 64 + 32 * j + lr;
+        if (n >= a.N) continue;
+        const float b = a.bias? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const long long m = m0 + wm * 64 + 32 * i + 8 * (r / 4) + 4 * hh + r % 4;
+                if (m < a.M) a.y[(size_t)m * a.N + n] = a.bias? __fadd_rn(acc[i][j][r],b) : acc[i][j][r];
+            }
+    }
+}
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3,3))) void conv_image_kernel(ConvArgs a)
 {
-    conv_body<2>(a);
+    conv_body_ring(a);
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3,3))) void conv_image_wide_kernel(ConvArgs a)

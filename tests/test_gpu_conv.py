@@ -78,6 +78,9 @@ def test_reference_vectors(sess):
     (40, 30, 512, 256, 3, F32, (2, 2, 0, 1, 0, 1), True),  # the encoder's stride-2 downsample
     (64, 64, 16, 512, 3, F16, None, True),              # conv_in from 16 latent channels (gathered)
     (20, 15, 3, 128, 3, F32, None, True),               # RGB input
+    (19, 13, 32, 160, 1, F16, None, True),              # one 32-value stage (the pipelined kernel's tail alone)
+    (17, 11, 64, 96, 1, BF16, None, False),             # two stages
+    (23, 9, 96, 128, 1, F32, None, True),               # three stages
 ])
 def test_against_oracle(sess, wd, ht, cin, cout, k, wtype, geom, bias):
     rng = np.random.default_rng(wd * cin + cout)
