@@ -74,7 +74,9 @@ __device__ __forceinline__ void conv_dma(CRsrc r, const uint16_t* lds_dst, uint3
 // s_waitcnt vmcnt(N) lgkmcnt(0), then s_barrier: the wave's own LDS reads
 // and writes are done and all but its N newest vector-memory operations
 // (loads and L2 -> LDS transfers, counted in issue order) have completed.
-// (__syncthreads would also drain every outstanding load.)
+// (__syncthreads' workgroup fence must complete the wave's LDS writes, and
+// with the compiler's L2 -> LDS transfers in flight that means every
+// outstanding vector-memory operation.)
 template <int N> __device__ __forceinline__ void conv_barrier()
 {
     static_assert(N >= 0 && N < 16, "vmcnt range");
