@@ -125,6 +125,47 @@ def test_vae_shape_band_and_translation(sess):
     assert np.array_equal(y2[:, 2:-1].view(np.uint32), y1[:, 1:-2].view(np.uint32)), "not translation-equivariant"
 
 
+def test_wide_image(sess):
+    """An input of exactly 2 GiB (2048 rows x 1024 pixels x 256 channels),
+    which takes the 64-bit-address image kernel: a random pattern whose period
+    (1,000,003 values) is not a multiple of a row, uploaded once and repeated
+    by device copies; output rows 0-1 and the last two against the oracle run
+    on the input rows they read (the last ones lie past 2^31 bytes)."""
+    wd, ht, cin, cout = 1024, 2048, 256, 64
+    n = wd * ht * cin
+    assert n * 4 == 1 << 31
+    rng = np.random.default_rng(2048)
+    period = 1_000_003
+    base = rng.standard_normal(period).astype(np.float32)
+    pattern = lambda lo, hi: base[np.arange(lo, hi, dtype=np.int64) % period]
+    w = (rng.standard_normal((cout, cin * 9)) / np.sqrt(cin * 9)).astype(np.float32)
+    raw, wv = weight_bytes(w, F16)
+    b = rng.standard_normal(cout).astype(np.float32)
+    h = sess.conv_weight("wide", raw, F16, 3, 3, cin, cout)
+    xb = sess.alloc(n * 4)
+    yb = sess.alloc(wd * ht * cout * 4)
+    bb = sess.to_device(b)
+    try:
+        xb.upload(base)
+        for lo in range(period, n, period):
+            sess.copy_device(xb.ptr + lo * 4, xb.ptr, min(period, n - lo) * 4)
+        print("2 GiB input in place", flush=True)
+        _lib.check(sess.conv2d(h, xb.ptr, wd, ht, yb.ptr, None, bb.ptr), "pixhip_conv2d")
+        o = oracle()
+        row = wd * cin
+        for y0, r0, r1, geom in ((0, 0, 3, (1, 1, 1, 1, 1, 0)), (ht - 2, ht - 3, ht, (1, 1, 1, 1, 0, 1))):
+            band = pattern(r0 * row, r1 * row).reshape(-1, cin)
+            want = conv2d(o, band, wd, r1 - r0, wv, 3, 3, b, geom)
+            got = yb.download(np.float32, 2 * wd * cout, y0 * wd * cout * 4).reshape(-1, cout)
+            err = row_rel_error(got, want).max()
+            print(f"rows {y0}-{y0 + 1}: rel={err:.2e}", flush=True)
+            assert err <= TOL
+    finally:
+        sess.synchronize()
+        for buf in (xb, yb, bb):
+            buf.free()
+
+
 def test_weight_from_model_file(sess, tmp_path):
     """A rank-5 [3, 3, 1, cin, cout] F16 tensor (the Qwen VAE's causal 3-D
     conv with one time step) through pixhip_model_conv_weight."""
