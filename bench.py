@@ -75,9 +75,9 @@ def affinity_cores():
 
 
 def cpu_threads():
-    """Threads for the CPU reference: every core this process may run on, at
-    most 16 (the host-core share of one GPU on a shared multi-GPU node)."""
-    return max(1, min(affinity_cores(), 16))
+    """Threads for the CPU reference: every core this process may run on
+    (the reference's -t default is hardware_concurrency, src/tensor.cpp:97-101)."""
+    return max(1, affinity_cores())
 
 
 def cpu_info():
@@ -165,20 +165,26 @@ def timed_series(sess, run_once, min_reps, floor_ms=SERIES_FLOOR_MS):
 
 
 def workload_inputs(synth, name, m, row_scale, linears):
-    """Seeded inputs of one workload: one activation matrix per distinct K
-    (~N(0,1), times a per-token scale where given) and N(0, 0.02) weights, all
-    from numpy's PCG64 generator, the generator of the parity tests' block
-    workloads.  Q5_K weights are packed here; Q8_0 weights are returned as
-    float32 and quantized by the HIP quantizer (bit-exact quantize_row_q8_0_ref)."""
-    xs = {}
-    for i, k in enumerate(sorted({k for _, _, k, _ in linears})):
-        x = np.random.default_rng(500 + 7 * i + len(name)).standard_normal((m, k), dtype=np.float32)
+    """Seeded inputs of one workload, all SplitMix64 + Box-Muller streams with
+    the headline's seeds: one activation matrix per distinct K (ascending K),
+    drawn as consecutive pieces of stream 1337 (~N(0,1)); the per-token scales
+    (log-uniform, where given) from stream 1339, one piece per activation
+    matrix; the weights of the linears, in their listed order, as consecutive
+    pieces of stream 1338 (~N(0, 0.02)).  Q5_K weights are packed here; Q8_0
+    weights are returned as float32 and quantized by the HIP quantizer
+    (bit-exact quantize_row_q8_0_ref)."""
+    xs, at, st = {}, 0, 0
+    for k in sorted({k for _, _, k, _ in linears}):
+        x = synth.normal(synth.SEED_ACTIVATIONS, (m, k), start=at)
+        at += m * k + (m * k) % 2
         if row_scale:
-            x *= synth.log_uniform(600 + k, m, *row_scale)[:, None]
+            x *= synth.log_uniform(synth.SEED_OUTLIERS, m, *row_scale, start=st)[:, None]
+            st += m
         xs[k] = x
-    ws = {}
-    for j, (lin, wtype, k, n) in enumerate(linears):
-        wf = np.random.default_rng(700 + 13 * j + len(name)).standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+    ws, wt = {}, 0
+    for lin, wtype, k, n in linears:
+        wf = synth.normal(synth.SEED_WEIGHTS, (n, k), std=0.02, start=wt)
+        wt += n * k + (n * k) % 2
         ws[lin] = synth.pack_q5_K(wf) if wtype == "Q5_K" else wf
     return xs, ws
 
@@ -438,8 +444,7 @@ def cpu_attention(cpu, rec, data):
 SURFACE_ROTATE_BYTES = 1 << 30
 
 
-def bench_surface(sess, _lib):
-    rng = np.random.default_rng(55)
+def bench_surface(sess, synth, _lib):
     out = {}
 
     def case(name, text, nbytes, make, min_reps=20):
@@ -462,7 +467,8 @@ def bench_surface(sess, _lib):
                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "work_per_launch": f"{nbytes} bytes"}}
         log(f"{name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of HBM peak)")
 
-    block = rng.standard_normal(1 << 20).astype(np.float32)
+    # one SplitMix64 block (seed 1337) of 2^20 values, tiled over every operand
+    block = synth.normal(synth.SEED_ACTIVATIONS, (1 << 20,))
 
     def dev(shape, scale=1.0):
         return sess.to_device(np.resize(block * np.float32(scale), shape))
@@ -504,18 +510,20 @@ def bench_surface(sess, _lib):
 CONV_CASES = [(256, 256, 512, 512, 3), (1024, 1024, 128, 128, 3), (128, 128, 16, 512, 3)]
 
 
-def bench_conv(sess, _lib):
+def bench_conv(sess, synth, _lib):
     """tensor_conv at VAE decoder shapes with F16 weights.  Algorithmic work
     2 * pixels * cout * cin * k^2; the kernel runs each product as three bf16
     MFMA terms, so its matrix-core work is 3x that, priced against the dense
-    bf16 peak."""
-    rng = np.random.default_rng(66)
+    bf16 peak.  Inputs: SplitMix64 normals, weights from seed 1338 scaled by
+    1/sqrt(fan-in), the image a 2^20-value block of seed 1337 tiled over the
+    pixels, the bias from seed 1339."""
     out = {}
+    block = synth.normal(synth.SEED_ACTIVATIONS, (1 << 20,))
     for wd, ht, cin, cout, k in CONV_CASES:
-        w = (rng.standard_normal((cout, cin * k * k)) / np.sqrt(cin * k * k)).astype(np.float16)
+        w = (synth.normal(synth.SEED_WEIGHTS, (cout, cin * k * k)) / np.float32(np.sqrt(cin * k * k))).astype(np.float16)
         h = sess.conv_weight(f"bench:conv:{wd}:{cin}:{cout}", w.view(np.uint8), 1, k, k, cin, cout)
-        xb = sess.to_device(np.resize(rng.standard_normal(1 << 20).astype(np.float32), (wd * ht, cin)))
-        bb = sess.to_device(rng.standard_normal(cout).astype(np.float32))
+        xb = sess.to_device(np.resize(block, (wd * ht, cin)))
+        bb = sess.to_device(synth.normal(synth.SEED_OUTLIERS, (cout,)))
         yb = sess.alloc(wd * ht * cout * 4)
 
         def run():
@@ -627,8 +635,8 @@ def main():
             yvb.free()
         fused = {} if args.no_fused else bench_fused(sess, synth, _lib, Q5_K, Q8_0, args.steps)
         attention, attn_data = (None, None) if args.no_attention else bench_attention(sess, synth, _lib, args.steps)
-        surface = None if args.no_surface else bench_surface(sess, _lib)
-        conv = None if args.no_conv else bench_conv(sess, _lib)
+        surface = None if args.no_surface else bench_surface(sess, synth, _lib)
+        conv = None if args.no_conv else bench_conv(sess, synth, _lib)
         if args.calibrate_copy:
             src, dst = sess.alloc(COPY_BYTES), sess.alloc(COPY_BYTES)
             sess.copy_device(dst.ptr, src.ptr, COPY_BYTES)
@@ -655,7 +663,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic: SplitMix64 + Box-Muller, seeds 1337 (X), 1338 (W), 1339 (outlier channels)",
+        "data": ("synthetic: SplitMix64 + Box-Muller for every workload, seeds 1337 (X), 1338 (W), 1339 (outlier "
+                 "channels, per-token scales); the block workloads draw consecutive pieces of the same streams"),
         "config": {"workload": "Q5_K GEMM M=4096 K=3840 N=10240 (Z-Image DiT FFN), quantize + GEMM per step",
                    "M": GEMM_M, "K": GEMM_K, "N": GEMM_N, "weight_type": "Q5_K", "activation_type": "Q8_K",
                    "outlier_channels": int(len(ch)), "device": device},
@@ -716,7 +725,7 @@ def main():
         log(f"CPU {t_cpu:.2f} s -> {cpu_tops * 1e3:.1f} GOPS; GPU vs CPU max row rel err {parity:.2e}")
         line["cpu_baseline"] = {"value": round(cpu_tops, 5), "unit": "TOPS", "cores": threads, "kind": cpu.kind,
                                 "sample": sample, "seconds": round(t_cpu, 3), **host,
-                                "threads_rule": "min(affinity cores, 16): one GPU's share of host cores"}
+                                "threads_rule": "every core in the process's affinity mask (the reference's -t default)"}
         line["parity"] = {"max_row_rel_err_vs_cpu": parity, "tolerance": 1e-4, "rows_checked": int(xs.shape[0])}
         for k, v in matvec.items():
             reps = args.matvec_reps

@@ -219,8 +219,10 @@ int pixhip_matmul_stage(pixhip_session* session, const pixhip_weight* weight, co
  * pixhip_matmul_ex with the same kind of call: columns == 1 for the matvec,
  * columns > 1 for the GEMM); otherwise PIXHIP_ERR_STATE.  Activations beyond
  * the array (Mpad*K bytes plus scales: e.g. 4096 x 3840 Q8_K takes 17.9 MB)
- * give PIXHIP_ERR_MEMORY.  Every call on one GPU shares the array: calls that
- * overlap on one GPU (several sessions or streams) race.  Results equal
+ * give PIXHIP_ERR_MEMORY.  Every call on one GPU shares the array: a call on
+ * another stream than the previous call on that GPU first waits (on the
+ * device, hipStreamWaitEvent) for that call's work, so calls from several
+ * sessions or streams run one after the other there.  Results equal
  * pixhip_matmul_ex's, bit for bit where that call runs unsplit, else within
  * the fp32 rounding of the split sums.  Leaves no activations for
  * PIXHIP_STAGE_MULTIPLY. */

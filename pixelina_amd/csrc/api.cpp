@@ -70,6 +70,12 @@ constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
+// Calls from different streams share a device's array: each call records
+// g_scratch_event on its stream, and a call on another stream than the last
+// one waits for that event first, so the calls run one after the other.
+hipEvent_t g_scratch_event[kMaxDevices] = {};
+hipStream_t g_scratch_stream[kMaxDevices] = {};
+bool g_scratch_used[kMaxDevices] = {};
 
 }  // namespace
 
@@ -90,6 +96,13 @@ int scratch_setup(int device)
         (void)hipGetLastError();
         return fail(PIXHIP_ERR_DEVICE,std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
     }
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev,hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(PIXHIP_ERR_DEVICE,std::string("hipEventCreateWithFlags: ") + hipGetErrorString(e));
+    }
+    g_scratch_event[device] = ev;
     g_scratch_ptr[device] = p;
     return PIXHIP_OK;
 }
@@ -424,6 +437,35 @@ bool device_visible(pixhip_session* s, const void* p, const void** dev)
     return false;
 }
 
+// A sized operand must lie within one allocation: the session's own block
+// when p is inside one, else the allocation HIP reports for p.  Pointers HIP
+// does not know (pageable host memory) pass here and are staged or rejected
+// by the caller.
+int check_span(pixhip_session* s, const void* p, size_t bytes)
+{
+    if (!p || !bytes) return PIXHIP_OK;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    auto it = s->live.upper_bound(a);
+    if (it != s->live.begin()) {
+        --it;
+        if (a < it->first + it->second) {
+            if (bytes > it->first + it->second - a)
+                return fail(PIXHIP_ERR_ARGUMENT,"an operand of " + std::to_string(bytes) + " bytes runs past the end of its allocation");
+            return PIXHIP_OK;
+        }
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base,&size,const_cast<void*>(p)) == hipSuccess && base) {
+        const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+        if (a >= b && a - b <= size && bytes > size - (a - b))
+            return fail(PIXHIP_ERR_ARGUMENT,"an operand of " + std::to_string(bytes) + " bytes runs past the end of its allocation");
+        return PIXHIP_OK;
+    }
+    (void)hipGetLastError();
+    return PIXHIP_OK;
+}
+
 // A read-only operand of an elementwise op: device memory (ours, HIP device or
 // managed) and mapped pinned host memory are passed to the kernel as they
 // are; pageable host memory, which a kernel must not dereference, is copied to
@@ -432,6 +474,7 @@ bool device_visible(pixhip_session* s, const void* p, const void** dev)
 int read_operand(pixhip_session* s, const void* p, size_t bytes, const void** dev, void** staged)
 {
     *staged = nullptr;
+    if (int rc = check_span(s,p,bytes)) return rc;
     if (device_visible(s,p,dev)) return PIXHIP_OK;
     hipPointerAttribute_t attr;
     if (hipPointerGetAttributes(&attr,p) == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer) {
@@ -452,9 +495,11 @@ int read_operand(pixhip_session* s, const void* p, size_t bytes, const void** de
     return PIXHIP_OK;
 }
 
-// The in-place tensor of an elementwise op: device or mapped pinned memory only.
-int write_operand(pixhip_session* s, void* p, void** dev)
+// The in-place tensor (or output) of an op, `bytes` long: device or mapped
+// pinned memory only.
+int write_operand(pixhip_session* s, void* p, size_t bytes, void** dev)
 {
+    if (int rc = check_span(s,p,bytes)) return rc;
     const void* d = nullptr;
     if (device_visible(s,p,&d)) {
         *dev = const_cast<void*>(d);
@@ -581,6 +626,10 @@ int run(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t c
     const size_t K = w->inner;
     const size_t in_bytes = columns * K * sizeof(float);
     const size_t out_elems = y_offset + (columns - 1) * ldy + w->rows;
+    if ((stages & PIXHIP_STAGE_QUANTIZE && (rc = check_span(s,input,in_bytes))) ||
+        (stages & PIXHIP_STAGE_MULTIPLY && (rc = check_span(s,output,out_elems * sizeof(float)))) ||
+        (bias && (rc = check_span(s,bias,w->rows * sizeof(float)))))
+        return rc;
 
     // Resolve pointers; stage host or misaligned inputs and host outputs.
     const void* xin = nullptr;
@@ -949,6 +998,10 @@ int pixhip_matmul_ex_noalloc(pixhip_session* s, const pixhip_weight* wc, const f
     if (ldy < w->rows) return fail(PIXHIP_ERR_ARGUMENT,"output stride smaller than rows");
     const void* xin = nullptr;
     const void* yv = nullptr;
+    if ((rc = check_span(s,input,columns * w->inner * sizeof(float))) ||
+        (rc = check_span(s,output,(y_offset + (columns - 1) * ldy + w->rows) * sizeof(float))) ||
+        (bias && (rc = check_span(s,bias,w->rows * sizeof(float)))))
+        return rc;
     if (!device_visible(s,input,&xin) || !device_visible(s,output,&yv))
         return fail(PIXHIP_ERR_ARGUMENT,"input and output must be device memory (nothing is staged here)");
     if (reinterpret_cast<uintptr_t>(xin) % 16) return fail(PIXHIP_ERR_ARGUMENT,"input must be 16-byte aligned");
@@ -971,6 +1024,11 @@ int pixhip_matmul_ex_noalloc(pixhip_session* s, const pixhip_weight* wc, const f
     if (!w->planes) return fail(PIXHIP_ERR_STATE,"GEMM layout not resident: run the weight once through pixhip_matmul_ex");
     // The quantized activations in `scratch`, carved as act_buffers carves the
     // session scratch; the GEMM then runs unsplit (no split-K workspace).
+    // Ordered after the last call on this device that used the array.
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    const int dev = s->device;
+    if (g_scratch_used[dev] && g_scratch_stream[dev] != s->stream)
+        PIX_HIP(hipStreamWaitEvent(s->stream,g_scratch_event[dev],0),"hipStreamWaitEvent (scratch order)");
     const size_t mpad = round_up(columns,kTileM);
     Carver c;
     uint8_t* base = static_cast<uint8_t*>(dev_scratch);
@@ -995,6 +1053,9 @@ int pixhip_matmul_ex_noalloc(pixhip_session* s, const pixhip_weight* wc, const f
                                : pixhip::launch_gemm_q6_K(a,w->q6,columns,w->rows,K,out,nullptr,s->stream);
     }
     PIX_HIP(e,"GEMM launch");
+    PIX_HIP(hipEventRecord(g_scratch_event[dev],s->stream),"hipEventRecord (scratch order)");
+    g_scratch_stream[dev] = s->stream;
+    g_scratch_used[dev] = true;
     return PIXHIP_OK;
 }
 
@@ -1127,7 +1188,7 @@ int pixhip_pointwise(pixhip_session* s, unsigned operation, float* destination, 
     if ((reinterpret_cast<uintptr_t>(destination) | reinterpret_cast<uintptr_t>(second)) % 4)
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,rows * channels * sizeof(float),&dst))) return rc;
     const void* other = nullptr;
     void* staged = nullptr;
     if (needs_second) {
@@ -1150,7 +1211,7 @@ int pixhip_rope(pixhip_session* s, float* tensor, size_t rows, size_t channels, 
     if ((reinterpret_cast<uintptr_t>(tensor) | reinterpret_cast<uintptr_t>(cosine) | reinterpret_cast<uintptr_t>(sine)) % 4)
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* dst = nullptr;
-    if ((rc = write_operand(s,tensor,&dst))) return rc;
+    if ((rc = write_operand(s,tensor,rows * channels * sizeof(float),&dst))) return rc;
     const size_t table = rows * (channels / heads / 2) * sizeof(float);
     const void *cd = nullptr, *sd = nullptr;
     void *cs = nullptr, *ss = nullptr;
@@ -1182,7 +1243,7 @@ int attention_run(pixhip_session* s, const float* q, size_t rows, const float* k
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 16-byte aligned");
     int rc;
     void* out = nullptr;
-    if ((rc = write_operand(s,output,&out))) return rc;
+    if ((rc = write_operand(s,output,rows * channels * sizeof(float),&out))) return rc;
     const void *qd = nullptr, *kd = nullptr, *vd = nullptr;
     void *qs = nullptr, *ks = nullptr, *vs = nullptr;
     auto release = [&]() {
@@ -1376,7 +1437,7 @@ int pixhip_pointwise_ex(pixhip_session* s, unsigned operation, float* destinatio
     if (!aligned4(destination) || !aligned4(second) || !aligned4(third)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     if ((size_t)part > SIZE_MAX / channels - 1) return fail(PIXHIP_ERR_ARGUMENT,"part out of range");
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,bytes,&dst))) return rc;
     Staged st(s);
     const void *other = nullptr, *param = nullptr;
     const size_t slice = (size_t)part * channels;
@@ -1410,7 +1471,7 @@ int pixhip_qwen_modulate(pixhip_session* s, float* destination, size_t rows, siz
         return fail(PIXHIP_ERR_ARGUMENT,"parameters hold fewer than (part + 1) * channels values per row");
     if (!aligned4(destination) || !aligned4(parameters) || !aligned4(residual)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,bytes,&dst))) return rc;
     Staged st(s);
     const void *param = nullptr, *other = nullptr;
     if ((rc = st.read(parameters,pbytes,&param))) return rc;
@@ -1434,7 +1495,7 @@ int pixhip_l2norm(pixhip_session* s, const float* input, size_t rows, size_t cha
         return fail(PIXHIP_ERR_ARGUMENT,"null pointer, empty tensor or epsilon <= 0");
     if (!aligned4(input) || !aligned4(output) || !aligned4(weight)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* out = nullptr;
-    if ((rc = write_operand(s,output,&out))) return rc;
+    if ((rc = write_operand(s,output,bytes,&out))) return rc;
     Staged st(s);
     const void *in = nullptr, *w = nullptr;
     if ((rc = st.read(input,bytes,&in))) return rc;
@@ -1460,7 +1521,7 @@ int pixhip_groupnorm(pixhip_session* s, const float* input, size_t rows, size_t 
     if (!aligned4(input) || !aligned4(output) || !aligned4(weight) || !aligned4(bias))
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* out = nullptr;
-    if ((rc = write_operand(s,output,&out))) return rc;
+    if ((rc = write_operand(s,output,bytes,&out))) return rc;
     Staged st(s);
     const void *in = nullptr, *w = nullptr, *b = nullptr;
     if ((rc = st.read(input,bytes,&in)) || (rc = st.read(weight,channels * sizeof(float),&w)) ||
@@ -1490,7 +1551,7 @@ int pixhip_embedding(pixhip_session* s, const void* table, uint32_t type, uint64
     for (size_t i = 0; i < count; i++)
         if (ids[i] < 0 || (uint64_t)ids[i] >= table_rows) return fail(PIXHIP_ERR_ARGUMENT,"token id " + std::to_string(ids[i]) + " out of range");
     void* out = nullptr;
-    if ((rc = write_operand(s,output,&out))) return rc;
+    if ((rc = write_operand(s,output,bytes,&out))) return rc;
     Staged st(s);
     const void* dev_table = nullptr;
     hipError_t e;
@@ -1543,7 +1604,7 @@ int pixhip_rows(pixhip_session* s, const float* source, size_t source_rows, floa
         src_rows.assign(rows,rows + count);
     }
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,dbytes,&dst))) return rc;
     Staged st(s);
     const void *src = nullptr, *sr = nullptr, *dr = nullptr;
     if ((rc = st.read(source,sbytes,&src)) || (rc = st.read(src_rows.data(),src_rows.size() * sizeof(uint64_t),&sr))) return rc;
@@ -1570,7 +1631,7 @@ int pixhip_copy_rows(pixhip_session* s, const float* source, size_t source_rows,
         return fail(PIXHIP_ERR_ARGUMENT,"the copied rows do not lie within both tensors");
     if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,dbytes,&dst))) return rc;
     Staged st(s);
     const void* src = nullptr;
     if ((rc = st.read(source,sbytes,&src))) return rc;
@@ -1592,7 +1653,7 @@ int pixhip_copy_features(pixhip_session* s, const float* source, size_t source_c
         return fail(PIXHIP_ERR_ARGUMENT,"null pointer, empty tensor, or the source does not fit at the destination feature");
     if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,destination_channels * sizeof(float),&dst))) return rc;
     Staged st(s);
     const void* src = nullptr;
     if ((rc = st.read(source,source_channels * sizeof(float),&src))) return rc;
@@ -1630,7 +1691,7 @@ int pixhip_layout(pixhip_session* s, unsigned operation, const float* source, si
     if (!ok) return fail(PIXHIP_ERR_ARGUMENT,"tensor shapes do not match the layout");
     if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,dbytes,&dst))) return rc;
     Staged st(s);
     const void* src = nullptr;
     if ((rc = st.read(source,sbytes,&src))) return rc;
@@ -1664,7 +1725,7 @@ int pixhip_shortcut(pixhip_session* s, const float* source, size_t width, size_t
         return fail(PIXHIP_ERR_ARGUMENT,"shape too large");
     if (!aligned4(source) || !aligned4(destination)) return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     void* dst = nullptr;
-    if ((rc = write_operand(s,destination,&dst))) return rc;
+    if ((rc = write_operand(s,destination,dbytes,&dst))) return rc;
     Staged st(s);
     const void* src = nullptr;
     if ((rc = st.read(source,sbytes,&src))) return rc;
@@ -1783,13 +1844,12 @@ int pixhip_conv2d(pixhip_session* s, const pixhip_weight* wc, const float* input
     if (width * height > SIZE_MAX / w->cin / 4 || ow * oh > SIZE_MAX / w->rows / 4) return fail(PIXHIP_ERR_ARGUMENT,"image too large");
     in_bytes = width * height * w->cin * 4;
     out_bytes = ow * oh * w->rows * 4;
-    (void)out_bytes;
     if (reinterpret_cast<uintptr_t>(input) % 4 || reinterpret_cast<uintptr_t>(output) % 4 || reinterpret_cast<uintptr_t>(bias) % 4)
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 4-byte aligned");
     w->used = ++s->uses;
     if ((rc = ensure_conv_form(s,w))) return rc;
     void* out = nullptr;
-    if ((rc = write_operand(s,output,&out))) return rc;
+    if ((rc = write_operand(s,output,out_bytes,&out))) return rc;
     Staged st(s);
     const void *in = nullptr, *b = nullptr;
     if ((rc = st.read(input,in_bytes,&in))) return rc;

@@ -52,11 +52,22 @@ __device__ __forceinline__ uint32_t bf16_rne(float x)
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// x -> (hi, lo) bf16 bit patterns with x ~ hi + lo.
+// x -> (hi, lo) bf16 bit patterns with x ~ hi + lo, for every fp32 value: a
+// finite x that rounds past the largest bf16 keeps hi truncated (finite) and
+// the rest in lo; Inf and NaN travel in hi alone (lo = 0), so a product with
+// them gives what the fp32 product gives instead of NaN from Inf - Inf.
 __device__ __forceinline__ void split2(float x, uint32_t& hi, uint32_t& lo)
 {
-    hi = bf16_rne(x);
-    lo = bf16_rne(x - __uint_as_float(hi << 16));
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7F800000u) == 0x7F800000u) {
+        hi = (u & 0x007FFFFFu)? 0x7FC0u | ((u >> 16) & 0x8000u) : u >> 16;
+        lo = 0;
+        return;
+    }
+    uint32_t h = bf16_rne(x);
+    if ((h & 0x7F80u) == 0x7F80u) h = u >> 16;
+    hi = h;
+    lo = bf16_rne(x - __uint_as_float(h << 16));
 }
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));

@@ -47,10 +47,24 @@ __device__ __forceinline__ uint32_t rne16(float x)
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// x -> (hi, lo) bf16 with x ~ hi + lo for every fp32 value (the weight form
+// and the value-by-value gather): a finite x that rounds past the largest
+// bf16 keeps hi truncated; Inf and NaN travel in hi alone (lo = 0).  The image
+// kernel's hardware split (halves2) assumes finite values that round to a
+// finite bf16, |x| < (2 - 2^-8) * 2^127 ~ 3.396e38: beyond that, and for Inf
+// and NaN, its halves give NaN.
 __device__ __forceinline__ void halves(float x, uint32_t& hi, uint32_t& lo)
 {
-    hi = rne16(x);
-    lo = rne16(x - __uint_as_float(hi << 16));
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7F800000u) == 0x7F800000u) {
+        hi = (u & 0x007FFFFFu)? 0x7FC0u | ((u >> 16) & 0x8000u) : u >> 16;
+        lo = 0;
+        return;
+    }
+    uint32_t h = rne16(x);
+    if ((h & 0x7F80u) == 0x7F80u) h = u >> 16;
+    hi = h;
+    lo = rne16(x - __uint_as_float(h << 16));
 }
 
 typedef __bf16 cbf16x2 __attribute__((ext_vector_type(2)));

@@ -336,9 +336,16 @@ public:
             if (!str(v.text)) return invalid();
             return v;
         }
+        // u8 i8 u16 i16 u32 i32 f32 bool - - u64 i64 f64
+        static const unsigned width[13] = {1,1,2,2,4,4,4,1,0,0,8,8,8};
         if (type == kGgufArray) {
             uint64_t element, count;
             if (!uint(4,element) || !uint(8,count) || count > kMaxItems || element == kGgufArray) return invalid();
+            // Every item takes at least this many header bytes (a string its
+            // 8-byte length): a count the rest of the header cannot hold is
+            // rejected before anything is reserved for it.
+            const uint64_t least = element == kGgufString? 8 : element <= kGgufFloat64 && width[element]? width[element] : 1;
+            if (count > (end - pos) / least) return invalid();
             v.kind = Value::Array;
             v.items.reserve((size_t)count);
             for (uint64_t i = 0; i < count; i++) {
@@ -348,8 +355,6 @@ public:
             }
             return v;
         }
-        // u8 i8 u16 i16 u32 i32 f32 bool - - u64 i64 f64
-        static const unsigned width[13] = {1,1,2,2,4,4,4,1,0,0,8,8,8};
         uint64_t raw;
         if (type > kGgufFloat64 || !uint(width[type],raw)) return invalid();
         v.kind = type == 7? Value::Boolean : Value::Number;

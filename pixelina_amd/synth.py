@@ -53,15 +53,20 @@ def _parallel(fn, items):
         return list(ex.map(fn, items))
 
 
-def normal(seed, shape, std=1.0, chunk=1 << 20):
-    """float32 N(0, std^2) of the given shape, Box-Muller pairs in row-major order."""
+def normal(seed, shape, std=1.0, chunk=1 << 20, start=0):
+    """float32 N(0, std^2) of the given shape, Box-Muller pairs in row-major order.
+
+    `start` (even) skips that many values of the stream, so consecutive
+    tensors drawn with start = the running count continue one stream."""
+    if start % 2:
+        raise ValueError("start must be even (values come in Box-Muller pairs)")
     n = int(np.prod(shape))
     out = np.empty(n, dtype=np.float32)
     pairs = (n + 1) // 2
 
     def fill(p0):
         p1 = min(pairs, p0 + chunk)
-        u = splitmix_uniform(seed, 2 * (p1 - p0), start=2 * p0)
+        u = splitmix_uniform(seed, 2 * (p1 - p0), start=start + 2 * p0)
         r = np.sqrt(-2.0 * np.log(u[0::2]))
         a = 2.0 * np.pi * u[1::2]
         z = np.empty(2 * (p1 - p0), dtype=np.float64)
@@ -80,8 +85,8 @@ def outlier_channels(k, fraction=0.01, seed=SEED_OUTLIERS):
     return np.sort(np.argsort(splitmix_uniform(seed, k), kind="stable")[:count])
 
 
-def log_uniform(seed, n, lo, hi):
-    u = splitmix_uniform(seed, n)
+def log_uniform(seed, n, lo, hi, start=0):
+    u = splitmix_uniform(seed, n, start=start)
     return np.exp(np.log(lo) + u * (np.log(hi) - np.log(lo))).astype(np.float32)
 
 

@@ -119,9 +119,9 @@ def reference():
 
 
 def default_threads():
-    """Host threads for the oracle: every core here, at most 16 (a GPU box's
-    share of its host, whatever os.cpu_count() reports there)."""
-    return max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)))
+    """Host threads for the oracle and the compiled reference: every core in
+    this process's affinity mask (the reference's default, src/tensor.cpp:97-101)."""
+    return max(1, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1))
 
 
 def ptr(a):

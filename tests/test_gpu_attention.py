@@ -129,6 +129,23 @@ def test_properties_at_full_size(sess):
     assert np.array_equal(y1.view(np.uint32), y3.view(np.uint32)), "repeats differ"
 
 
+def test_values_beyond_bf16_range(sess):
+    """V entries of 3.4e38 (finite in fp32, but past the largest bf16, so a
+    rounded-to-nearest split would make hi = Inf and lo = NaN): the split keeps
+    hi finite and the outputs match the oracle with no NaN."""
+    rng = np.random.default_rng(77)
+    rows, keys, heads, dim = 64, 96, 2, 64
+    q, k, v = qkv(rng, rows, keys, heads, heads, dim)
+    v[5, 3] = np.float32(3.4e38)
+    v[40, dim + 7] = np.float32(-3.4e38)
+    y = gpu_attention(sess, q, k, v, heads, heads)
+    ref = attention(oracle(), "orc", q, k, v, heads, heads)
+    assert np.isfinite(ref).all() and np.isfinite(y).all()
+    err = row_rel_error(y, ref).max()
+    print(f"rel={err:.2e}", flush=True)
+    assert err <= TOL
+
+
 def test_errors(sess):
     rng = np.random.default_rng(1)
     q, k, v = qkv(rng, 8, 8, 2, 2, 64)

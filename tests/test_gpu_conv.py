@@ -193,6 +193,43 @@ def test_weight_from_model_file(sess, tmp_path):
         sess.lib.pixhip_model_close(model)
 
 
+def test_weights_beyond_bf16_range(sess):
+    """F32 weights of +-3.4e38 (finite, past the largest bf16: a rounded split
+    would give hi = Inf, lo = NaN) against image values small enough for
+    finite products: the weight split keeps hi finite, no NaN, within TOL."""
+    rng = np.random.default_rng(5)
+    wd, ht, cin, cout, k = 16, 12, 64, 64, 3
+    x = (rng.standard_normal((wd * ht, cin)) * 1e-30).astype(np.float32)
+    w = (rng.standard_normal((cout, cin * k * k)) / np.sqrt(cin * k * k)).astype(np.float32)
+    w[3, 10] = np.float32(3.4e38)
+    w[40, 500] = np.float32(-3.4e38)
+    y = gpu_conv(sess, "conv:huge", x, wd, ht, w.view(np.uint8), F32, k, k, cin, cout)
+    ref = conv2d(oracle(), x, wd, ht, w, k, k, None, None)
+    assert np.isfinite(ref).all() and np.isfinite(y).all()
+    err = row_rel_error(y, ref).max()
+    print(f"rel={err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_output_past_its_allocation():
+    """An output (or input) that runs past the end of its device allocation is
+    rejected before any launch (a fresh session, so every block is exactly its
+    request rounded to 256 bytes)."""
+    s = new_session()
+    try:
+        raw = np.zeros(4 * 8 * 9 * 2, np.uint8)
+        w = s.conv_weight("span", raw, F16, 3, 3, 8, 4)
+        x, y = s.alloc(16 * 8 * 4), s.alloc(16 * 4 * 4)      # 512 and 256 bytes
+        assert s.conv2d(w, x.ptr, 4, 4, y.ptr) == _lib.OK
+        s.synchronize()
+        assert s.conv2d(w, x.ptr, 4, 4, y.ptr + 4) == _lib.ERR_ARGUMENT      # output one float past the end
+        assert s.conv2d(w, x.ptr + 16, 4, 4, y.ptr) == _lib.ERR_ARGUMENT     # input four floats past the end
+        x.free()
+        y.free()
+    finally:
+        s.close()
+
+
 def test_errors(sess):
     arg, uns = _lib.ERR_ARGUMENT, _lib.ERR_UNSUPPORTED
     raw = np.zeros(4 * 8 * 9 * 2, np.uint8)

@@ -215,3 +215,29 @@ def test_rejects_what_the_reference_rejects(sess):
     assert q(1, 4, 2, 256) == _lib.ERR_UNSUPPORTED  # MODEL_F16 stays on the reference's float path
     assert np.all(y == 0)
     assert q(Q5_K, 4, 2, 256) == _lib.OK
+
+
+def test_operands_past_their_allocation():
+    """pixhip_matmul_ex with an output region (y_offset + (M-1)*ldy + N floats),
+    an input (M*K floats) or a bias (N floats) that runs past the end of its
+    device allocation is rejected, and nothing is launched (a fresh session:
+    every block is exactly its request rounded to 256 bytes)."""
+    from gpu_helpers import new_session
+    s = new_session()
+    try:
+        m, k, n = 4, 256, 64
+        w = s.weight("span:q5", weights(910, n, k, Q5_K), Q5_K, k, n)
+        xb, yb, bb = s.alloc(m * k * 4), s.alloc(m * n * 4), s.alloc(n * 4)
+        xb.upload(activations(911, m, k))
+        bb.upload(np.zeros(n, np.float32))
+        mx = lambda x, y, bias, ldy=0, off=0: s.lib.pixhip_matmul_ex(s.handle, w, x, m, y, bias, ldy, off)
+        assert mx(xb.ptr, yb.ptr, bb.ptr) == _lib.OK
+        s.synchronize()
+        assert mx(xb.ptr, yb.ptr, bb.ptr, 0, 1) == _lib.ERR_ARGUMENT        # y offset by one float
+        assert mx(xb.ptr, yb.ptr, bb.ptr, n + 1) == _lib.ERR_ARGUMENT       # a wider row stride
+        assert mx(xb.ptr + 4, yb.ptr, bb.ptr) == _lib.ERR_ARGUMENT          # input one float past the end
+        assert mx(xb.ptr, yb.ptr, bb.ptr + 4) == _lib.ERR_ARGUMENT          # bias one float past the end
+        for b in (xb, yb, bb):
+            b.free()
+    finally:
+        s.close()
