@@ -15,7 +15,8 @@ workloads (`workloads`: a single Q8_0 linear [256, 3840] x [3840, 3840], every
 linear of a Z-Image DiT block at M = 4608 and of a Qwen-Image edit block at
 M = 8448, each linear and the block back to back), the same step with host
 (pinned) operands staged over PCIe, self-attention at the DiT block's shape
-(30 heads of 128 over 4608 tokens), the rest of the op surface (`surface`:
+(30 heads of 128 over 4608 tokens) and the VAE mid-block's (one head of 512
+over 16384 tokens), the rest of the op surface (`surface`:
 norms, layouts and row moves at the models' shapes, against the HBM peak), VAE
 convolutions (`conv`, against the bf16 MFMA peak), and the reference CPU path
 (cpu_quant_matmul, tensor_attention) timed on this host on the same inputs.
@@ -384,57 +385,63 @@ def bench_fused(sess, synth, _lib, Q5_K, Q8_0, reps):
     return out
 
 
-ATTN_ROWS, ATTN_HEADS, ATTN_DIM = 4608, 30, 128  # Z-Image DiT self-attention (4096 image + 512 text tokens)
-ATTN_CPU_ROWS = 32                                # query rows the CPU reference is timed on
+# (key, tokens, heads, head size, kernel, workload text)
+ATTN_SHAPES = [
+    ("attention", 4608, 30, 128, "attn_kernel<128>",
+     "self-attention, 30 heads of 128, 4608 tokens, not causal (Z-Image DiT: 4096 image + 512 text tokens)"),
+    ("attention_vae", 16384, 1, 512, "attn_wide_kernel<128>",
+     "self-attention, one head of 512, 16384 tokens, not causal (Z-Image VAE mid-block at a 128 x 128 latent)"),
+]
+ATTN_CPU_ROWS = 32  # query rows the CPU reference is timed on
 
 
-def bench_attention(sess, synth, _lib, reps):
-    """tensor_attention at the DiT block's shape (30 heads of 128 over 4608
-    tokens, not causal).  Algorithmic work 4 * heads * rows^2 * dim flops (the
-    two products); the kernel runs each fp32 product as three bf16 MFMA terms,
-    so its matrix-core work is 3x that, priced against the dense bf16 peak."""
-    q = synth.normal(synth.SEED_ACTIVATIONS, (ATTN_ROWS, ATTN_HEADS * ATTN_DIM))
-    k = synth.normal(synth.SEED_WEIGHTS, (ATTN_ROWS, ATTN_HEADS * ATTN_DIM))
-    v = synth.normal(synth.SEED_OUTLIERS, (ATTN_ROWS, ATTN_HEADS * ATTN_DIM))
+def bench_attention(sess, synth, _lib, reps, shape):
+    """tensor_attention at one model shape (not causal).  Algorithmic work 4 *
+    heads * rows^2 * dim flops (the two products); the kernel runs each fp32
+    product as three bf16 MFMA terms, so its matrix-core work is 3x that,
+    priced against the dense bf16 peak."""
+    key, rows, heads, dim, kernel, text = shape
+    ch = heads * dim
+    q = synth.normal(synth.SEED_ACTIVATIONS, (rows, ch))
+    k = synth.normal(synth.SEED_WEIGHTS, (rows, ch))
+    v = synth.normal(synth.SEED_OUTLIERS, (rows, ch))
     qb, kb, vb, ob = sess.to_device(q), sess.to_device(k), sess.to_device(v), sess.alloc(q.nbytes)
-    ch = ATTN_HEADS * ATTN_DIM
 
     def run():
-        _lib.check(sess.attention(qb.ptr, ATTN_ROWS, kb.ptr, vb.ptr, ATTN_ROWS, ATTN_HEADS, ATTN_HEADS, ch, ob.ptr), "attention")
+        _lib.check(sess.attention(qb.ptr, rows, kb.ptr, vb.ptr, rows, heads, heads, ch, ob.ptr), "attention")
 
     ms, n = timed_series(sess, run, max(5, reps // 5))
-    y = ob.download(np.float32, ATTN_ROWS * ch).reshape(ATTN_ROWS, ch)
+    y = ob.download(np.float32, rows * ch).reshape(rows, ch)
     for b in (qb, kb, vb, ob):
         b.free()
-    flops = 4.0 * ATTN_HEADS * ATTN_ROWS * ATTN_ROWS * ATTN_DIM
+    flops = 4.0 * heads * rows * rows * dim
     tf = flops / (ms * 1e-3) / 1e12
-    log(f"attention {ATTN_HEADS}x{ATTN_DIM} over {ATTN_ROWS} tokens: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s "
+    log(f"{key} {heads}x{dim} over {rows} tokens: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s "
         f"({3 * tf:.1f} TFLOP/s of bf16 MFMA work)")
-    rec = {"workload": f"self-attention, {ATTN_HEADS} heads of {ATTN_DIM}, {ATTN_ROWS} tokens, not causal (Z-Image DiT)",
-           "us": round(ms * 1e3, 2), "tflops": round(tf, 2), "reps": n,
-           "roofline": {"kernel": "attn_kernel<128>", "bound": "mfma", "achieved": round(3 * tf, 2), "peak": PEAK_BF16_TFLOPS,
-                        "unit": "TFLOP/s", "frac": round(3 * tf / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic("attention"),
+    rec = {"workload": text, "us": round(ms * 1e3, 2), "tflops": round(tf, 2), "reps": n,
+           "roofline": {"kernel": kernel, "bound": "mfma", "achieved": round(3 * tf, 2), "peak": PEAK_BF16_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(3 * tf / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(key),
                         "work_per_launch": f"3 x 4*heads*rows^2*dim = {3 * flops:.4e} bf16 MFMA flops (fp32 products as three bf16 terms)"}}
-    return rec, (q, k, v, y)
+    return rec, (shape, q, k, v, y)
 
 
 def cpu_attention(cpu, rec, data):
     """The reference's tensor_attention (oracle/_ref, or the oracle) on the
     first ATTN_CPU_ROWS query rows against every key, the time scaled to all
     rows (each row's work is the same), and the GPU rows checked against it."""
-    q, k, v, y = data
+    (key, tokens, heads, dim, _, _), q, k, v, y = data
     rows = ATTN_CPU_ROWS
-    cpu.ol.attention(cpu.lib, cpu.prefix, q[:4], k[:64], v[:64], ATTN_HEADS, ATTN_HEADS)  # pool warm-up
+    cpu.ol.attention(cpu.lib, cpu.prefix, q[:4], k[:64], v[:64], heads, heads)  # pool warm-up
     t = time.perf_counter()
-    yc = cpu.ol.attention(cpu.lib, cpu.prefix, q[:rows], k, v, ATTN_HEADS, ATTN_HEADS)
-    sec = (time.perf_counter() - t) * ATTN_ROWS / rows
+    yc = cpu.ol.attention(cpu.lib, cpu.prefix, q[:rows], k, v, heads, heads)
+    sec = (time.perf_counter() - t) * tokens / rows
     err = row_rel(y[:rows], yc)
-    flops = 4.0 * ATTN_HEADS * ATTN_ROWS * ATTN_ROWS * ATTN_DIM
+    flops = 4.0 * heads * tokens * tokens * dim
     rec["cpu_baseline"] = {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": cpu.threads, "kind": cpu.kind,
-                           "sample": f"first {rows} of {ATTN_ROWS} query rows, all keys, scaled to all rows",
+                           "sample": f"first {rows} of {tokens} query rows, all keys, scaled to all rows",
                            "us": round(sec * 1e6, 1)}
     rec["parity_max_row_rel_err_vs_cpu"] = err
-    log(f"CPU attention: {sec * 1e3:.0f} ms (scaled); GPU vs CPU rel err {err:.2e}")
+    log(f"CPU {key}: {sec * 1e3:.0f} ms (scaled); GPU vs CPU rel err {err:.2e}")
 
 
 # The rest of the op surface at the models' shapes: (name, workload text).
@@ -559,7 +566,7 @@ def main():
     ap.add_argument("--no-fused", action="store_true", help="skip the fused norm / SiLU-gate producers")
     ap.add_argument("--no-blocks", action="store_true", help="skip the single Q8_0 linear and the block workloads")
     ap.add_argument("--no-pcie", action="store_true", help="skip the host-operand (PCIe-inclusive) step")
-    ap.add_argument("--no-attention", action="store_true", help="skip the DiT-shape attention")
+    ap.add_argument("--no-attention", action="store_true", help="skip the DiT- and VAE-shape attention")
     ap.add_argument("--no-surface", action="store_true", help="skip the norms, layouts and row moves")
     ap.add_argument("--no-conv", action="store_true", help="skip the VAE convolutions")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -634,7 +641,7 @@ def main():
             xvb.free()
             yvb.free()
         fused = {} if args.no_fused else bench_fused(sess, synth, _lib, Q5_K, Q8_0, args.steps)
-        attention, attn_data = (None, None) if args.no_attention else bench_attention(sess, synth, _lib, args.steps)
+        attention = {} if args.no_attention else {sh[0]: bench_attention(sess, synth, _lib, args.steps, sh) for sh in ATTN_SHAPES}
         surface = None if args.no_surface else bench_surface(sess, synth, _lib)
         conv = None if args.no_conv else bench_conv(sess, synth, _lib)
         if args.calibrate_copy:
@@ -686,8 +693,8 @@ def main():
 
     if fused:
         line["fused"] = fused
-    if attention:
-        line["attention"] = attention
+    for key, (rec, _) in attention.items():
+        line[key] = rec
     if surface:
         line["surface"] = surface
     if conv:
@@ -744,8 +751,8 @@ def main():
             log(f"CPU matvec {k}: {tc * 1e6:.0f} us; GPU vs CPU rel err {err:.2e}")
         if keep:
             cpu_workloads(cpu, types, workloads, keep)
-        if attention:
-            cpu_attention(cpu, attention, attn_data)
+        for rec, data in attention.values():
+            cpu_attention(cpu, rec, data)
     print(json.dumps(line), flush=True)
 
 

@@ -28,7 +28,7 @@ extern "C" {
 
 #define PIXHIP_OK 0
 #define PIXHIP_ERR_ARGUMENT (-1)    /* bad pointer, size or shape (cpu_quant_matmul's `return false`, src/kernels_quant.cpp:373-377) */
-#define PIXHIP_ERR_UNSUPPORTED (-2) /* weight type other than Q8_0 / Q5_K / Q6_K; attention head size above 128 */
+#define PIXHIP_ERR_UNSUPPORTED (-2) /* weight type other than Q8_0 / Q5_K / Q6_K; attention head size above 512 */
 #define PIXHIP_ERR_MEMORY (-3)      /* device allocation failed or exceeds the budget (src/backend_vulkan.cpp:689, :718-720) */
 #define PIXHIP_ERR_DEVICE (-4)      /* HIP runtime failure: no device, launch or synchronisation error */
 #define PIXHIP_ERR_STATE (-5)       /* missing session, MULTIPLY without matching activations, or an evicted weight without host bytes */
@@ -326,7 +326,7 @@ typedef struct pixhip_attention_range {
  * vulkan_attention, src/backend_vulkan.h:143): `output` [rows][channels] for
  * q [rows][channels] and k, v [keys][channels / heads * kv_heads], head h
  * reading kv head h / (heads / kv_heads), scale 1/sqrt(channels / heads);
- * causal rows see keys 0..row.  Head sizes 1..128 (PIXHIP_ERR_UNSUPPORTED
+ * causal rows see keys 0..row.  Head sizes 1..512 (PIXHIP_ERR_UNSUPPORTED
  * beyond; the reference's Vulkan path takes up to 1280).  Rejects
  * (PIXHIP_ERR_ARGUMENT) heads not a multiple of kv_heads, channels not a
  * multiple of heads, and causal with rows > keys (where the reference reads

@@ -72,7 +72,8 @@ def _compile(src):
 # completely too, but sit at the register limit, where a spill would mean
 # scratch traffic in the key loop; they are checked as well.
 NO_SPILL = {
-    "csrc/attention.hip": ("attn_kernelILi128E", "attn_kernelILi64E"),
+    "csrc/attention.hip": ("attn_kernelILi128E", "attn_kernelILi64E", "attn_wide_kernelILi128E", "attn_wide_kernelILi96E",
+                           "attn_wide_kernelILi64E"),
     "csrc/gemm_kq.hip": ("gemm_kq_kernelILb1ELb0E", "gemm_kq_kernelILb0ELb0E"),
     "csrc/gemm.hip": ("gemm_kernelILb0E", "gemm_small_kernel"),
 }

@@ -1237,7 +1237,7 @@ int attention_run(pixhip_session* s, const float* q, size_t rows, const float* k
 {
     const size_t dim = channels / heads, kv_channels = dim * kv_heads;
     if (!pixhip::attention_dim_pad(dim))
-        return fail(PIXHIP_ERR_UNSUPPORTED,"attention head size " + std::to_string(dim) + " is not supported (1..128)");
+        return fail(PIXHIP_ERR_UNSUPPORTED,"attention head size " + std::to_string(dim) + " is not supported (1..512)");
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
          reinterpret_cast<uintptr_t>(output)) % 16)
         return fail(PIXHIP_ERR_ARGUMENT,"tensors must be 16-byte aligned");

@@ -1,6 +1,6 @@
 // Attention: tensor_attention (src/tensor.cpp:347-427) and vulkan_attention
 // (src/backend_vulkan.cpp:1318-1340) on bf16 MFMA (gfx950), head sizes up to
-// 128.
+// 512 (up to 128 in the kernel below, 129..512 in attn_wide_kernel).
 //
 // Numerics: the reference works in fp32 (scores = dot * 1/sqrt(dim), exp(score
 // - max), probabilities p / sum, out += p * v).  Here every fp32 operand x of
@@ -15,8 +15,8 @@
 // Layout: a split pass writes K as bf16 planes [head][key][D] and V transposed,
 // [head][D][key], with the keys of each 16-key group permuted (bits 2 and 3
 // swapped) so that the operand a lane needs for P*V is 16 contiguous bytes (D
-// = 64 or 128: the head size rounded up, zero-padded).  Q, read by one
-// workgroup per row, is split in the kernel.
+// = 64, 128, 256, 384 or 512: the head size rounded up, zero-padded).  Q, read
+// by one workgroup per row, is split in the kernel.
 //
 // Kernel: a workgroup of 8 waves owns 256 queries of one head (32 per wave)
 // and streams 64-key tiles of K and V^T (both planes) through a 2-stage LDS
@@ -510,6 +510,272 @@ __global__ __launch_bounds__(256) void attn_combine(AttnArgs a)
         if (d0 + i < a.dim) row[d0 + i] = v[i] / l;
 }
 
+// ---------------------------------------------------------------- wide heads
+
+// Head sizes 129..512 (the VAEs' single head of 384 or 512 channels), padded
+// to D = 4 DQ with DQ = 64, 96 or 128.  Q and O^T of a 32-query wave no longer
+// fit in registers whole, so the head is cut in quarters: a workgroup of 8
+// waves is 2 groups of 32 queries x 4 quarters of DQ dims.  Per 32-key tile
+// each wave computes the S^T partial over its quarter (its Q quarter stays in
+// registers), the four partials of a group meet in LDS and are summed in
+// quarter order -- every wave of the group then holds the same scores and
+// runs the same online softmax, so the four waves' running maximum and sum
+// agree bit for bit -- and each wave adds V^T[quarter] * P^T into its quarter
+// of O^T.  One K tile and one V^T tile are resident (K: 32 keys x D, V^T: D x
+// 32 keys, both planes; 160 KB of LDS with the exchange at D = 512); V^T of
+// tile t is fetched while the scores of t are formed, K of tile t + 1 while
+// the softmax and P*V of t run.
+constexpr int kWQ = 64;  // queries per workgroup
+constexpr int kWK = 32;  // keys per tile
+
+__device__ __forceinline__ void attn_sync_lds()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int DQ>
+__global__ __launch_bounds__(kAThreads, 1) void attn_wide_kernel(AttnArgs a)
+{
+    constexpr int D = 4 * DQ;
+    constexpr int PK = D / 8;                  // 16-byte pieces per K row
+    constexpr int KPLANE = kWK * D * 2;        // one plane of a K tile: 32 rows of 2D bytes
+    constexpr int VPLANE = D * kWK * 2;        // one plane of a V^T tile: D rows of 64 bytes
+    constexpr int CPP = KPLANE / 1024;         // 1 KB DMA chunks per plane
+    constexpr int PER_WAVE = 2 * CPP / kAWaves;  // chunks per wave per tile (K or V^T)
+    constexpr int KS = DQ / 16, TD = DQ / 32;
+    constexpr int EX = 2 * KPLANE + 2 * VPLANE;  // exchange: [group][quarter][4][64 lanes] float4
+    static_assert(PER_WAVE * kAWaves == 2 * CPP && PK % 16 == 0, "tile DMAs split evenly, K swizzle within the row");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[EX + 2 * 4 * 4 * 1024];
+
+    // consecutive units on one XCD (they share K and V when they share a head)
+    int bid = (int)blockIdx.x;
+    if ((gridDim.x & 7) == 0) bid = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);
+    const int head = bid / a.tiles_q, qt = bid % a.tiles_q;
+    const int kvh = head / a.kv_group;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int grp = wave >> 2, qtr = wave & 3;
+    const int lane = (int)(threadIdx.x & 63), lr = lane & 31, hh = lane >> 5;
+    const int q = a.qb + qt * kWQ + grp * 32 + lr;
+    const bool live = q < a.qe;
+    const int limit = !live? 1 : a.causal? min(a.key_end,a.qoff + q + 1) : a.key_end;
+    const int q_last = min(a.qe,a.qb + (qt + 1) * kWQ) - 1;
+    const int wg_limit = a.causal? min(a.key_end,a.qoff + q_last + 1) : a.key_end;
+    const int tiles = (wg_limit + kWK - 1) / kWK;
+
+    // Q quarter fragments: lane = query, dims qtr*DQ + 16k + 8hh .. +7
+    bf16x8 qfh[KS], qfl[KS];
+    {
+        const float* qrow = a.q + (size_t)min(q,a.rows - 1) * a.channels + (size_t)head * a.dim;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            u32x4 vh, vl;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = qtr * DQ + 16 * k + 8 * hh + 2 * i;
+                uint32_t h0, l0, h1, l1;
+                split2(d < a.dim? qrow[d] : 0.0f,h0,l0);
+                split2(d + 1 < a.dim? qrow[d + 1] : 0.0f,h1,l1);
+                vh[i] = h0 | (h1 << 16);
+                vl[i] = l0 | (l1 << 16);
+            }
+            qfh[k] = __builtin_bit_cast(bf16x8,vh);
+            qfl[k] = __builtin_bit_cast(bf16x8,vl);
+        }
+    }
+    int wave_limit = limit;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) wave_limit = min(wave_limit,__shfl_xor(wave_limit,m));
+
+    const size_t plane = (size_t)a.keys_pad * D * 2;
+    const size_t hoff = (size_t)kvh * a.keys_pad * D;
+    const ARsrc rk[2] = {__builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.kh) + hoff,(short)0,(int)plane,0x00020000),
+                         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.kl) + hoff,(short)0,(int)plane,0x00020000)};
+    const ARsrc rv[2] = {__builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.vh) + hoff,(short)0,(int)plane,0x00020000),
+                         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.vl) + hoff,(short)0,(int)plane,0x00020000)};
+
+    // K tile kt: chunk c = wave + 8i of the two planes; lane j of a chunk lands
+    // on piece 64 ci + j of the plane = row r, physical piece p, which holds
+    // logical piece p ^ (r & 15).
+    auto issue_k = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; i++) {
+            const int c = wave + kAWaves * i, pl = c / CPP, ci = c % CPP;
+            const int f = ci * 64 + lane, r = f / PK, p = f % PK;
+            const uint32_t off = (uint32_t)((kt * kWK + r) * D * 2 + 16 * (p ^ (r & 15)));
+            adma(rk[pl],lds + pl * KPLANE + ci * 1024,off,0);
+        }
+    };
+    // V^T tile kt: rows of 4 pieces (32 keys); row r, physical piece p holds
+    // logical piece p ^ ((r >> 2) & 3).
+    auto issue_v = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; i++) {
+            const int c = wave + kAWaves * i, pl = c / CPP, ci = c % CPP;
+            const int f = ci * 64 + lane, r = f >> 2, p = f & 3;
+            const uint32_t off = (uint32_t)(((size_t)r * a.keys_pad + kt * kWK) * 2 + 16 * (p ^ ((r >> 2) & 3)));
+            adma(rv[pl],lds + 2 * KPLANE + pl * VPLANE + ci * 1024,off,0);
+        }
+    };
+
+    v16f o[TD];
+#pragma unroll
+    for (int t = 0; t < TD; t++) o[t] = v16f{};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float c2 = a.scale * kLog2e;
+
+    // partial S^T over this wave's quarter (keys = MFMA rows, lane's query =
+    // column)
+    auto score = [&]() {
+        v16f s = v16f{};
+        const uint8_t *h = lds + lr * (2 * D), *l = lds + KPLANE + lr * (2 * D);
+        auto frag = [&](const uint8_t* row, int k) {
+            return lds_read<bf16x8>(row + 16 * ((qtr * (DQ / 8) + 2 * k + hh) ^ (lr & 15)));
+        };
+        bf16x8 ah = frag(h,0), al = frag(l,0);
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            bf16x8 nh, nl;
+            if (k + 1 < KS) {
+                nh = frag(h,k + 1);
+                nl = frag(l,k + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfh[k],s,0,0,0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,qfl[k],s,0,0,0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,qfh[k],s,0,0,0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + 1 < KS) {
+                ah = nh;
+                al = nl;
+            }
+        }
+        return s;
+    };
+    // the online softmax of the existing kernel over one 32-key tile
+    auto softmax = [&](v16f& sv, int key0, uint32_t (&ph)[2][4], uint32_t (&pl)[2][4]) {
+        const bool edge = key0 + 32 > wave_limit;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            float x = sv[r] * c2;
+            if (edge && key0 + 8 * (r >> 2) + 4 * hh + (r & 3) >= limit) x = -INFINITY;
+            sv[r] = x;
+            mx = fmaxf(mx,x);
+        }
+        mx = fmaxf(mx,__shfl_xor(mx,32));
+        const bool need = mx > m_run + 8.0f;
+        const float m_use = need? mx : m_run;
+        if (__any(need)) {
+            const float alpha = need? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
+#pragma unroll
+            for (int t = 0; t < TD; t++) o[t] *= alpha;
+            l_run *= alpha;
+        }
+        m_run = m_use;
+        const float m_ref = m_use == -INFINITY? 0.0f : m_use;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(sv[r] - m_ref);
+            const float p1 = __builtin_amdgcn_exp2f(sv[r + 1] - m_ref);
+            l_run += p0;
+            l_run += p1;
+            const uint32_t h = pack_bf16(p0,p1);
+            const int t = r / 8, w = (r % 8) / 2;
+            ph[t][w] = h;
+            pl[t][w] = pack_bf16(p0 - __uint_as_float(h << 16),p1 - __uint_as_float(h & 0xFFFF0000u));
+        }
+    };
+    // O^T[quarter] += V^T[quarter] * P^T over the tile's two 16-key k-steps
+    auto pv = [&](const uint32_t (&ph)[2][4], const uint32_t (&pl)[2][4]) {
+        auto frag = [&](int pln, int j, int td) {
+            const int r = qtr * DQ + 32 * td + lr;
+            return lds_read<bf16x8>(lds + 2 * KPLANE + pln * VPLANE + r * 64 + 16 * ((2 * j + hh) ^ ((lr >> 2) & 3)));
+        };
+        bf16x8 ah = frag(0,0,0), al = frag(1,0,0);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const bf16x8 bh = __builtin_bit_cast(bf16x8,u32x4{ph[j][0],ph[j][1],ph[j][2],ph[j][3]});
+            const bf16x8 bl = __builtin_bit_cast(bf16x8,u32x4{pl[j][0],pl[j][1],pl[j][2],pl[j][3]});
+#pragma unroll
+            for (int td = 0; td < TD; td++) {
+                const int nj = td + 1 < TD? j : j + 1, ntd = td + 1 < TD? td + 1 : 0;
+                bf16x8 nh, nl;
+                if (nj < 2) {
+                    nh = frag(0,nj,ntd);
+                    nl = frag(1,nj,ntd);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,bh,o[td],0,0,0);
+                o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah,bl,o[td],0,0,0);
+                o[td] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al,bh,o[td],0,0,0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (nj < 2) {
+                    ah = nh;
+                    al = nl;
+                }
+            }
+        }
+    };
+
+    uint8_t* const ex = lds + EX;
+    issue_k(0);
+    for (int kt = 0; kt < tiles; kt++) {
+        attn_wait_vmcnt<0>();
+        attn_sync_lds();  // K of kt visible; every wave is past P*V of kt - 1
+        issue_v(kt);
+        const v16f s = score();
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            *reinterpret_cast<float4*>(ex + ((grp * 4 + qtr) * 4 + i) * 1024 + lane * 16) =
+                make_float4(s[4 * i],s[4 * i + 1],s[4 * i + 2],s[4 * i + 3]);
+        attn_sync_lds();  // partials visible; every wave is past its K reads
+        if (kt + 1 < tiles) issue_k(kt + 1);
+        v16f t;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 p = lds_read<float4>(ex + ((grp * 4 + w) * 4 + i) * 1024 + lane * 16);
+                if (w == 0) {
+                    t[4 * i] = p.x; t[4 * i + 1] = p.y; t[4 * i + 2] = p.z; t[4 * i + 3] = p.w;
+                } else {
+                    t[4 * i] += p.x; t[4 * i + 1] += p.y; t[4 * i + 2] += p.z; t[4 * i + 3] += p.w;
+                }
+            }
+        uint32_t ph[2][4], pl[2][4];
+        softmax(t,kt * kWK,ph,pl);
+        if (kt + 1 < tiles) attn_wait_vmcnt<PER_WAVE>();  // this wave's V^T DMAs of kt (K of kt + 1 may still run)
+        else attn_wait_vmcnt<0>();
+        attn_sync_lds();  // V^T of kt visible
+        pv(ph,pl);
+    }
+    l_run += __shfl_xor(l_run,32);
+    attn_wait_vmcnt<0>();
+
+    if (!live) return;
+    float* row = a.out + (size_t)q * a.channels + (size_t)head * a.dim;
+    const bool vec = (a.dim & 3) == 0;
+#pragma unroll
+    for (int td = 0; td < TD; td++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int d0 = qtr * DQ + 32 * td + 8 * g + 4 * hh;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = o[td][4 * g + i] / l_run;
+            if (vec && d0 + 4 <= a.dim) {
+                *reinterpret_cast<float4*>(row + d0) = make_float4(v[0],v[1],v[2],v[3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (d0 + i < a.dim) row[d0 + i] = v[i];
+            }
+        }
+}
+
 // ---------------------------------------------------------------- host side
 
 static int attn_cus()
@@ -529,7 +795,7 @@ static size_t aru(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
 int attention_dim_pad(size_t dim)
 {
-    return dim == 0? 0 : dim <= 64? 64 : dim <= 128? 128 : 0;
+    return dim == 0? 0 : dim <= 64? 64 : dim <= 128? 128 : dim <= 256? 256 : dim <= 384? 384 : dim <= 512? 512 : 0;
 }
 
 size_t attention_workspace_bytes(size_t rows, size_t keys, size_t heads, size_t kv_heads, size_t dim)
@@ -539,8 +805,9 @@ size_t attention_workspace_bytes(size_t rows, size_t keys, size_t heads, size_t 
     (void)rows;
     (void)heads;
     const size_t kv = kv_heads * aru(keys,kAK) * D;
-    // K and V^T planes + the key-split pieces (at most one per CU)
-    return 4 * kv * sizeof(uint16_t) + (size_t)attn_cus() * kAQ * (D + 4) * sizeof(float);
+    // K and V^T planes + the key-split pieces of the narrow kernel (at most
+    // one per CU)
+    return 4 * kv * sizeof(uint16_t) + (D <= 128? (size_t)attn_cus() * kAQ * (D + 4) * sizeof(float) : 0);
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, size_t rows, size_t keys, size_t heads,
@@ -587,6 +854,17 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
         a.qe = (int)r.query_end;
         a.key_end = (int)r.key_end;
         a.causal = r.causal? 1 : 0;
+        if (D > 128) {
+            a.tiles_q = (int)((r.query_end - r.query_begin + kWQ - 1) / kWQ);
+            a.full = (int)heads * a.tiles_q;
+            const dim3 grid((unsigned)a.full);
+            if (D == 512) attn_wide_kernel<128><<<grid,dim3(kAThreads),0,s>>>(a);
+            else if (D == 384) attn_wide_kernel<96><<<grid,dim3(kAThreads),0,s>>>(a);
+            else attn_wide_kernel<64><<<grid,dim3(kAThreads),0,s>>>(a);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            continue;
+        }
         a.tiles_q = (int)((r.query_end - r.query_begin + kAQ - 1) / kAQ);
         // One workgroup per CU at a time: when the last round of (head, query
         // tile) units would leave at least half of the CUs idle, its units

@@ -149,7 +149,7 @@ bool hip_rope(float* tensor, size_t rows, size_t channels, size_t heads, const f
 // k, v [keys][channels / heads * kv_heads], on the active session's stream.
 // The ranges form takes the reference's PixAttentionRange fields as
 // pixhip_attention_range.  False (with pixhip_last_error) on what the backend
-// does not take (head sizes above 128) or rejects, as vulkan_attention returns
+// does not take (head sizes above 512) or rejects, as vulkan_attention returns
 // an empty tensor.
 bool hip_attention(const float* q, size_t rows, const float* k, const float* v, size_t keys, size_t heads, size_t kv_heads,
                    size_t channels, bool causal, float* output);

@@ -19,7 +19,8 @@ Fixtures (numpy .npz, data only):
                         tensor_rope (split and interleaved halves)
   g9_attention.npz      tensor_attention, causal form and ranges form: MHA and
                         grouped heads, head sizes 64 / 72 / 128, causal and
-                        not, ranges with a query offset
+                        not, ranges with a query offset; wide heads 200 / 384 /
+                        512
   g10_tensor_ops.npz    tensor_l2norm, tensor_groupnorm (group widths 4, 2, 3),
                         cpu_decode of every type (fp16 specials, random
                         blocks), tensor_gather / tensor_scatter (repeated rows),
@@ -161,6 +162,9 @@ G9_CASES = [
     (64, 64, 2, 2, 128, 1, None, 0),
     (30, 48, 4, 2, 64, 0, [(0, 7, 9, 1), (7, 30, 48, 0)], 5),
     (20, 20, 3, 1, 128, 0, [(0, 12, 12, 0), (12, 20, 20, 1)], 0),
+    (24, 40, 1, 1, 512, 0, None, 0),          # the VAE's single wide head
+    (25, 25, 2, 1, 384, 1, None, 0),
+    (16, 24, 2, 2, 200, 0, [(0, 6, 11, 1), (6, 16, 24, 0)], 4),
 ]
 
 

@@ -7,7 +7,9 @@ The kernel computes the two products with three bf16 MFMA terms per fp32
 product and an online fp32 softmax, so results are held to TOL = 1e-4 of each
 output row's largest magnitude (max |y - r| / max |r| per row).  At the DiT
 shape (30 heads of 128, 4608 tokens) the oracle runs on a sample of query rows
-(non-causal rows are independent of each other).  Size-independent properties
+(non-causal rows are independent of each other), and so at the VAE mid-block
+shapes (one head of 512 over 16384 tokens, one of 384 over 4096: the wide-head
+kernel, head sizes 129..512).  Size-independent properties
 at full size: V of ones gives ones, a key permutation leaves non-causal
 outputs unchanged, and repeats are bit-identical.
 """
@@ -85,6 +87,61 @@ def test_against_oracle(sess, rows, keys, heads, kvh, dim, causal):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("rows,keys,heads,kvh,dim,causal", [
+    (300, 300, 2, 1, 512, True),      # head size 512, grouped, causal
+    (130, 257, 3, 3, 384, False),     # head size 384, ragged key tile
+    (97, 97, 4, 2, 256, True),        # head size 256
+    (64, 200, 2, 2, 129, False),      # head size 129: padded to 256, scalar stores
+    (33, 40, 1, 1, 508, False),       # head size 508: rows not of 8 values
+    (1, 65, 1, 1, 320, False),        # one query row
+])
+def test_wide_heads_against_oracle(sess, rows, keys, heads, kvh, dim, causal):
+    rng = np.random.default_rng(rows * 13 + dim)
+    q, k, v = qkv(rng, rows, keys, heads, kvh, dim, qscale=0.6)
+    print(f"rows={rows} keys={keys} heads={heads}/{kvh} dim={dim} causal={causal}", flush=True)
+    y = gpu_attention(sess, q, k, v, heads, kvh, causal)
+    ref = attention(oracle(), "orc", q, k, v, heads, kvh, causal=causal)
+    err = row_rel_error(y, ref).max()
+    print(f"  rel={err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_wide_head_ranges(sess):
+    """Head size 384 under the ranges form: a causal prefix, full rows and a
+    key-limited block, with a query offset."""
+    rng = np.random.default_rng(384)
+    rows, keys, heads, dim, offset = 200, 260, 2, 384, 40
+    q, k, v = qkv(rng, rows, keys, heads, heads, dim, qscale=0.6)
+    ranges = [(0, 50, 260, 1), (50, 150, 260, 0), (150, 200, 77, 0)]
+    y = gpu_attention(sess, q, k, v, heads, heads, ranges=ranges, query_offset=offset)
+    ref = attention(oracle(), "orc", q, k, v, heads, heads, ranges, offset)
+    err = row_rel_error(y, ref).max()
+    print(f"rel={err:.2e}", flush=True)
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("tokens,dim", [(16384, 512), (4096, 384)])
+def test_vae_mid_block_sampled(sess, tokens, dim):
+    """The VAE mid-block attention: one head of 512 channels over the 128 x 128
+    latent (Z-Image, src/inference.cpp:485) and one of 384 (Qwen-Image,
+    src/qwen_vae.cpp:97, here at 64 x 64); inputs of a GroupNorm'd scale.  The
+    oracle on 32 query rows spread over the image; V of ones gives ones and a
+    repeat is bit-identical at full size."""
+    rng = np.random.default_rng(tokens + dim)
+    q, k, v = qkv(rng, tokens, tokens, 1, 1, dim, qscale=0.6)
+    print(f"tokens={tokens} dim={dim}", flush=True)
+    y = gpu_attention(sess, q, k, v, 1, 1)
+    pick = np.linspace(0, tokens - 1, 32).astype(int)
+    ref = attention(oracle(), "orc", q[pick], k, v, 1, 1)
+    err = row_rel_error(y[pick], ref).max()
+    print(f"  sampled rel={err:.2e}", flush=True)
+    assert err <= TOL
+    y2 = gpu_attention(sess, q, k, v, 1, 1)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32)), "repeats differ"
+    ones = gpu_attention(sess, q, k, np.ones_like(v), 1, 1)
+    assert np.abs(ones - 1.0).max() <= 1e-5
+
+
 def test_ranges_with_query_offset(sess):
     """The Qwen-Image layout: a causal text prefix, then image rows seeing every
     key, then rows limited to a key prefix, with a query offset (KV cache)."""
@@ -154,7 +211,7 @@ def test_errors(sess):
     assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 3, 1, 128, ob.ptr) == arg          # channels not of heads
     assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 2, 3, 128, ob.ptr) == arg          # heads not of kv_heads
     assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 7, 2, 2, 128, ob.ptr, True) == arg    # causal, rows > keys
-    assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 1, 1, 128 * 2, ob.ptr) == _lib.ERR_UNSUPPORTED  # head size 256
+    assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 1, 1, 128 * 5, ob.ptr) == _lib.ERR_UNSUPPORTED  # head size 640
     for bad in ([(0, 3, 8, 0)], [(1, 8, 8, 0)], [(0, 8, 0, 0)], [(0, 8, 9, 0)], [(0, 4, 8, 0), (5, 8, 8, 0)]):
         assert sess.attention(qb.ptr, 8, kb.ptr, vb.ptr, 8, 2, 2, 128, ob.ptr, ranges=bad) == arg, bad
     for b in (qb, kb, vb, ob):

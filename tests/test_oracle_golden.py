@@ -167,7 +167,8 @@ def g9_cases():
 
 def test_attention_matches_reference_vectors():
     """tensor_attention (src/tensor.cpp:347-427): both forms, grouped heads,
-    head sizes 64 / 72 / 128, ranges with a query offset; bit-exact."""
+    head sizes 64 / 72 / 128 / 200 / 384 / 512, ranges with a query offset;
+    bit-exact."""
     o = oracle()
     for c, q, k, v, heads, kvh, causal, ranges, offset, y in g9_cases():
         got = attention(o, "orc", q, k, v, heads, kvh, ranges, offset, causal=bool(causal))
