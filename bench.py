@@ -16,7 +16,8 @@ linear of a Z-Image DiT block at M = 4608 and of a Qwen-Image edit block at
 M = 8448, each linear and the block back to back), the same step with host
 (pinned) operands staged over PCIe, self-attention at the DiT block's shape
 (30 heads of 128 over 4608 tokens) and the VAE mid-block's (one head of 512
-over 16384 tokens), the rest of the op surface (`surface`:
+over 16384 tokens), one whole Z-Image DiT block through the C ABI (`block`:
+4608 tokens, per-op times and shares), the rest of the op surface (`surface`:
 norms, layouts and row moves at the models' shapes, against the HBM peak), VAE
 convolutions (`conv`, against the bf16 MFMA peak), and the reference CPU path
 (cpu_quant_matmul, tensor_attention) timed on this host on the same inputs.
@@ -444,6 +445,85 @@ def cpu_attention(cpu, rec, data):
     log(f"CPU {key}: {sec * 1e3:.0f} ms (scaled); GPU vs CPU rel err {err:.2e}")
 
 
+BLOCK_CAPTION, BLOCK_IMAGE, BLOCK_PATCH_WIDTH = 512, 4096, 64  # the DiT's joint sequence: caption rows, then a 64 x 64 grid
+
+
+def bench_block(sess, synth, _lib, reps):
+    """One Z-Image DiT block (z_block, src/inference.cpp:293-345) through the C
+    ABI (pixelina_amd/zimage.py) at 4608 tokens with its timestep modulation:
+    the whole block back to back, then each of its ops alone (in block order,
+    so every op finds the state its predecessor leaves) for per-op shares.
+    Linears Q5_K except FFN-down and the modulation Q8_0 (HIP quantizer),
+    weights from stream 1338 in the order qkv, out, w1, w3, w2, modulation;
+    x and the timestep from stream 1337; norm weights 1 + N(0, 0.1) and the
+    modulation bias N(0, 0.1) from stream 1339."""
+    from pixelina_amd import Q5_K, Q8_0, zimage
+
+    rows = BLOCK_CAPTION + BLOCK_IMAGE
+    lin, at = {}, 0
+    for key in ("qkv", "out", "w1", "w3", "w2", "modulation"):
+        inner, n = zimage.ZBlockWeights.SHAPES[key]
+        wf = synth.normal(synth.SEED_WEIGHTS, (n, inner), std=0.02, start=at)
+        at += n * inner + (n * inner) % 2
+        if key in ("w2", "modulation"):
+            wdev, qdev = sess.to_device(wf), sess.alloc(n * inner // 32 * 34)
+            _lib.check(sess.quantize_q8_0(wdev.ptr, qdev.ptr, n, inner), "quantize weights")
+            lin[key] = (qdev.download(np.uint8, n * inner // 32 * 34).reshape(n, -1), Q8_0)
+            wdev.free()
+            qdev.free()
+        else:
+            lin[key] = (synth.pack_q5_K(wf), Q5_K)
+        del wf
+    vec, vt = {}, 0
+    for key, n in (("attention_norm1", zimage.HIDDEN), ("attention_norm2", zimage.HIDDEN), ("ffn_norm1", zimage.HIDDEN),
+                   ("ffn_norm2", zimage.HIDDEN), ("q_norm", zimage.HEAD_DIM), ("k_norm", zimage.HEAD_DIM),
+                   ("modulation_bias", 4 * zimage.HIDDEN)):
+        g = synth.normal(synth.SEED_OUTLIERS, (n,), std=0.1, start=vt)
+        vt += n + n % 2
+        vec[key] = g if key == "modulation_bias" else 1.0 + g
+    x = synth.normal(synth.SEED_ACTIVATIONS, (rows, zimage.HIDDEN))
+    t = synth.normal(synth.SEED_ACTIVATIONS, (1, zimage.TIME_DIM), start=x.size)
+    cc, cs = zimage.rotary(BLOCK_CAPTION, 0, 0, False)
+    ic, iS = zimage.rotary(BLOCK_IMAGE, BLOCK_CAPTION, BLOCK_PATCH_WIDTH, True)
+    wts = zimage.ZBlockWeights(sess, "bench:zblock", lin, vec)
+    blk = zimage.ZBlock(sess, wts, rows)
+    xb, tb = sess.to_device(x), sess.to_device(t)
+    cb, sb = sess.to_device(np.concatenate([cc, ic])), sess.to_device(np.concatenate([cs, iS]))
+    ops = blk.ops(xb.ptr, cb.ptr, sb.ptr, tb.ptr)
+
+    def run():
+        for _, fn in ops:
+            fn()
+
+    block_ms, n = timed_series(sess, run, max(3, reps // 10))
+    per = {}
+    for name, fn in ops:
+        ms, k = timed_series(sess, fn, max(5, reps // 5), floor_ms=5.0)
+        per[name] = ms
+    total = sum(per.values())
+    gemm_ops = {"modulation": 2.0 * zimage.TIME_DIM * 4 * zimage.HIDDEN,
+                "qkv": 2.0 * rows * zimage.HIDDEN * 3 * zimage.HIDDEN, "out": 2.0 * rows * zimage.HIDDEN ** 2,
+                "w1": 2.0 * rows * zimage.HIDDEN * zimage.INTERMEDIATE, "w3": 2.0 * rows * zimage.HIDDEN * zimage.INTERMEDIATE,
+                "w2": 2.0 * rows * zimage.INTERMEDIATE * zimage.HIDDEN}
+    attn_flops = 4.0 * zimage.HEADS * rows * rows * zimage.HEAD_DIM
+    for b in (xb, tb, cb, sb):
+        b.free()
+    blk.free()
+    wts.free()
+    rec = {"workload": f"Z-Image DiT block (z_block) at {rows} tokens ({BLOCK_CAPTION} caption + {BLOCK_IMAGE} image), "
+                       f"hidden {zimage.HIDDEN}, {zimage.HEADS} heads of {zimage.HEAD_DIM}, timestep-modulated; "
+                       "Q5_K linears, Q8_0 FFN-down and modulation",
+           "us": round(block_ms * 1e3, 2), "reps": n, "sum_of_ops_us": round(total * 1e3, 2),
+           "linear_int8_tops": round(sum(gemm_ops.values()) / (block_ms * 1e-3) / 1e12, 2),
+           "attention_tflops": round(attn_flops / (per["attention"] * 1e-3) / 1e12, 2),
+           "ops": {k: {"us": round(v * 1e3, 2), "share": round(v / total, 4)} for k, v in per.items()},
+           "note": "each op timed alone in block order; shares of the sum of the ops; ops that enqueue several launches "
+                   "(split: 3 row copies, head_norm and rope: q and k) are one entry"}
+    log(f"block {rows} tokens: {block_ms * 1e3:.1f} us (sum of ops {total * 1e3:.1f} us); "
+        + ", ".join(f"{k} {v * 1e3:.0f}" for k, v in per.items()))
+    return rec
+
+
 # The rest of the op surface at the models' shapes: (name, workload text).
 # Every case rotates over enough buffer copies (>= 1 GiB) that the 256 MB
 # Infinity Cache cannot serve a repeat, and is priced by its algorithmic HBM
@@ -569,6 +649,7 @@ def main():
     ap.add_argument("--no-attention", action="store_true", help="skip the DiT- and VAE-shape attention")
     ap.add_argument("--no-surface", action="store_true", help="skip the norms, layouts and row moves")
     ap.add_argument("--no-conv", action="store_true", help="skip the VAE convolutions")
+    ap.add_argument("--no-block", action="store_true", help="skip the whole DiT block")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one plain 512 MiB device copy (the calibration kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -644,6 +725,7 @@ def main():
         attention = {} if args.no_attention else {sh[0]: bench_attention(sess, synth, _lib, args.steps, sh) for sh in ATTN_SHAPES}
         surface = None if args.no_surface else bench_surface(sess, synth, _lib)
         conv = None if args.no_conv else bench_conv(sess, synth, _lib)
+        block = None if args.no_block else bench_block(sess, synth, _lib, args.steps)
         if args.calibrate_copy:
             src, dst = sess.alloc(COPY_BYTES), sess.alloc(COPY_BYTES)
             sess.copy_device(dst.ptr, src.ptr, COPY_BYTES)
@@ -699,6 +781,8 @@ def main():
         line["surface"] = surface
     if conv:
         line["conv"] = conv
+    if block:
+        line["block"] = block
     if workloads:
         line["workloads"] = workloads
     if pcie:
