@@ -305,6 +305,82 @@ def bench_pcie(sess, _lib, w, x, reps=10):
             "h2d_bytes": nx, "d2h_bytes": ny, "clock": f"host perf_counter, median of {reps} synchronous calls"}
 
 
+def bench_pcie_ops(sess, synth, _lib, reps=5):
+    """One VAE convolution (3x3, 256 x 256 pixels, 512 -> 512 channels) and the
+    DiT attention (30 heads of 128, 4608 tokens) with every tensor in pinned
+    host memory, as HipAllocator hands PixTensorVals to the backend, against
+    the same call on device-resident tensors; both timed on the host clock
+    around the call and a synchronisation (median of `reps`)."""
+    hip = sess.lib
+    hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+    hip.hipHostFree.argtypes = [ctypes.c_void_p]
+    pinned = []
+
+    def host(a):
+        p = ctypes.c_void_p()
+        if hip.hipHostMalloc(ctypes.byref(p), a.nbytes, 0):
+            raise RuntimeError("hipHostMalloc failed")
+        pinned.append(p)
+        ctypes.memmove(p, a.ctypes.data, a.nbytes)
+        return p.value
+
+    def clock(fn):
+        fn()
+        sess.synchronize()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            sess.synchronize()
+            ts.append(time.perf_counter() - t)
+        return float(np.median(ts))
+
+    out = {}
+    try:
+        wd, ht, cin, cout, k = CONV_CASES[0]
+        w = (synth.normal(synth.SEED_WEIGHTS, (cout, cin * k * k)) / np.float32(np.sqrt(cin * k * k))).astype(np.float16)
+        h = sess.conv_weight(f"bench:conv:{wd}:{cin}:{cout}", w.view(np.uint8), 1, k, k, cin, cout)
+        x = np.resize(synth.normal(synth.SEED_ACTIVATIONS, (1 << 20,)), (wd * ht, cin))
+        b = synth.normal(synth.SEED_OUTLIERS, (cout,))
+        y = np.zeros((wd * ht, cout), np.float32)
+        hx, hb, hy = host(x), host(b), host(y)
+        xb, bb, yb = sess.to_device(x), sess.to_device(b), sess.alloc(y.nbytes)
+        t_host = clock(lambda: _lib.check(sess.conv2d(h, hx, wd, ht, hy, None, hb), "conv2d (pinned)"))
+        t_dev = clock(lambda: _lib.check(sess.conv2d(h, xb.ptr, wd, ht, yb.ptr, None, bb.ptr), "conv2d"))
+        for bf in (xb, bb, yb):
+            bf.free()
+        moved = x.nbytes + y.nbytes + b.nbytes
+        out["conv"] = {"workload": f"VAE conv {k}x{k}, {wd}x{ht} pixels, {cin} -> {cout} channels, input, bias and output "
+                                   "in pinned host memory",
+                       "us": round(t_host * 1e6, 1), "device_resident_us": round(t_dev * 1e6, 1), "pcie_bytes": moved,
+                       "gbs_over_pcie": round(moved / (t_host - t_dev) / 1e9, 1) if t_host > t_dev else None}
+        log(f"pinned-host conv: {t_host * 1e6:.0f} us (device-resident {t_dev * 1e6:.0f} us)")
+
+        rows, heads, dim = 4608, 30, 128
+        ch = heads * dim
+        q = synth.normal(synth.SEED_ACTIVATIONS, (rows, ch))
+        kk = synth.normal(synth.SEED_WEIGHTS, (rows, ch))
+        v = synth.normal(synth.SEED_OUTLIERS, (rows, ch))
+        hq, hk, hv, ho = host(q), host(kk), host(v), host(np.zeros_like(q))
+        qb, kb, vb, ob = sess.to_device(q), sess.to_device(kk), sess.to_device(v), sess.alloc(q.nbytes)
+        t_host = clock(lambda: _lib.check(sess.attention(hq, rows, hk, hv, rows, heads, heads, ch, ho), "attention (pinned)"))
+        t_dev = clock(lambda: _lib.check(sess.attention(qb.ptr, rows, kb.ptr, vb.ptr, rows, heads, heads, ch, ob.ptr), "attention"))
+        for bf in (qb, kb, vb, ob):
+            bf.free()
+        moved = 4 * q.nbytes
+        out["attention"] = {"workload": f"self-attention, {heads} heads of {dim}, {rows} tokens, q, k, v and the output in "
+                                        "pinned host memory",
+                            "us": round(t_host * 1e6, 1), "device_resident_us": round(t_dev * 1e6, 1), "pcie_bytes": moved,
+                            "gbs_over_pcie": round(moved / (t_host - t_dev) / 1e9, 1) if t_host > t_dev else None}
+        log(f"pinned-host attention: {t_host * 1e6:.0f} us (device-resident {t_dev * 1e6:.0f} us)")
+    finally:
+        for p in pinned:
+            hip.hipHostFree(p)
+    for v in out.values():
+        v["clock"] = f"host perf_counter around the call and a synchronisation, median of {reps}"
+    return out
+
+
 def bench_fused(sess, synth, _lib, Q5_K, Q8_0, reps):
     """The producers of a linear layer's input fused with its quantizer, at the
     DiT block's shapes, each against the same work done unfused (the producer
@@ -688,6 +764,7 @@ def main():
         pcie = None if args.no_pcie else bench_pcie(sess, _lib, w, x)
         if pcie:
             log(f"host operands (PCIe-inclusive): {pcie['us']:.0f} us per step")
+            pcie = {"headline": pcie, **bench_pcie_ops(sess, synth, _lib)}
         types = {"Q5_K": Q5_K, "Q8_0": Q8_0}
         workloads, keep = ({}, {}) if args.no_blocks else bench_workloads(sess, synth, _lib, types, args.steps)
         gguf_bytes, resident_bytes = sess.residency()

@@ -470,22 +470,28 @@ int check_span(pixhip_session* s, const void* p, size_t bytes)
 // managed) and mapped pinned host memory are passed to the kernel as they
 // are; pageable host memory, which a kernel must not dereference, is copied to
 // a device block first (returned in *staged, freed by the caller after the
-// launch: the pool reuses it only for work queued after this op).
-int read_operand(pixhip_session* s, const void* p, size_t bytes, const void** dev, void** staged)
+// launch: the pool reuses it only for work queued after this op).  With
+// `stage_pinned`, pinned host memory is copied too (for kernels that read
+// their input more than once).
+int read_operand(pixhip_session* s, const void* p, size_t bytes, const void** dev, void** staged, bool stage_pinned = false)
 {
     *staged = nullptr;
     if (int rc = check_span(s,p,bytes)) return rc;
     if (device_visible(s,p,dev)) return PIXHIP_OK;
     hipPointerAttribute_t attr;
-    if (hipPointerGetAttributes(&attr,p) == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer) {
+    const bool pinned = hipPointerGetAttributes(&attr,p) == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer;
+    if (!pinned) (void)hipGetLastError();
+    if (pinned && !stage_pinned) {
         *dev = attr.devicePointer;
         return PIXHIP_OK;
     }
-    (void)hipGetLastError();
     void* block = pixhip_allocate(s,bytes);
     if (!block) return fail(PIXHIP_ERR_MEMORY,"staging of a host operand failed");
     hipError_t e = hipMemcpyAsync(block,p,bytes,hipMemcpyHostToDevice,s->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);  // the host buffer may change after return
+    // Pageable memory may change after return, so its copy completes first;
+    // pinned memory is the caller's until the next synchronisation, as when
+    // the kernels read it in place.
+    if (e == hipSuccess && !pinned) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) {
         pixhip_free(s,block);
         return hip_fail(e,"staging of a host operand");
@@ -1381,10 +1387,10 @@ struct Staged {
     {
         for (void* b : blocks) pixhip_free(s,b);
     }
-    int read(const void* p, size_t bytes, const void** dev)
+    int read(const void* p, size_t bytes, const void** dev, bool stage_pinned = false)
     {
         void* staged = nullptr;
-        const int rc = read_operand(s,p,bytes,dev,&staged);
+        const int rc = read_operand(s,p,bytes,dev,&staged,stage_pinned);
         if (staged) blocks.push_back(staged);
         return rc;
     }
@@ -1852,7 +1858,9 @@ int pixhip_conv2d(pixhip_session* s, const pixhip_weight* wc, const float* input
     if ((rc = write_operand(s,output,out_bytes,&out))) return rc;
     Staged st(s);
     const void *in = nullptr, *b = nullptr;
-    if ((rc = st.read(input,in_bytes,&in))) return rc;
+    // The kernel reads each input pixel once per kernel tap: pinned host input
+    // is copied to HBM once rather than re-read over PCIe.
+    if ((rc = st.read(input,in_bytes,&in,true))) return rc;
     if (bias && (rc = st.read(bias,w->rows * sizeof(float),&b))) return rc;
     pixhip::ConvArgs a{};
     a.x = static_cast<const float*>(in);

@@ -11,12 +11,12 @@
 // other slots zero): both scales are fp16 values, so every product is exact in
 // fp32, and the vector ALU is left with one convert and one FMA per element
 // and block.  That epilogue, not the matrix core, bounds this kernel: per
-// block a wave runs 4 i8 and 4 fp16 MFMAs (192 cycles) and 128 vector
-// instructions (512 cycles).
+// block a wave runs 2 i8 and 2 fp16 MFMAs (96 cycles) and 64 vector
+// instructions (256 cycles).
 //
-// Tiling: a workgroup of 8 waves (2 per SIMD) owns a 256 (tokens) x 128
-// (features) tile; wave w owns the 64 x 64 block at tokens 64*(w%4), features
-// 64*(w/4): two token tiles x two feature tiles of 32 x 32.
+// Tiling: a workgroup of 16 waves (4 per SIMD) owns a 256 (tokens) x 128
+// (features) tile; wave w owns the 64 x 32 block at tokens 64*(w%4), features
+// 32*(w/4): two token tiles of 32 x 32.
 //
 // Data movement: K advances in 64-value stages (two blocks), loaded with
 // buffer_load_dwordx4 ... lds (HBM -> LDS, no registers) into a 4-stage ring.
@@ -156,7 +156,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks)
     return xcd < r? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
-// DMA of stage c into `sa` / `sw`: chunk wave + 8*q of the 32 is this wave's
+// DMA of stage c into `sa` / `sw`: chunk wave + 16*q of the 32 is this wave's
 // q-th.  Chunks 0..15 are activation rows (16 rows of 64 B each), 16..23 the
 // weight rows, 24 and 25 the activation scales of blocks 2c and 2c+1, 26 the
 // weight scales of both blocks; 27..31 load nothing.  Lane l fetches chunk row
@@ -299,6 +299,131 @@ __device__ __forceinline__ void step(const GemmArgs& g, const Ctx& x, int c, Acc
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// The main loop's per-lane constants, computed once: every per-stage LDS
+// address is one of these plus an immediate (the loop is unrolled over the
+// ring slots), and every DMA source offset is one of these plus a
+// wave-uniform scalar offset, so the loop spends no vector instructions on
+// addresses.
+constexpr int kZero = 16 * 704;  // a zeroed word range in every W slot (past the scales)
+struct Lanes {
+    uint32_t ra[2], rw[2];  // operand reads of k-step s: this lane's A row piece (ring 0) and W row piece (from kWRing)
+    uint32_t sx, sw;        // block scales: xd of this lane's token row / wd of its feature (lanes 32..63: a zero word)
+    uint32_t d0, d1;        // source offsets of this wave's two DMAs of a stage
+};
+
+__device__ __forceinline__ Lanes lanes_of(const GemmArgs& g, const Ctx& x)
+{
+    Lanes L;
+    const uint32_t ln = lane_now(), lr = ln & 31, hi = ln >> 5;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const uint32_t cp = lr * 64 + 16 * ((2 * s + hi) ^ ((lr >> 2) & 3));
+        L.ra[s] = (uint32_t)(x.wm * 64 * 64) + cp;
+        L.rw[s] = (uint32_t)(kWRing + x.wn * kWN * 64) + cp;
+    }
+    L.sx = kWRing + (hi? kZero : 16 * kSlotXd80 + (x.wm * 64 + lr) * 4);
+    L.sw = kWRing + (hi? kZero : 16 * kSlotWd80 + (x.wn * kWN + lr) * 4);
+    const uint32_t rows = (ln >> 2) * (uint32_t)x.K + 16u * ((ln & 3) ^ ((ln >> 4) & 3));
+    L.d0 = rows;  // chunk x.wave < 16: activation rows
+    const int c1 = x.wave + kWaves;
+    L.d1 = c1 < 24? rows : c1 < 26? 16u * ln : c1 == 26? 16u * lr + hi * 4u * (uint32_t)g.Npad : 0u;
+    return L;
+}
+
+// DMA of stage c into ring slot SLOT (the chunk map of issue_stage).
+template <int SLOT>
+__device__ __forceinline__ void issue_slot(const GemmArgs& g, const Ctx& x, const Lanes& L, int c, uint8_t* lds)
+{
+    const uint32_t k0 = (uint32_t)c * kKC;
+    uint8_t* sa = lds + SLOT * kHalfBytes;
+    uint8_t* sw = lds + kWRing + SLOT * kHalfBytes;
+    const int c0 = x.wave, c1 = x.wave + kWaves;
+    dma(x.rx,sa + c0 * kChunk,L.d0,(uint32_t)(x.m0 + c0 * 16) * x.K + k0);
+    if (c1 < 24) dma(x.rwq,sw + (c1 - 16) * kChunk,L.d1,(uint32_t)(x.n0 + (c1 - 16) * 16) * x.K + k0);
+    else if (c1 < 26) dma(x.rxd,sw + (c1 - 16) * kChunk,L.d1,(uint32_t)((2 * c + c1 - 24) * g.Mpad + x.m0) * 4u);
+    else if (c1 == 26) dma(x.rwd,sw + (c1 - 16) * kChunk,L.d1,(uint32_t)(2 * c * g.Npad + x.n0) * 4u);
+    else dma(x.rnull,lds + kStages * kStageBytes,0,0);
+}
+
+// {fp16(v), 0, 0, 0}: the scale in K slot 0 of an fp16 MFMA operand (v is an
+// fp16 value, so the round-toward-zero conversion is exact; lanes 32..63 read
+// the zero word).
+__device__ __forceinline__ v4h scale_operand(float v)
+{
+    const auto h = __builtin_amdgcn_cvt_pkrtz(v,0.0f);
+    return v4h{(_Float16)h[0],(_Float16)h[1],(_Float16)0.0f,(_Float16)0.0f};
+}
+
+// One stage from ring slot SLOT: the product order of step() (the MFMAs of
+// product t+1 before the update of product t), the DMA of stage c + kDist into
+// slot (SLOT + kDist) % kStages after the second product.
+template <int SLOT>
+__device__ __forceinline__ void stage_slot(const GemmArgs& g, const Ctx& x, const Lanes& L, int c, Acc& acc, uint8_t* lds)
+{
+    const v16i izero = {};
+    const v16f fzero = {};
+    v4i a[2][2], w[2][kNJ];
+    v4h xa[2][2], wb[2][kNJ];
+    auto load = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) a[s][i] = *reinterpret_cast<const v4i*>(lds + L.ra[s] + SLOT * kHalfBytes + i * 2048);
+#pragma unroll
+        for (int j = 0; j < kNJ; j++) w[s][j] = *reinterpret_cast<const v4i*>(lds + L.rw[s] + SLOT * kHalfBytes + j * 2048);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            xa[s][i] = scale_operand(*reinterpret_cast<const float*>(lds + L.sx + SLOT * kHalfBytes + (s * kBM + i * 32) * 4));
+#pragma unroll
+        for (int j = 0; j < kNJ; j++)
+            wb[s][j] = scale_operand(*reinterpret_cast<const float*>(lds + L.sw + SLOT * kHalfBytes + (s * kBN + j * 32) * 4));
+    };
+    constexpr int T = 2 * 2 * kNJ;
+    v16i p[2];
+    v16f cs[2];
+    auto epi = [&](int t) {
+        const int i = (t / kNJ) & 1, j = t % kNJ;
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc.y[i][j][r] = __builtin_fmaf(cs[t & 1][r],(float)p[t & 1][r],acc.y[i][j][r]);
+        pin(acc.y[i][j]);
+    };
+    load(0);
+    p[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][0],w[0][0],izero,0,0,0);
+    cs[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(xa[0][0],wb[0][0],fzero,0,0,0);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int u = t + 1, s = u / (2 * kNJ), i = (u / kNJ) & 1, j = u % kNJ;
+        __builtin_amdgcn_sched_barrier(0);
+        if (u < T) {
+            p[u & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s][i],w[s][j],izero,0,0,0);
+            pin(p[u & 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (t == 1 && c + kDist < x.nchunks) issue_slot<(SLOT + kDist) % kStages>(g,x,L,c + kDist,lds);
+        __builtin_amdgcn_sched_barrier(0);
+        epi(t);
+        __builtin_amdgcn_sched_barrier(0);
+        if (u < T) {
+            cs[u & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(xa[s][i],wb[s][j],fzero,0,0,0);
+            pin(cs[u & 1]);
+        }
+        if (t == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            load(1);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Stage c (slot SLOT) of the main loop: wait for its DMAs, barrier, compute.
+template <int SLOT>
+__device__ __forceinline__ void loop_stage(const GemmArgs& g, const Ctx& x, const Lanes& L, int c, Acc& acc, uint8_t* lds)
+{
+    if (c + kDist - 1 < x.nchunks) wait_vmcnt<(kDist - 1) * kPerWave>();
+    else wait_vmcnt<0>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    stage_slot<SLOT>(g,x,L,c,acc,lds);
+}
+
 template <bool SUMS>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
 {
@@ -344,21 +469,39 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
         for (int j = 0; j < kNJ; j++) acc.y[i][j] = v16f{};
 
     const int C0 = x.c_begin, C = x.nchunks;
-    for (int c = C0; c < C0 + kDist; c++)
-        if (c < C) issue_stage(g,x,c,lds + (c % kStages) * kHalfBytes,lds + kWRing + (c % kStages) * kHalfBytes,discard);
-
-    // Stage c has landed once only the DMAs issued in the kDist-1 iterations
-    // before c may still be in flight (the prologue counts as iterations
-    // -kDist..-1).  The last kDist-1 iterations issue fewer, so they drain.
-    // (The integer-sum debug variant also stores inside the loop; stores share
-    // vmcnt and may retire early, so it drains everything.)
-    for (int c = C0; c < C; c++) {
-        if (c + kDist - 1 < C && !SUMS) wait_vmcnt<(kDist - 1) * kPerWave>();
-        else wait_vmcnt<0>();
-        wait_lgkm0();
-        __builtin_amdgcn_s_barrier();
-        const int sd = (c + kDist) % kStages, sc = c % kStages;
-        step<SUMS>(g,x,c,acc,lds + sd * kHalfBytes,lds + kWRing + sd * kHalfBytes,discard,lds + sc * kHalfBytes);
+    if constexpr (SUMS) {
+        for (int c = C0; c < C0 + kDist; c++)
+            if (c < C) issue_stage(g,x,c,lds + (c % kStages) * kHalfBytes,lds + kWRing + (c % kStages) * kHalfBytes,discard);
+        // (The integer-sum debug variant also stores inside the loop; stores
+        // share vmcnt and may retire early, so it drains everything.)
+        for (int c = C0; c < C; c++) {
+            wait_vmcnt<0>();
+            wait_lgkm0();
+            __builtin_amdgcn_s_barrier();
+            const int sd = (c + kDist) % kStages, sc = c % kStages;
+            step<SUMS>(g,x,c,acc,lds + sd * kHalfBytes,lds + kWRing + sd * kHalfBytes,discard,lds + sc * kHalfBytes);
+        }
+    } else {
+        // Stage c sits in ring slot (c - C0) % kStages.  The scale operands of
+        // lanes 32..63 read the zero word range of each W slot, which no DMA
+        // writes: clear it once (ordered before the first reads by the first
+        // barrier).
+        const Lanes L = lanes_of(g,x);
+        for (int i = (int)threadIdx.x; i < kStages * 320; i += kThreads)
+            *reinterpret_cast<uint32_t*>(lds + kWRing + (i / 320) * kHalfBytes + kZero + (i % 320) * 4) = 0u;
+        if (C0 < C) issue_slot<0>(g,x,L,C0,lds);
+        if (C0 + 1 < C) issue_slot<1>(g,x,L,C0 + 1,lds);
+        if (C0 + 2 < C) issue_slot<2>(g,x,L,C0 + 2,lds);
+        static_assert(kStages == 4 && kDist == 3, "the prologue and the unrolled loop assume a 4-slot ring");
+        // Stage c has landed once only the DMAs issued in the kDist-1 stages
+        // before c may still be in flight; the last kDist-1 stages issue
+        // fewer, so they drain.
+        for (int c = C0; c < C; c += kStages) {
+            loop_stage<0>(g,x,L,c,acc,lds);
+            if (c + 1 < C) loop_stage<1>(g,x,L,c + 1,acc,lds);
+            if (c + 2 < C) loop_stage<2>(g,x,L,c + 2,acc,lds);
+            if (c + 3 < C) loop_stage<3>(g,x,L,c + 3,acc,lds);
+        }
     }
 
     if (!SUMS && (int)blockIdx.x >= g.full_tiles) {
