@@ -562,7 +562,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g)
 // group issues three of the twelve DMAs.
 constexpr int kSBM = 64, kSBN = 64, kSGroups = 4, kSWaves = 16, kSThreads = 64 * kSWaves;
 constexpr int kSSlots = 4, kSDist = kSSlots - 1;
-constexpr int kSXd = 8 * kChunk, kSWd = kSXd + 2 * 256, kSSlotBytes = kSWd + 2 * 256;
+// kSZero: 512 zeroed bytes after the scales, read by lanes 32..63 as their
+// (zero) scale operand slots.
+constexpr int kSXd = 8 * kChunk, kSWd = kSXd + 2 * 256, kSZero = kSWd + 2 * 256, kSSlotBytes = kSZero + 512;
 constexpr int kSChunks = 12, kSGroupBytes = kSSlots * kSSlotBytes;
 constexpr int kSPerWave = 3;
 constexpr int kSRedBytes = (kSGroups - 1) * 4 * 32 * 32 * 4;  // groups 1..3: four 32 x 32 fp32 blocks each
@@ -575,50 +577,60 @@ struct SmallCtx {
     Rsrc rx, rxd, rwq, rwd;
 };
 
-__device__ __forceinline__ void small_issue(const SmallCtx& x, int c, uint8_t* slot)
+// Per-lane constants of the K-grouped loop (as Lanes for the 256 x 128 form):
+// operand and scale reads relative to the group's ring, DMA source offsets.
+struct SmallLanes {
+    uint32_t ra[2], rw[2], sx, sw;
+    uint32_t d_rows, d_scale;
+};
+
+__device__ __forceinline__ SmallLanes small_lanes(const SmallCtx& x, uint32_t ring)
 {
-    const uint32_t k0 = (uint32_t)c * kKC;
+    SmallLanes L;
+    const uint32_t ln = lane_now(), lr = ln & 31, hi = ln >> 5;
 #pragma unroll
-    for (int i = 0; i < kSPerWave; i++) {
-        const int chunk = x.q + 4 * i;  // wave-uniform
-        const uint32_t lane = lane_now();
-        if (chunk < 8) {
-            const uint32_t vo = (lane >> 2) * (uint32_t)x.K + 16u * ((lane & 3) ^ ((lane >> 4) & 3));
-            if (chunk < 4) dma(x.rx,slot + chunk * kChunk,vo,(uint32_t)(x.m0 + chunk * 16) * x.K + k0);
-            else dma(x.rwq,slot + chunk * kChunk,vo,(uint32_t)(x.n0 + (chunk - 4) * 16) * x.K + k0);
-        } else if (chunk < 10) {
-            const int b = chunk - 8;
-            dma4(x.rxd,slot + kSXd + 256 * b,4u * lane,(uint32_t)((2 * c + b) * x.Mpad + x.m0) * 4u);
-        } else {
-            const int b = chunk - 10;
-            dma4(x.rwd,slot + kSWd + 256 * b,4u * lane,(uint32_t)((2 * c + b) * x.Npad + x.n0) * 4u);
-        }
+    for (int s = 0; s < 2; s++) {
+        const uint32_t piece = 16 * ((2 * s + hi) ^ ((lr >> 2) & 3));
+        L.ra[s] = ring + (x.wm * 32 + lr) * 64 + piece;
+        L.rw[s] = ring + 4 * kChunk + (x.wn * 32 + lr) * 64 + piece;
     }
+    L.sx = ring + (hi? kSZero : kSXd + (x.wm * 32 + lr) * 4);
+    L.sw = ring + (hi? kSZero : kSWd + (x.wn * 32 + lr) * 4);
+    L.d_rows = (ln >> 2) * (uint32_t)x.K + 16u * ((ln & 3) ^ ((ln >> 4) & 3));
+    L.d_scale = 4u * ln;
+    return L;
 }
 
-// One stage from `slot`: two blocks, each an i8 MFMA and the fp16 scale outer
-// product, then y += cs * P; the DMA of stage c + kSDist goes out after the
-// MFMAs.
-__device__ __forceinline__ void small_stage(const SmallCtx& x, int c, v16f& acc, const uint8_t* __restrict__ slot,
-                                            uint8_t* __restrict__ dma_slot)
+// DMA of stage c into ring slot SLOT: wave q of a group issues chunks q (an
+// activation row block), q + 4 (a weight row block) and q + 8 (the scales of
+// block 2c + q for q < 2, else the weight scales of block 2c + q - 2).
+template <int SLOT>
+__device__ __forceinline__ void small_issue(const SmallCtx& x, const SmallLanes& L, int c, uint8_t* ring)
+{
+    const uint32_t k0 = (uint32_t)c * kKC;
+    uint8_t* slot = ring + SLOT * kSSlotBytes;
+    dma(x.rx,slot + x.q * kChunk,L.d_rows,(uint32_t)(x.m0 + x.q * 16) * x.K + k0);
+    dma(x.rwq,slot + (x.q + 4) * kChunk,L.d_rows,(uint32_t)(x.n0 + x.q * 16) * x.K + k0);
+    if (x.q < 2) dma4(x.rxd,slot + kSXd + 256 * x.q,L.d_scale,(uint32_t)((2 * c + x.q) * x.Mpad + x.m0) * 4u);
+    else dma4(x.rwd,slot + kSWd + 256 * (x.q - 2),L.d_scale,(uint32_t)((2 * c + x.q - 2) * x.Npad + x.n0) * 4u);
+}
+
+// One stage from ring slot SLOT: two blocks, each an i8 MFMA and the fp16 scale
+// outer product, then y += cs * P; the DMA of stage c + kSDist goes out after
+// the MFMAs.
+template <int SLOT>
+__device__ __forceinline__ void small_stage(const SmallCtx& x, const SmallLanes& L, int c, v16f& acc, uint8_t* lds, uint8_t* ring)
 {
     const v16i izero = {};
     const v16f fzero = {};
-    const uint32_t ln = lane_now(), lr = ln & 31;
-    const bool k0 = ln < 32;
-    const _Float16 z = (_Float16)0.0f;
-    const float* sxd = reinterpret_cast<const float*>(slot + kSXd);
-    const float* swd = reinterpret_cast<const float*>(slot + kSWd);
     v4i a[2], w[2];
     v4h xa[2], wb[2];
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-        const uint32_t piece = 16 * ((2 * s + (ln >> 5)) ^ ((lr >> 2) & 3));
-        a[s] = *reinterpret_cast<const v4i*>(slot + (x.wm * 32 + lr) * 64 + piece);
-        w[s] = *reinterpret_cast<const v4i*>(slot + 4 * kChunk + (x.wn * 32 + lr) * 64 + piece);
-        const float xv = sxd[s * kSBM + x.wm * 32 + lr], wv = swd[s * kSBN + x.wn * 32 + lr];
-        xa[s] = v4h{(_Float16)(k0? xv : 0.0f),z,z,z};
-        wb[s] = v4h{(_Float16)(k0? wv : 0.0f),z,z,z};
+        a[s] = *reinterpret_cast<const v4i*>(lds + L.ra[s] + SLOT * kSSlotBytes);
+        w[s] = *reinterpret_cast<const v4i*>(lds + L.rw[s] + SLOT * kSSlotBytes);
+        xa[s] = scale_operand(*reinterpret_cast<const float*>(lds + L.sx + SLOT * kSSlotBytes + s * kSBM * 4));
+        wb[s] = scale_operand(*reinterpret_cast<const float*>(lds + L.sw + SLOT * kSSlotBytes + s * kSBN * 4));
     }
     v16i p[2];
     v16f cs[2];
@@ -628,13 +640,24 @@ __device__ __forceinline__ void small_stage(const SmallCtx& x, int c, v16f& acc,
         cs[s] = __builtin_amdgcn_mfma_f32_32x32x8f16(xa[s],wb[s],fzero,0,0,0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (c + kSDist < x.end) small_issue(x,c + kSDist,dma_slot);
+    if (c + kSDist < x.end) small_issue<(SLOT + kSDist) % kSSlots>(x,L,c + kSDist,ring);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[r] = __builtin_fmaf(cs[s][r],(float)p[s][r],acc[r]);
     pin(acc);
+}
+
+template <int SLOT>
+__device__ __forceinline__ void small_loop_stage(const SmallCtx& x, const SmallLanes& L, int c, v16f& acc, uint8_t* lds,
+                                                 uint8_t* ring)
+{
+    if (c + kSDist - 1 < x.end) wait_vmcnt<(kSDist - 1) * kSPerWave>();
+    else wait_vmcnt<0>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    if (c < x.end) small_stage<SLOT>(x,L,c,acc,lds,ring);
 }
 
 __global__ __launch_bounds__(kSThreads, 1) void gemm_small_kernel(GemmArgs g)
@@ -665,20 +688,26 @@ __global__ __launch_bounds__(kSThreads, 1) void gemm_small_kernel(GemmArgs g)
         x.rwd = make_rsrc(g.wdT,nblk * np * 4);
     }
     uint8_t* const ring = lds + grp * kSGroupBytes;
+    const SmallLanes L = small_lanes(x,(uint32_t)(grp * kSGroupBytes));
+    // The zero bytes after each slot's scales (lanes 32..63's scale reads),
+    // which no DMA writes; the first barrier orders this before the reads.
+    for (int i = (int)threadIdx.x; i < kSGroups * kSSlots * 128; i += kSThreads)
+        *reinterpret_cast<uint32_t*>(lds + (i / 128) * kSSlotBytes + kSZero + (i % 128) * 4) = 0u;
 
     v16f acc = {};
-    for (int j = 0; j < kSDist; j++)
-        if (x.begin + j < x.end) small_issue(x,x.begin + j,ring + j * kSSlotBytes);
+    static_assert(kSSlots == 4 && kSDist == 3, "the prologue and the unrolled loop assume a 4-slot ring");
+    if (x.begin < x.end) small_issue<0>(x,L,x.begin,ring);
+    if (x.begin + 1 < x.end) small_issue<1>(x,L,x.begin + 1,ring);
+    if (x.begin + 2 < x.end) small_issue<2>(x,L,x.begin + 2,ring);
     // Every wave runs Cg iterations (one barrier each); a group past its
-    // range idles through them.  Stage c has landed once at most the DMAs of
-    // stage c+1 are in flight.
-    for (int i = 0; i < Cg; i++) {
+    // range idles through them.  Stage c (slot (c - begin) % 4) has landed
+    // once at most the DMAs of stage c+1 are in flight.
+    for (int i = 0; i < Cg; i += kSSlots) {
         const int c = x.begin + i;
-        if (c + kSDist - 1 < x.end) wait_vmcnt<(kSDist - 1) * kSPerWave>();
-        else wait_vmcnt<0>();
-        wait_lgkm0();
-        __builtin_amdgcn_s_barrier();
-        if (c < x.end) small_stage(x,c,acc,ring + (i % kSSlots) * kSSlotBytes,ring + ((i + kSDist) % kSSlots) * kSSlotBytes);
+        small_loop_stage<0>(x,L,c,acc,lds,ring);
+        if (i + 1 < Cg) small_loop_stage<1>(x,L,c + 1,acc,lds,ring);
+        if (i + 2 < Cg) small_loop_stage<2>(x,L,c + 2,acc,lds,ring);
+        if (i + 3 < Cg) small_loop_stage<3>(x,L,c + 3,acc,lds,ring);
     }
     wait_vmcnt<0>();
     wait_lgkm0();
