@@ -58,6 +58,8 @@ WORKLOADS = [
     ("qwen_edit_block", 4096 + 4096 + 256, (0.1, 10.0),
      [("qkv", "Q5_K", 3072, 9216), ("out", "Q5_K", 3072, 3072), ("ff_up", "Q5_K", 3072, 12288), ("ff_down", "Q5_K", 12288, 3072)]),
 ]
+# HBM bytes per launch measured for these linears' GEMM kernels (profiles/hbm_traffic.json)
+TRAFFIC_KEYS = {("q8_0_linear", "linear"): "gemm_q8_0_linear", ("dit_block", "w2"): "gemm_q8_0_w2"}
 WORKLOAD_TEXT = {
     "q8_0_linear": "single Q8_0 linear, X[256,3840] W[3840,3840]",
     "dit_block": "Z-Image DiT block linears, M=4608 (4096 image + 512 text), Q5_K except FFN-down Q8_0",
@@ -223,6 +225,8 @@ def bench_workloads(sess, synth, _lib, types, steps):
                          "frac": round(ops / (step_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
                          "gemm_us": round(gemm_ms * 1e3, 2), "gemm_tops": round(ops / (gemm_ms * 1e-3) / 1e12, 2),
                          "gemm_frac": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4), "reps": reps}
+            if (name, lin) in TRAFFIC_KEYS:
+                recs[lin]["traffic"] = measured_traffic(TRAFFIC_KEYS[(name, lin)])
             log(f"  {lin} [{m},{k}]x[{n}] {wtype}: {step_ms * 1e3:.1f} us ({recs[lin]['frac'] * 100:.1f}%), "
                 f"GEMM {gemm_ms * 1e3:.1f} us ({recs[lin]['gemm_frac'] * 100:.1f}%)")
 
