@@ -1,5 +1,6 @@
 """Shared helpers for the GPU parity tests: run the HIP path through the C ABI
 and compare with the oracle under the parity metric."""
+import ctypes
 import hashlib
 
 import numpy as np
@@ -35,3 +36,23 @@ def gpu_matmul(sess, wbytes, wtype, x, rows, key=None, **kw):
 
 def new_session():
     return Session(0)
+
+
+class Pinned:
+    """Pinned host memory from hipHostMalloc (what HipAllocator hands over)."""
+
+    def __init__(self, sess, array):
+        lib = sess.lib
+        lib.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+        lib.hipHostFree.argtypes = [ctypes.c_void_p]
+        self.lib, self.nbytes, self.p = lib, array.nbytes, ctypes.c_void_p()
+        assert lib.hipHostMalloc(ctypes.byref(self.p), self.nbytes, 0) == 0
+        ctypes.memmove(self.p, array.ctypes.data, self.nbytes)
+
+    def read(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        ctypes.memmove(out.ctypes.data, self.p, out.nbytes)
+        return out
+
+    def free(self):
+        self.lib.hipHostFree(self.p)

@@ -18,7 +18,7 @@ import os
 import numpy as np
 import pytest
 
-from gpu_helpers import TOL, row_rel_error
+from gpu_helpers import TOL, Pinned, row_rel_error
 from oracle_lib import attention, oracle
 from pixelina_amd import _lib
 
@@ -201,6 +201,25 @@ def test_large_magnitudes(sess):
     err = row_rel_error(y, ref).max()
     print(f"rel={err:.2e}", flush=True)
     assert err <= TOL
+
+
+def test_pinned_host_operands(sess):
+    """q, k, v and the output in pinned host memory (read and written in place
+    over the bus): bit-identical to the device-resident call."""
+    rng = np.random.default_rng(17)
+    rows, keys, heads, kvh, dim = 130, 150, 4, 2, 64
+    q, k, v = qkv(rng, rows, keys, heads, kvh, dim)
+    ref = gpu_attention(sess, q, k, v, heads, kvh)
+    hq, hk, hv, ho = Pinned(sess, q), Pinned(sess, k), Pinned(sess, v), Pinned(sess, np.zeros_like(q))
+    try:
+        _lib.check(sess.attention(hq.p.value, rows, hk.p.value, hv.p.value, keys, heads, kvh, heads * dim, ho.p.value),
+                   "attention (pinned)")
+        sess.synchronize()
+        y = ho.read(np.float32, q.shape)
+    finally:
+        for p in (hq, hk, hv, ho):
+            p.free()
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
 def test_errors(sess):

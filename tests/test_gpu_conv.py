@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import model_files as mf
-from gpu_helpers import TOL, new_session, row_rel_error
+from gpu_helpers import TOL, Pinned, new_session, row_rel_error
 from oracle_lib import conv2d, conv_out_size, oracle, same_geometry
 from pixelina_amd import _lib
 
@@ -228,6 +228,29 @@ def test_output_past_its_allocation():
         y.free()
     finally:
         s.close()
+
+
+def test_pinned_host_operands(sess):
+    """Input, bias and output in pinned host memory: the input is copied to the
+    device once (the kernel reads each pixel once per tap) and the output is
+    written in place; the result is bit-identical to the device-resident call."""
+    rng = np.random.default_rng(31)
+    wd, ht, cin, cout = 40, 24, 64, 96
+    w = (rng.standard_normal((cout, cin * 9)) / 24).astype(np.float32)
+    raw, _ = weight_bytes(w, F16)
+    x = rng.standard_normal((wd * ht, cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    ref = gpu_conv(sess, "test:pinned", x, wd, ht, raw, F16, 3, 3, cin, cout, bias=b)
+    h = sess.conv_weight("test:pinned", raw, F16, 3, 3, cin, cout)
+    hx, hb, hy = Pinned(sess, x), Pinned(sess, b), Pinned(sess, np.zeros((wd * ht, cout), np.float32))
+    try:
+        _lib.check(sess.conv2d(h, hx.p.value, wd, ht, hy.p.value, None, hb.p.value), "pixhip_conv2d (pinned)")
+        sess.synchronize()
+        y = hy.read(np.float32, (wd * ht, cout))
+    finally:
+        for p in (hx, hb, hy):
+            p.free()
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
 def test_errors(sess):
