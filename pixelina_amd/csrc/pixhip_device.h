@@ -158,6 +158,77 @@ __device__ __forceinline__ void quantize_q8_K_wave(float4 v, int lane, uint32_t&
     d = __fdiv_rn(1.0f,iscale);
 }
 
+// Four Q8_K blocks quantized by one wave, 16 lanes per block, with the
+// semantics of quantize_q8_K_wave.  Lane l works on block l/16 and holds its
+// values 64j + 4(l%16) .. +3 in v[j] (j = 0..3): for each j the block's 16
+// lanes read 256 contiguous bytes.  Outputs: packed[j], the four quantized
+// bytes of v[j]; d, the block scale (the same in the block's 16 lanes);
+// gsum[j], the sum of the block's 16-value group 4j + (l%16)/4 (the same in
+// a lane quad).  Per-block work (the maximum, the sign of its first
+// occurrence, the two divisions) is shared by four blocks per instruction.
+//   The first largest |x| of the block: each lane scans its values in
+//   position order (j, then the four of v[j]) with a strict '>' (NaN never
+//   wins); the block maximum is the unsigned maximum of the lanes' bit
+//   patterns over the 16 lanes; among the lanes whose own maximum equals it,
+//   the earliest (smallest j, then lane) holds the first occurrence, whose
+//   sign it broadcasts.
+__device__ __forceinline__ void quantize_q8_K_x4(const float4 (&v)[4], int lane, uint32_t (&packed)[4], float& d, int (&gsum)[4])
+{
+    const uint32_t lp = (uint32_t)(lane & 15);
+    float M = 0.0f, S = 0.0f;
+    uint32_t J = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float xs[4] = {v[j].x,v[j].y,v[j].z,v[j].w};
+        float m = 0.0f, s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float ax = fabsf(xs[e]);
+            const bool gt = ax > m;
+            m = gt? ax : m;
+            s = gt? xs[e] : s;
+        }
+        const bool gt = m > M;
+        M = gt? m : M;
+        S = gt? s : S;
+        J = gt? (uint32_t)j : J;
+    }
+    uint32_t mb = __float_as_uint(M);
+    mb = max(mb,(uint32_t)dpp_i32<kDppXor1>((int)mb));
+    mb = max(mb,(uint32_t)dpp_i32<kDppXor2>((int)mb));
+    mb = max(mb,(uint32_t)dpp_i32<kDppHalfMirror>((int)mb));
+    mb = max(mb,(uint32_t)dpp_i32<kDppMirror>((int)mb));
+    const float amax = __uint_as_float(mb);
+    const uint32_t own = J * 16 + lp;
+    uint32_t key = M == amax? own : 0xffu;
+    key = min(key,(uint32_t)dpp_i32<kDppXor1>((int)key));
+    key = min(key,(uint32_t)dpp_i32<kDppXor2>((int)key));
+    key = min(key,(uint32_t)dpp_i32<kDppHalfMirror>((int)key));
+    key = min(key,(uint32_t)dpp_i32<kDppMirror>((int)key));
+    uint32_t neg = (own == key && S < 0.0f)? 1u : 0u;
+    neg = max(neg,(uint32_t)dpp_i32<kDppXor1>((int)neg));
+    neg = max(neg,(uint32_t)dpp_i32<kDppXor2>((int)neg));
+    neg = max(neg,(uint32_t)dpp_i32<kDppHalfMirror>((int)neg));
+    neg = max(neg,(uint32_t)dpp_i32<kDppMirror>((int)neg));
+    const bool zero = amax == 0.0f;
+    const float mval = __uint_as_float(mb | (neg << 31));
+    const float iscale = __fdiv_rn(-127.0f,mval);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float xs[4] = {v[j].x,v[j].y,v[j].z,v[j].w};
+        uint32_t t[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) t[e] = (uint32_t)min(nearest_int_fused(iscale,xs[e]),127);
+        const uint32_t p = __builtin_amdgcn_perm(t[1],t[0],0x0c0c0400u) | __builtin_amdgcn_perm(t[3],t[2],0x04000c0cu);
+        packed[j] = zero? 0u : p;
+        int s = __builtin_amdgcn_sdot4((int)packed[j],0x01010101,0,false);
+        s += dpp_i32<kDppXor1>(s);
+        s += dpp_i32<kDppXor2>(s);
+        gsum[j] = s;
+    }
+    d = zero? 0.0f : __fdiv_rn(1.0f,iscale);
+}
+
 // One Q8_0 block (32 values) quantized by 8 lanes holding 4 consecutive values
 // each (the 8-lane group is aligned: lanes 8g..8g+7).  Semantics of
 // quantize_row_q8_0_ref (src/kernels_quant.cpp:120-144): amax = max|x| with

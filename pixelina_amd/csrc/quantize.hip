@@ -4,8 +4,9 @@
 // planar layout the GEMM reads and, when asked, the reference's own block
 // layout (block_q8_0 / block_q8_K) for callers and for the integer parity gate.
 //
-// HBM-bound byte work: one wave per Q8_K block (64 lanes x float4 = 256
-// values), one 8-lane group per Q8_0 block; reads 4 B/value, writes ~1.1 B/value.
+// HBM-bound byte work: 16 lanes per Q8_K block (four blocks per wave, a
+// float4 per lane and block quarter), one 8-lane group per Q8_0 block; reads
+// 4 B/value, writes ~1.1 B/value.
 // A workgroup covers one chunk of a group of consecutive rows (kQuantRows,
 // kQ8KRows).
 #include <algorithm>
@@ -24,45 +25,56 @@ constexpr int kQuantWaves = 8;  // waves per workgroup: 8 measured ~12% faster t
 // row's 8 consecutive chunks per workgroup.
 constexpr int kQuantRows = 16;
 constexpr int kQuantPer = kQuantRows / kQuantWaves;  // rows per wave
-// Q8_K writes one scale per 256 values, so a long grid matters more than its
-// scale runs: one row per wave.  On [4096, 3840]: 15.2 us with 8 rows, 16.1
-// with 16, 16.4 with 32, 15.9 with one row's 8 consecutive blocks.
-constexpr int kQ8KRows = 8;
-constexpr int kQ8KPer = kQ8KRows / kQuantWaves;
+// Q8_K: a wave quantizes one block of four consecutive rows, 16 lanes per
+// row (quantize_q8_K_x4), and a workgroup one block of 4 * kQuantWaves rows:
+// its scales leave as one 128-byte run of dT, its 16-value sums as 32 rows of
+// the tiled bs plane (one 1 KB block), its bytes as whole 64-byte row pieces.
+constexpr int kQ8KRows = 4 * kQuantWaves;
 
-// One wave per (row, block); the workgroup is (row group, block), block fastest.
+// The workgroup is (row group, block), block fastest.
 __global__ __launch_bounds__(64 * kQuantWaves) void quantize_q8_K_kernel(const float* __restrict__ x, size_t rows, size_t inner,
                                                                          size_t mpad, int8_t* __restrict__ qs, float* __restrict__ dT,
                                                                          _Float16* __restrict__ bs, uint8_t* __restrict__ blocks)
 {
     const uint32_t nb = (uint32_t)(inner / PIX_QK);
     const uint32_t group = blockIdx.x / nb, b = blockIdx.x % nb;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t first = (size_t)group * kQ8KRows + wave;
-    float4 v[kQ8KPer];
-    for (int i = 0; i < kQ8KPer; i++) {  // all loads first, from clamped rows
-        const size_t row = first + (size_t)kQuantWaves * i, r = row < rows? row : rows - 1;
-        v[i] = reinterpret_cast<const float4*>(x + r * inner + (size_t)b * PIX_QK)[lane];
-    }
-    for (int i = 0; i < kQ8KPer; i++) {
-        const size_t row = first + (size_t)kQuantWaves * i;
-        if (row >= rows) break;  // whole wave
-        uint32_t packed;
-        float d;
-        int gsum;
-        quantize_q8_K_wave(v[i],lane,packed,d,gsum);
-        if (qs) {
-            *reinterpret_cast<uint32_t*>(qs + tiled_offset(row,(size_t)b * PIX_QK + 4 * lane,inner)) = packed;
-            if (lane == 0) dT[(size_t)b * mpad + row] = d;
-            // group t = lane/4 stored at (t&1)*8 + t/2: even groups first, then odd
-            const int t = lane >> 2;
-            if ((lane & 3) == 0) bs[tiled_bs_index(row,b,(t & 1) * 8 + (t >> 1),inner)] = (_Float16)(float)gsum;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lp = lane & 15;
+    const size_t row = (size_t)group * kQ8KRows + 4 * wave + (lane >> 4);
+    const size_t r = row < rows? row : rows - 1;  // loads from a clamped row
+    const size_t k0 = (size_t)b * PIX_QK + 4 * lp;
+    const float* src = x + r * inner + k0;
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = *reinterpret_cast<const float4*>(src + 64 * j);
+    uint32_t packed[4];
+    float d;
+    int gsum[4];
+    quantize_q8_K_x4(v,lane,packed,d,gsum);
+    if (row >= rows) return;
+    if (qs) {
+        // values k0 + 64j are in consecutive 1 KB pieces of the row group
+        int8_t* q = qs + tiled_offset(row,k0,inner);
+#pragma unroll
+        for (int j = 0; j < 4; j++) *reinterpret_cast<uint32_t*>(q + 1024 * j) = packed[j];
+        if (lp == 0) dT[(size_t)b * mpad + row] = d;
+        // group g = 4j + lp/4 stored at (g&1)*8 + g/2: even groups first, then odd
+        if ((lp & 3) == 0) {
+            _Float16* o = bs + tiled_bs_index(row,b,0,inner);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int g = 4 * j + (lp >> 2);
+                o[(g & 1) * 8 + (g >> 1)] = (_Float16)(float)gsum[j];
+            }
         }
-        if (blocks) {
-            uint8_t* blk = blocks + (row * nb + b) * PIX_Q8_K_BYTES;
-            reinterpret_cast<uint32_t*>(blk + 4)[lane] = packed;
-            if (lane == 0) *reinterpret_cast<float*>(blk) = d;
-            if ((lane & 3) == 0) reinterpret_cast<int16_t*>(blk + 4 + PIX_QK)[lane >> 2] = (int16_t)gsum;
+    }
+    if (blocks) {
+        uint8_t* blk = blocks + (row * nb + b) * PIX_Q8_K_BYTES;
+#pragma unroll
+        for (int j = 0; j < 4; j++) *reinterpret_cast<uint32_t*>(blk + 4 + 64 * j + 4 * lp) = packed[j];
+        if (lp == 0) *reinterpret_cast<float*>(blk) = d;
+        if ((lp & 3) == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) reinterpret_cast<int16_t*>(blk + 4 + PIX_QK)[4 * j + (lp >> 2)] = (int16_t)gsum[j];
         }
     }
 }
