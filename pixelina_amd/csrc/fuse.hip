@@ -13,8 +13,9 @@
 // a row once: one to four waves per token row (two for rows of 2049-4096
 // values: measured 18% faster than one wave of 16 chunks at 3 waves per SIMD,
 // and as fast as four), holding the row in registers (a 256-value chunk per
-// float4 per lane) from the sum of squares to the quantizer.  The gate
-// product is one wave per 256-value chunk.
+// float4 per lane) from the sum of squares to the quantizer; into Q8_K, four
+// chunks at a time are transposed across lanes to the 16-lanes-per-block
+// quantizer.  The gate product is one wave per 256-value chunk.
 #include <type_traits>
 
 #include "pixhip_device.h"
@@ -102,6 +103,65 @@ __device__ __forceinline__ void store_chunk(const FuseArgs& a, size_t row, int c
             q16[0] = (uint16_t)(packed & 0xffffu);
             q16[1] = (uint16_t)(packed >> 16);
             if ((lane & 7) == 0) *reinterpret_cast<uint16_t*>(out) = dh;
+        }
+    }
+}
+
+// Four chunks of a row in the wave layout (v[q], lane l: values 4l..4l+3 of
+// chunk q) moved into the layout of quantize_q8_K_x4 (t[j], lane l: values
+// 64j + 4(l%16) .. +3 of chunk l/16): a transpose of 16-lane rows, two lane
+// swaps per word (permlane32 swaps the upper half of its first operand with
+// the lower half of its second, permlane16 the odd rows of the first with the
+// even rows of the second).
+__device__ __forceinline__ void chunks_to_blocks(const float4 (&v)[4], float4 (&t)[4])
+{
+    auto sw = [](float a0, float a1, float a2, float a3, float& t0, float& t1, float& t2, float& t3) {
+        const auto p02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a0),__float_as_uint(a2),false,false);
+        const auto p13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a1),__float_as_uint(a3),false,false);
+        const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0],p13[0],false,false);
+        const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1],p13[1],false,false);
+        t0 = __uint_as_float(q01[0]);
+        t1 = __uint_as_float(q01[1]);
+        t2 = __uint_as_float(q23[0]);
+        t3 = __uint_as_float(q23[1]);
+    };
+    sw(v[0].x,v[1].x,v[2].x,v[3].x,t[0].x,t[1].x,t[2].x,t[3].x);
+    sw(v[0].y,v[1].y,v[2].y,v[3].y,t[0].y,t[1].y,t[2].y,t[3].y);
+    sw(v[0].z,v[1].z,v[2].z,v[3].z,t[0].z,t[1].z,t[2].z,t[3].z);
+    sw(v[0].w,v[1].w,v[2].w,v[3].w,t[0].w,t[1].w,t[2].w,t[3].w);
+}
+
+// Writes block c of `row` from the lanes of one 16-lane row after
+// quantize_q8_K_x4 (lane l%16 = lp holds the block's values 64j + 4lp .. +3).
+__device__ __forceinline__ void store_q8_K_x4(const FuseArgs& a, size_t row, int c, int lane, const uint32_t (&packed)[4], float d,
+                                              const int (&gsum)[4])
+{
+    const int lp = lane & 15;
+    const size_t K = a.K, k0 = (size_t)c * PIX_QK + 4 * lp, nb = K / PIX_QK;
+    if (a.qs) {
+        // values k0 + 64j are in consecutive 1 KB pieces of the row group
+        int8_t* q = a.qs + tiled_offset(row,k0,K);
+#pragma unroll
+        for (int j = 0; j < 4; j++) *reinterpret_cast<uint32_t*>(q + 1024 * j) = packed[j];
+        if (lp == 0) a.d[(size_t)c * a.mpad + row] = d;
+        if ((lp & 3) == 0) {
+            // group g = 4j + lp/4 at (g&1)*8 + g/2: even groups first, then odd
+            _Float16* o = a.bs + tiled_bs_index(row,(size_t)c,0,K);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int g = 4 * j + (lp >> 2);
+                o[(g & 1) * 8 + (g >> 1)] = (_Float16)(float)gsum[j];
+            }
+        }
+    }
+    if (a.blocks) {
+        uint8_t* blk = a.blocks + (row * nb + c) * PIX_Q8_K_BYTES;
+#pragma unroll
+        for (int j = 0; j < 4; j++) *reinterpret_cast<uint32_t*>(blk + 4 + 64 * j + 4 * lp) = packed[j];
+        if (lp == 0) *reinterpret_cast<float*>(blk) = d;
+        if ((lp & 3) == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) reinterpret_cast<int16_t*>(blk + 4 + PIX_QK)[4 * j + (lp >> 2)] = (int16_t)gsum[j];
         }
     }
 }
@@ -198,7 +258,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs
     }
     if (WPR == 1 && !live) return;
     auto chunk = [&](int j) -> float4 {
-        if constexpr (CACHE > 0) return v[j];
+        if constexpr (CACHE > 0) return v[j < CACHE? j : CACHE - 1];  // (slots past CACHE are never live)
         else return load4(src,K,(size_t)(part + WPR * j) * 256 + 4 * lane);
     };
     const int J = CACHE > 0? CACHE : mine;
@@ -229,36 +289,65 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs
     if (!live) return;  // after the last barrier
     const float inv = (float)(1.0 / sqrt(sq / (double)K + (double)a.eps));
 
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-        if (j < mine) {  // wave-uniform
-            const int c = part + WPR * j;
-            const size_t k0 = (size_t)c * 256 + 4 * lane;
-            float4 y = make_float4(0.f,0.f,0.f,0.f);
-            if (k0 < K) {
-                const float4 t = chunk(j);
-                // weight and 1 + modulation: 1.0 where absent (multiplying by
-                // 1.0 is exact, as the reference's empty weight is)
-                float4 w4, m4;
-                if (staged) {
-                    w4 = vec_lds[k0 / 4];
-                    m4 = vec_lds[K / 4 + k0 / 4];
-                } else {
-                    w4 = a.w? *reinterpret_cast<const float4*>(a.w + k0) : make_float4(1.f,1.f,1.f,1.f);
-                    m4 = a.mod? *reinterpret_cast<const float4*>(a.mod + k0) : make_float4(0.f,0.f,0.f,0.f);
-                    m4 = make_float4(__fadd_rn(1.0f,m4.x),__fadd_rn(1.0f,m4.y),__fadd_rn(1.0f,m4.z),__fadd_rn(1.0f,m4.w));
-                }
-                const float xs[4] = {t.x,t.y,t.z,t.w}, ws[4] = {w4.x,w4.y,w4.z,w4.w}, ms[4] = {m4.x,m4.y,m4.z,m4.w};
-                float ys[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    // (float)(x - 0.0) is x: no double arithmetic without a mean
-                    const float c = CENTERED? (float)((double)xs[e] - mean) : xs[e];
-                    ys[e] = __fmul_rn(__fmul_rn(__fmul_rn(c,inv),ws[e]),ms[e]);
-                }
-                y = make_float4(ys[0],ys[1],ys[2],ys[3]);
+    // y of the wave's chunk j (zeros past the row's end)
+    auto norm_y = [&](int j) -> float4 {
+        const int c = part + WPR * j;
+        const size_t k0 = (size_t)c * 256 + 4 * lane;
+        float4 y = make_float4(0.f,0.f,0.f,0.f);
+        if (k0 < K) {
+            const float4 t = chunk(j);
+            // weight and 1 + modulation: 1.0 where absent (multiplying by
+            // 1.0 is exact, as the reference's empty weight is)
+            float4 w4, m4;
+            if (staged) {
+                w4 = vec_lds[k0 / 4];
+                m4 = vec_lds[K / 4 + k0 / 4];
+            } else {
+                w4 = a.w? *reinterpret_cast<const float4*>(a.w + k0) : make_float4(1.f,1.f,1.f,1.f);
+                m4 = a.mod? *reinterpret_cast<const float4*>(a.mod + k0) : make_float4(0.f,0.f,0.f,0.f);
+                m4 = make_float4(__fadd_rn(1.0f,m4.x),__fadd_rn(1.0f,m4.y),__fadd_rn(1.0f,m4.z),__fadd_rn(1.0f,m4.w));
             }
-            store_chunk<KIND>(a,row,c,lane,y);
+            const float xs[4] = {t.x,t.y,t.z,t.w}, ws[4] = {w4.x,w4.y,w4.z,w4.w}, ms[4] = {m4.x,m4.y,m4.z,m4.w};
+            float ys[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // (float)(x - 0.0) is x: no double arithmetic without a mean
+                const float c = CENTERED? (float)((double)xs[e] - mean) : xs[e];
+                ys[e] = __fmul_rn(__fmul_rn(__fmul_rn(c,inv),ws[e]),ms[e]);
+            }
+            y = make_float4(ys[0],ys[1],ys[2],ys[3]);
+        }
+        return y;
+    };
+    if constexpr (KIND == 1) {
+        // Q8_K: four chunks at a time through quantize_q8_K_x4 (16-lane row
+        // q of the transposed set holds chunk slot j0 + q)
+#pragma unroll
+        for (int j0 = 0; j0 < J; j0 += 4) {
+            float4 yv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int j = j0 + q;
+                yv[q] = make_float4(0.f,0.f,0.f,0.f);
+                if (j < mine) {  // wave-uniform
+                    yv[q] = norm_y(j);
+                    const size_t k0 = (size_t)(part + WPR * j) * 256 + 4 * lane;
+                    if (a.y && k0 < K) *reinterpret_cast<float4*>(a.y + row * K + k0) = yv[q];
+                }
+            }
+            float4 t[4];
+            chunks_to_blocks(yv,t);
+            uint32_t packed[4];
+            float d;
+            int gsum[4];
+            quantize_q8_K_x4(t,lane,packed,d,gsum);
+            const int jb = j0 + (lane >> 4);
+            if (jb < mine) store_q8_K_x4(a,row,part + WPR * jb,lane,packed,d,gsum);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            if (j < mine) store_chunk<KIND>(a,row,part + WPR * j,lane,norm_y(j));  // wave-uniform
         }
     }
 }
