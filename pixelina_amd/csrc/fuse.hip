@@ -352,6 +352,65 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs
     }
 }
 
+// Rows of up to 128 values written in fp32 only (the per-head q / k norm of
+// a DiT block: rows x heads rows of 128): 16 lanes per row, four rows per wave.
+// Lane l holds values 4(l%16) .. +3 and 64 + 4(l%16) .. +3 of row l/16, so
+// each load's 16 lanes read 256 contiguous bytes; the double sums are 16-lane
+// DPP reductions.  Same arithmetic as norm_quantize_kernel.
+template <bool CENTERED>
+__global__ __launch_bounds__(64 * kNormWaves) void norm_small_kernel(FuseArgs a)
+{
+    const int lane = (int)(threadIdx.x & 63), lp = lane & 15;
+    const size_t row = ((size_t)blockIdx.x * kNormWaves + (threadIdx.x >> 6)) * 4 + (size_t)(lane >> 4);
+    const bool live = row < a.rows;
+    const size_t K = a.K;
+    const float* src = a.x + (live? row : a.rows - 1) * K;  // loads from a clamped row
+    float4 v[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) v[h] = load4(src,K,(size_t)(64 * h + 4 * lp));
+    auto row_sum16 = [](double t) {
+        t += dpp_f64<kDppXor1>(t);
+        t += dpp_f64<kDppXor2>(t);
+        t += dpp_f64<kDppHalfMirror>(t);
+        t += dpp_f64<kDppMirror>(t);
+        return t;
+    };
+    double mean = 0.0;
+    if constexpr (CENTERED) {
+        double s = 0.0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) s += ((double)v[h].x + (double)v[h].y) + ((double)v[h].z + (double)v[h].w);
+        mean = row_sum16(s) / (double)K;
+    }
+    double sq = 0.0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        if ((size_t)(64 * h + 4 * lp) < K) {
+            const double e0 = (double)v[h].x - mean, e1 = (double)v[h].y - mean, e2 = (double)v[h].z - mean, e3 = (double)v[h].w - mean;
+            sq += (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+        }
+    }
+    sq = row_sum16(sq);
+    const float inv = (float)(1.0 / sqrt(sq / (double)K + (double)a.eps));
+    if (!live) return;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const size_t k0 = (size_t)(64 * h + 4 * lp);
+        if (k0 >= K) continue;
+        const float4 w4 = a.w? *reinterpret_cast<const float4*>(a.w + k0) : make_float4(1.f,1.f,1.f,1.f);
+        float4 m4 = a.mod? *reinterpret_cast<const float4*>(a.mod + k0) : make_float4(0.f,0.f,0.f,0.f);
+        m4 = make_float4(__fadd_rn(1.0f,m4.x),__fadd_rn(1.0f,m4.y),__fadd_rn(1.0f,m4.z),__fadd_rn(1.0f,m4.w));
+        const float xs[4] = {v[h].x,v[h].y,v[h].z,v[h].w}, ws[4] = {w4.x,w4.y,w4.z,w4.w}, ms[4] = {m4.x,m4.y,m4.z,m4.w};
+        float ys[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float c = CENTERED? (float)((double)xs[e] - mean) : xs[e];
+            ys[e] = __fmul_rn(__fmul_rn(__fmul_rn(c,inv),ws[e]),ms[e]);
+        }
+        *reinterpret_cast<float4*>(a.y + row * K + k0) = make_float4(ys[0],ys[1],ys[2],ys[3]);
+    }
+}
+
 // SiLU of one value as the reference's tensor_silu computes it in fp32:
 // v / (1.0f + expf(-v)).  expf is taken as the fp32 rounding of a double
 // exponential (within 1e-16 relative of e^-v): the correctly rounded value.
@@ -446,6 +505,13 @@ hipError_t launch_norm_quantize(const float* x, size_t rows, size_t K, const flo
     a.mod = modulation;
     a.eps = eps;
     a.centered = centered? 1 : 0;
+    if (kind == 0 && K <= 128 && !a.blocks) {
+        // 16 lanes per row (a one-wave-per-row launch leaves half the lanes idle at 128 values)
+        const size_t grid = (rows + 4 * kNormWaves - 1) / (4 * kNormWaves);
+        if (centered) norm_small_kernel<true><<<dim3((unsigned)grid),dim3(64 * kNormWaves),0,s>>>(a);
+        else norm_small_kernel<false><<<dim3((unsigned)grid),dim3(64 * kNormWaves),0,s>>>(a);
+        return hipGetLastError();
+    }
     if (kind == 1) return launch_norm_kind<1>(a,s);
     if (kind == 2) return launch_norm_kind<2>(a,s);
     return launch_norm_kind<0>(a,s);

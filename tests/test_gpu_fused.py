@@ -149,6 +149,28 @@ def test_norm_type0_normalizes_only(sess, k, centered):
     assert sess.norm_quantize(0, xb.ptr, 5, k) == _lib.ERR_ARGUMENT  # nothing to write
 
 
+@pytest.mark.parametrize("rows,k,centered,weighted,modulated", [
+    (37 * 30, 128, 0, True, False),   # DiT per-head q / k norm: rows x heads rows of 128
+    (33, 128, 1, True, True),
+    (17, 124, 0, False, True),        # past-the-end lanes of the second half
+    (5, 20, 1, True, False),          # one float4 per lane or none
+    (3, 4, 0, True, True),
+])
+def test_norm_short_rows(sess, rows, k, centered, weighted, modulated):
+    """Rows of up to 128 values (16 lanes per row) against the oracle, bit for bit."""
+    rng = np.random.default_rng(rows + k)
+    x = (rng.standard_normal((rows, k)) * rng.choice([1e-3, 1.0, 40.0], (rows, 1)) + 1.5 * centered).astype(np.float32)
+    w = (1.0 + 0.2 * rng.standard_normal(k)).astype(np.float32) if weighted else None
+    mod = (0.3 * rng.standard_normal(k)).astype(np.float32) if modulated else None
+    o = oracle()
+    ref = norm_rows(o, "orc", x, w, 1e-6, centered)
+    if mod is not None:
+        ref = modulate_rows(o, ref, mod)
+    y, blocks = run_norm(sess, 0, x, w, 1e-6, centered, mod)
+    assert blocks is None
+    assert np.array_equal(bits(y), bits(ref)), np.nonzero((bits(y) != bits(ref)).any(axis=1))[0][:8]
+
+
 def test_multiply_after_norm_checks_the_activation_kind(sess):
     rng = np.random.default_rng(4)
     x = rng.standard_normal((8, 512)).astype(np.float32)
