@@ -88,7 +88,14 @@ def test_pointwise_vs_oracle(sess, rows, channels):
         assert close(run_op(sess, name, x), gelu(o, "orc", x, form), x), name
 
 
-@pytest.mark.parametrize("rows,heads,dim,interleaved", [(3, 2, 8, 0), (4608, 30, 128, 0), (257, 16, 64, 1)])
+@pytest.mark.parametrize("rows,heads,dim,interleaved", [
+    (3, 2, 8, 0), (4608, 30, 128, 0), (257, 16, 64, 1),
+    (4608, 30, 128, 1),   # the DiT block's q / k (interleaved pairs, a float4 per thread)
+    (5, 3, 12, 1),        # interleaved, head size a multiple of 4 only
+    (5, 3, 12, 0),        # split halves of 6: the scalar pair kernel
+    (7, 2, 6, 1),         # head size not a multiple of 4: the scalar pair kernel
+    (70001, 1, 8, 1),     # more rows than one grid dimension holds
+])
 def test_rope_vs_oracle(sess, rows, heads, dim, interleaved):
     rng = np.random.default_rng(rows * heads + dim)
     x = rng.standard_normal((rows, heads * dim)).astype(np.float32)
