@@ -45,6 +45,8 @@ constexpr size_t kTileN = PIX_GEMM_NTILE;  // GEMM feature-tile rows (weight pad
 constexpr size_t kTileM = PIX_GEMM_MTILE;  // GEMM token-tile rows (activation padding)
 constexpr size_t kAlign = 256;       // sub-allocation alignment
 constexpr double kHeapFraction = 0.85;  // VULKAN_HEAP_FRACTION, src/backend_vulkan.h:26
+constexpr size_t kPipeChunks = 8;          // row chunks of a matmul on host operands
+constexpr size_t kPipeMinColumns = 2 * kTileM;  // (fewer rows: one staged pass)
 constexpr size_t kMatvecMaxInner = 24576;  // matvec keeps x in LDS and a row in registers (64 units per lane x 6)
 
 bool supported_type(uint32_t t) { return t == PIX_Q8_0 || t == PIX_Q5_K || t == PIX_Q6_K; }
@@ -167,6 +169,9 @@ struct pixhip_session {
     // groupnorm's chunk statistics
     void* gn = nullptr;
     size_t gn_bytes = 0;
+    // matmul on host operands: copy streams (input, output) and the chunks' events
+    hipStream_t pipe_in = nullptr, pipe_out = nullptr;
+    hipEvent_t pipe_ev[2 * kPipeChunks + 1] = {};
     // activations left by the last QUANTIZE stage
     int act_kind = 0;  // 0 none, 1 Q8_K, 2 Q8_0
     size_t act_columns = 0, act_inner = 0;
@@ -615,6 +620,87 @@ int matvec(pixhip_session* s, pixhip_weight* w, const float* x, const pixhip::Ou
     return PIXHIP_OK;
 }
 
+// Quantize + GEMM of a matmul whose input and output are host memory, in row
+// chunks on three streams: chunk c's input is copied to HBM on pipe_in, then
+// quantized and multiplied on the session stream (after that copy's event),
+// then its output copied back on pipe_out (after the GEMM's event).  PCIe
+// carries input chunks in one direction and output chunks in the other at the
+// same time, and each chunk's GEMM runs under the copies of its neighbours.
+// Every chunk starts at a multiple of the GEMM token tile, so its quantized
+// activations are a view of the session's buffers for all rows (which they
+// hold afterwards, as after an unchunked call) and its GEMM reads that view.
+// Taken only when the chunks' GEMMs and the whole one run the same kernel
+// form with no split-K, so every output is the same bits either way.
+size_t pipe_chunk(size_t columns) { return round_up((columns + kPipeChunks - 1) / kPipeChunks,kTileM); }
+
+bool pipeline_ok(const pixhip_weight* w, size_t columns)
+{
+    if (columns < kPipeMinColumns) return false;
+    const size_t N = w->rows, Kr = round_up(w->inner,64), chunk = pipe_chunk(columns);
+    const size_t last = columns - (columns - 1) / chunk * chunk;
+    for (size_t m : {columns,chunk,last})
+        if (pixhip::gemm_split_bytes(m,N,Kr)) return false;
+    if (w->type == PIX_Q8_0) {
+        const bool g = pixhip::gemm_q8_0_grouped(columns,N);
+        if (pixhip::gemm_q8_0_grouped(chunk,N) != g || pixhip::gemm_q8_0_grouped(last,N) != g) return false;
+    }
+    return true;
+}
+
+int run_pipelined(pixhip_session* s, pixhip_weight* w, const float* input, size_t columns, float* output, const float* bias)
+{
+    const size_t K = w->inner, N = w->rows;
+    const int kind = w->type == PIX_Q8_0? 2 : 1;
+    const size_t chunk = pipe_chunk(columns);
+    const size_t chunks = (columns + chunk - 1) / chunk;
+    if (!s->pipe_in) PIX_HIP(hipStreamCreate(&s->pipe_in),"hipStreamCreate");
+    if (!s->pipe_out) PIX_HIP(hipStreamCreate(&s->pipe_out),"hipStreamCreate");
+    for (hipEvent_t& e : s->pipe_ev)
+        if (!e) PIX_HIP(hipEventCreateWithFlags(&e,hipEventDisableTiming),"hipEventCreate");
+    int rc = ensure_gemm_form(s,w);
+    if (rc) return rc;
+    const size_t in_region = round_up(columns * K * sizeof(float),kAlign);
+    if ((rc = grow(s,&s->stage,&s->stage_bytes,in_region + columns * N * sizeof(float)))) return rc;
+    if ((rc = act_buffers(s,kind,columns,K,nullptr))) return rc;
+    float* xs = static_cast<float*>(s->stage);
+    float* ys = reinterpret_cast<float*>(static_cast<uint8_t*>(s->stage) + in_region);
+    // the staging buffers are free once the work already on the session stream is done
+    hipEvent_t start = s->pipe_ev[2 * kPipeChunks];
+    PIX_HIP(hipEventRecord(start,s->stream),"hipEventRecord");
+    PIX_HIP(hipStreamWaitEvent(s->pipe_in,start,0),"hipStreamWaitEvent");
+    for (size_t c = 0; c < chunks; c++) {
+        const size_t r0 = c * chunk, rows = std::min(chunk,columns - r0);
+        hipEvent_t in_done = s->pipe_ev[2 * c], out_ready = s->pipe_ev[2 * c + 1];
+        PIX_HIP(hipMemcpyAsync(xs + r0 * K,input + r0 * K,rows * K * sizeof(float),hipMemcpyHostToDevice,s->pipe_in),"stage input");
+        PIX_HIP(hipEventRecord(in_done,s->pipe_in),"hipEventRecord");
+        PIX_HIP(hipStreamWaitEvent(s->stream,in_done,0),"hipStreamWaitEvent");
+        const pixhip::Output out = {ys + r0 * N,bias,N,0};
+        float* const part = nullptr;  // (no split-K: pipeline_ok)
+        hipError_t e;
+        if (kind == 2) {
+            const size_t kp = round_up(K,64);
+            const pixhip::Act80 a = {s->a80.qs + r0 * kp,s->a80.d + r0,s->a80.mpad};
+            PIX_HIP(pixhip::launch_quantize_q8_0(xs + r0 * K,rows,K,kp,a,nullptr,s->stream),"quantize Q8_0");
+            e = pixhip::launch_gemm_q8_0(a,w->q80,rows,N,K,out,part,s->stream);
+        } else {
+            // tiled planes: rows r0.. (r0 a multiple of 32) start r0*K bytes in, the
+            // 16-value sums r0*K/16 elements in; the scales r0 columns in
+            const pixhip::Act8K a = {s->a8k.qs + r0 * K,s->a8k.d + r0,s->a8k.bs + r0 * (K / 16),s->a8k.mpad};
+            PIX_HIP(pixhip::launch_quantize_q8_K(xs + r0 * K,rows,K,a,nullptr,s->stream),"quantize Q8_K");
+            e = w->type == PIX_Q5_K? pixhip::launch_gemm_q5_K(a,w->q5,rows,N,K,out,part,s->stream)
+                                   : pixhip::launch_gemm_q6_K(a,w->q6,rows,N,K,out,part,s->stream);
+        }
+        PIX_HIP(e,"GEMM launch");
+        PIX_HIP(hipEventRecord(out_ready,s->stream),"hipEventRecord");
+        PIX_HIP(hipStreamWaitEvent(s->pipe_out,out_ready,0),"hipStreamWaitEvent");
+        PIX_HIP(hipMemcpyAsync(output + r0 * N,ys + r0 * N,rows * N * sizeof(float),hipMemcpyDeviceToHost,s->pipe_out),"copy output");
+    }
+    set_act_shape(s,kind,columns,K);
+    // pipe_out waited for the last GEMM, which waited for the last input copy
+    PIX_HIP(hipStreamSynchronize(s->pipe_out),"hipStreamSynchronize");
+    return PIXHIP_OK;
+}
+
 int run(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t columns, float* output, const float* bias,
         size_t ldy, size_t y_offset, unsigned stages, bool allow_host)
 {
@@ -658,6 +744,9 @@ int run(pixhip_session* s, const pixhip_weight* wc, const float* input, size_t c
             yout = const_cast<void*>(yv);
         }
     }
+    if (stage_in && !xin && stage_out && stages == (PIXHIP_STAGE_QUANTIZE | PIXHIP_STAGE_MULTIPLY) && ldy == w->rows && !y_offset &&
+        pipeline_ok(w,columns))
+        return run_pipelined(s,w,input,columns,output,bias);
     const size_t in_region = stage_in? round_up(in_bytes,kAlign) : 0;
     if (stage_in || stage_out) {
         rc = grow(s,&s->stage,&s->stage_bytes,in_region + (stage_out? out_elems * sizeof(float) : 0));
@@ -756,6 +845,10 @@ void pixhip_session_destroy(pixhip_session* s)
     if (s->gn) (void)hipFree(s->gn);
     if (s->t0) (void)hipEventDestroy(s->t0);
     if (s->t1) (void)hipEventDestroy(s->t1);
+    for (hipEvent_t e : s->pipe_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (s->pipe_in) (void)hipStreamDestroy(s->pipe_in);
+    if (s->pipe_out) (void)hipStreamDestroy(s->pipe_out);
     if (s->own_stream) (void)hipStreamDestroy(s->own_stream);
     delete s;
 }

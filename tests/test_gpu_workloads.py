@@ -198,6 +198,37 @@ def test_quant_matmul_host_pointers(sess, m):
     assert row_rel_error(y, quant_matmul(oracle(), "orc", wb, Q5_K, x, n)).max() <= TOL
 
 
+@pytest.mark.parametrize("wtype", [Q5_K, Q6_K, Q8_0])
+def test_host_operands_in_chunks(sess, wtype):
+    """pixhip_matmul with pinned host input and output at a shape that runs in
+    row chunks on three streams (copy in, quantize + GEMM, copy out): the same
+    bits as the device-resident call, the quantized activations of every row
+    left in the session (a MULTIPLY-only call afterwards matches too), and
+    sampled rows against the oracle."""
+    from gpu_helpers import Pinned
+    m, k, n = 4000, 256, 10240  # chunks of 512 rows (the last 416): no split-K either way
+    x = activations(620, m, k)
+    wb = weights(621, n, k, wtype)
+    key = f"wl:chunks:{wtype}"
+    y_dev = run_gpu(sess, key, wb, wtype, x, n)
+    w = sess.weight(key, wb, wtype, k, n)
+    xp, yp = Pinned(sess, x), Pinned(sess, np.full((m, n), np.nan, np.float32))
+    try:
+        _lib.check(sess.matmul(w, xp.p.value, m, yp.p.value), "pixhip_matmul (pinned host operands)")
+        y_host = yp.read(np.float32, (m, n))
+    finally:
+        xp.free()
+        yp.free()
+    assert np.array_equal(y_host.view(np.uint32), y_dev.view(np.uint32))
+    yb = sess.alloc(m * n * 4)
+    _lib.check(sess.matmul_stage(w, None, m, yb.ptr, _lib.STAGE_MULTIPLY), "MULTIPLY after the chunked call")
+    y_again = yb.download(np.float32, m * n).reshape(m, n)
+    yb.free()
+    assert np.array_equal(y_again.view(np.uint32), y_dev.view(np.uint32))
+    rows = np.array([0, 1, 511, 512, 1535, 2047, 3583, 3584, 3999])
+    assert row_rel_error(y_host[rows], quant_matmul(oracle(), "orc", wb, wtype, x[rows], n)).max() <= TOL
+
+
 def test_rejects_what_the_reference_rejects(sess):
     """cpu_quant_matmul returns false for zero sizes, a ragged inner dimension and
     other weight types (src/kernels_quant.cpp:373-375); so does the HIP path, with
