@@ -177,14 +177,24 @@ hipError_t launch_channel_op(int op, float* x, const float* other, const float* 
 // ---- l2norm ---------------------------------------------------------------
 //
 // A row per segment of L lanes (L a power of two, 64 / L rows per wave, four
-// waves per block), so that short rows (the VAE's 96 channels) keep every
-// lane loading:
+// waves per block), so that short rows (the VAE's 96 channels: L = 8) keep
+// every lane loading:
 //   square  = sum of (double)x * x
 //   inverse = (float)(sqrt((double)channels) / max(sqrt(square), (double)eps))
 //   y       = x * inverse * w[c]      (fp32, left to right; w NULL: * 1)
 // Rows of up to kL2Cache units per lane stay in registers between the two
 // passes; longer rows are re-read (from L2, which the first pass filled).
 constexpr int kL2Cache = 8;
+
+// The weights of unit u (VEC of them, one load; 1.0 without a weight vector).
+template <int VEC> __device__ __forceinline__ typename Vec<VEC>::T weights(const float* __restrict__ w, size_t u)
+{
+    typename Vec<VEC>::T t;
+    if (w) return *reinterpret_cast<const typename Vec<VEC>::T*>(w + u * VEC);
+#pragma unroll
+    for (int j = 0; j < VEC; j++) Vec<VEC>::set(t,j,1.0f);
+    return t;
+}
 
 template <int VEC, int L>
 __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
@@ -225,9 +235,10 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x
         for (int k = 0; k < kL2Cache; k++) {
             const size_t u = sl + (size_t)k * L;
             if (u < units) {
+                const T wv = weights<VEC>(w,u);
 #pragma unroll
                 for (int j = 0; j < VEC; j++)
-                    Vec<VEC>::set(v[k],j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v[k],j),inverse),w? w[u * VEC + j] : 1.0f));
+                    Vec<VEC>::set(v[k],j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v[k],j),inverse),Vec<VEC>::get(wv,j)));
                 *reinterpret_cast<T*>(out + u * VEC) = v[k];
             }
         }
@@ -250,9 +261,9 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x
 #pragma unroll 4
     for (size_t u = sl; u < units; u += L) {
         T v = *reinterpret_cast<const T*>(in + u * VEC);
+        const T wv = weights<VEC>(w,u);
 #pragma unroll
-        for (int j = 0; j < VEC; j++)
-            Vec<VEC>::set(v,j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v,j),inverse),w? w[u * VEC + j] : 1.0f));
+        for (int j = 0; j < VEC; j++) Vec<VEC>::set(v,j,__fmul_rn(__fmul_rn(Vec<VEC>::get(v,j),inverse),Vec<VEC>::get(wv,j)));
         *reinterpret_cast<T*>(out + u * VEC) = v;
     }
 }
@@ -260,11 +271,14 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x
 template <int VEC>
 static hipError_t l2norm_launch(const float* x, const float* w, float* y, size_t rows, size_t channels, float eps, hipStream_t s)
 {
-    // lanes per row: all 64 for long rows, else about four units per lane
+    // lanes per row: all 64 for long rows, else about three units per lane
+    // (96 channels: 8 lanes, each load's 8 lanes of a row reading one whole
+    // 128-byte line; with 4 lanes a load read half lines of 16 rows:
+    // 185 -> 145 us at [1M, 96])
     const size_t units = channels / VEC;
     int lanes = 64;
     if (units < 256)
-        for (lanes = 1; lanes * 2 <= 64 && (size_t)lanes * 2 * 4 <= units;) lanes *= 2;
+        for (lanes = 1; lanes * 2 <= 64 && (size_t)lanes * 2 * 3 <= units;) lanes *= 2;
     const size_t per_block = 4 * (64 / lanes), blocks = (rows + per_block - 1) / per_block;
     if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
     const dim3 g((unsigned)blocks), b(256);
@@ -283,7 +297,7 @@ static hipError_t l2norm_launch(const float* x, const float* w, float* y, size_t
 hipError_t launch_l2norm(const float* x, const float* w, float* y, size_t rows, size_t channels, float eps, hipStream_t s)
 {
     if (!rows || !channels) return hipSuccess;
-    if (channels % 4 == 0 && aligned16(x) && aligned16(y)) return l2norm_launch<4>(x,w,y,rows,channels,eps,s);
+    if (channels % 4 == 0 && aligned16(x) && aligned16(y) && (!w || aligned16(w))) return l2norm_launch<4>(x,w,y,rows,channels,eps,s);
     return l2norm_launch<1>(x,w,y,rows,channels,eps,s);
 }
 
