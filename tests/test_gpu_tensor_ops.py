@@ -250,7 +250,7 @@ def test_l2norm_vs_oracle(sess, rows, channels, weighted, eps):
     assert same(y, l2norm(oracle(), "orc", x, w, eps))
 
 
-@pytest.mark.parametrize("rows,channels", [(256 * 256, 512), (128 * 128, 128), (64 * 64, 256), (1000, 96), (50000, 32), (7, 8192)])
+@pytest.mark.parametrize("rows,channels", [(256 * 256, 512), (128 * 128, 128), (64 * 64, 256), (1000, 96), (50000, 32), (7, 8192), (3000, 384)])
 def test_groupnorm_vs_oracle(sess, rows, channels):
     """The VAE's GroupNorm(32) over pixels, up to a 256x256 image of 512
     channels; group widths 1 and 3 take the scalar path."""
