@@ -40,6 +40,14 @@ __device__ __forceinline__ uint4 load_stream(const uint4* p)
     const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(p));
     return make_uint4(t.x,t.y,t.z,t.w);
 }
+// The same for the 12-byte unit records of the Q5_K form (lanes read
+// consecutive 12-byte pieces: 10.0 -> 9.65 us at 18944 x 3584).
+typedef unsigned int u3v __attribute__((ext_vector_type(3)));
+__device__ __forceinline__ uint3 load_stream(const uint3* p)
+{
+    const u3v t = __builtin_nontemporal_load(reinterpret_cast<const u3v*>(p));
+    return make_uint3(t.x,t.y,t.z);
+}
 
 
 constexpr int kMvWaves = 8;
@@ -273,7 +281,7 @@ __device__ __forceinline__ void q5_load(Q5Rows<UPL,R>& f, const PlanarQ5K& w, in
             const uint4* q = reinterpret_cast<const uint4*>(w.qs + (size_t)row * (K / 2));
             f.qs0[rr][k] = load_stream(q + u);
             f.qs1[rr][k] = load_stream(q + units + u);
-            f.rec[rr][k] = *reinterpret_cast<const uint3*>(w.rec + ((size_t)row * units + u) * 3);
+            f.rec[rr][k] = load_stream(reinterpret_cast<const uint3*>(w.rec + ((size_t)row * units + u) * 3));
         }
     }
 }
