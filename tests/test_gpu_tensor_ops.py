@@ -343,6 +343,33 @@ def test_copies_at_model_shape(sess):
     assert same(y, want)
 
 
+def test_outputs_past_the_cache(sess):
+    """The non-temporal store forms, taken when an output exceeds 256 MB: l2norm
+    [1M, 96] (Qwen VAE), groupnorm [1M, 128] and the 2x upsample of 512 x 512 x
+    128, each against the oracle, bit-exact."""
+    rng = np.random.default_rng(97)
+    o = oracle()
+    rows = 1 << 20
+    x = rng.standard_normal((rows, 96), dtype=np.float32)
+    w = (1.0 + 0.2 * rng.standard_normal(96)).astype(np.float32)
+    print("l2norm [1M, 96]", flush=True)
+    y = call_out(sess, x.shape, lambda d, op: _lib.check(sess.l2norm(d.up(x), rows, 96, d.up(w), 1e-12, op), "l2norm"))
+    assert same(y, l2norm(o, "orc", x, w, 1e-12))
+    del x, y
+    x = (rng.standard_normal((rows, 128), dtype=np.float32) * 1.5 + 0.25).astype(np.float32)
+    w = (1.0 + 0.3 * rng.standard_normal(128)).astype(np.float32)
+    b = (0.2 * rng.standard_normal(128)).astype(np.float32)
+    print("groupnorm [1M, 128]", flush=True)
+    y = call_out(sess, x.shape, lambda d, op: _lib.check(sess.groupnorm(d.up(x), rows, 128, d.up(w), d.up(b), op), "groupnorm"))
+    assert same(y, groupnorm(o, "orc", x, w, b))
+    del x, y
+    img = rng.standard_normal((512 * 512, 128), dtype=np.float32)
+    print("upsample [512x512, 128]", flush=True)
+    y = call_out(sess, (4 * 512 * 512, 128), lambda d, op: _lib.check(sess.layout(OP_UPSAMPLE, d.up(img), 512 * 512, 128, op, 4 * 512 * 512,
+                                                                                  128, 512), "upsample"))
+    assert same(y, layout(o, OP_UPSAMPLE, img, 512, 512, 128))
+
+
 def test_layouts_at_model_shape(sess):
     """Z-Image DiT patchify of 128 x 128 latents of 16 channels (patch 2: 4096
     tokens of 64), unpatchify back, and the VAE's 2x upsample of 256 x 256 x 128."""
