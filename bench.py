@@ -9,11 +9,12 @@ Inputs are resident in HBM before timing starts.
 
 Also reported in the same JSON line: the GEMM kernel alone (the roofline
 object, against the int8 MFMA peak), the quantize pass alone, the M=1 decode
-matvec (Q5_K and Q8_0, W [18944, 3584], 100 repeats rotating >= 1 GiB of weight
-copies so the 256 MB Infinity Cache cannot serve them), the other specified
-workloads (`workloads`: a single Q8_0 linear [256, 3840] x [3840, 3840], every
-linear of a Z-Image DiT block at M = 4608 and of a Qwen-Image edit block at
-M = 8448, each linear and the block back to back), the same step with host
+matvec (Q5_K, Q8_0 and Q6_K, W [18944, 3584], 100 repeats rotating >= 1 GiB of
+weight copies so the 256 MB Infinity Cache cannot serve them), the other
+specified workloads (`workloads`: a single Q8_0 linear [256, 3840] x [3840,
+3840], every linear of a Z-Image DiT block at M = 4608 and of a Qwen-Image edit
+block at M = 8448, each linear and the block back to back, and the DiT
+FFN-down with Q6_K weights), the same step with host
 (pinned) operands staged over PCIe, self-attention at the DiT block's shape
 (30 heads of 128 over 4608 tokens) and the VAE mid-block's (one head of 512
 over 16384 tokens), one whole Z-Image DiT block through the C ABI (`block`:
@@ -57,6 +58,7 @@ WORKLOADS = [
                                      ("w3", "Q5_K", 3840, 10240), ("w2", "Q8_0", 10240, 3840)]),
     ("qwen_edit_block", 4096 + 4096 + 256, (0.1, 10.0),
      [("qkv", "Q5_K", 3072, 9216), ("out", "Q5_K", 3072, 3072), ("ff_up", "Q5_K", 3072, 12288), ("ff_down", "Q5_K", 12288, 3072)]),
+    ("q6_K_ffn_down", 4096 + 512, None, [("w2", "Q6_K", 10240, 3840)]),
 ]
 # HBM bytes per launch measured for these linears' GEMM kernels (profiles/hbm_traffic.json)
 TRAFFIC_KEYS = {("q8_0_linear", "linear"): "gemm_q8_0_linear", ("dit_block", "w2"): "gemm_q8_0_w2"}
@@ -64,6 +66,7 @@ WORKLOAD_TEXT = {
     "q8_0_linear": "single Q8_0 linear, X[256,3840] W[3840,3840]",
     "dit_block": "Z-Image DiT block linears, M=4608 (4096 image + 512 text), Q5_K except FFN-down Q8_0",
     "qwen_edit_block": "Qwen-Image edit block linears, M=8448 (2x4096 image + 256 text), Q5_K, per-token scales log-uniform [0.1,10]",
+    "q6_K_ffn_down": "Z-Image DiT FFN-down with Q6_K weights (the type Q5_K_M files give ffn_down), M=4608",
 }
 
 
@@ -174,9 +177,9 @@ def workload_inputs(synth, name, m, row_scale, linears):
     drawn as consecutive pieces of stream 1337 (~N(0,1)); the per-token scales
     (log-uniform, where given) from stream 1339, one piece per activation
     matrix; the weights of the linears, in their listed order, as consecutive
-    pieces of stream 1338 (~N(0, 0.02)).  Q5_K weights are packed here; Q8_0
-    weights are returned as float32 and quantized by the HIP quantizer
-    (bit-exact quantize_row_q8_0_ref)."""
+    pieces of stream 1338 (~N(0, 0.02)).  Q5_K and Q6_K weights are packed
+    here; Q8_0 weights are returned as float32 and quantized by the HIP
+    quantizer (bit-exact quantize_row_q8_0_ref)."""
     xs, at, st = {}, 0, 0
     for k in sorted({k for _, _, k, _ in linears}):
         x = synth.normal(synth.SEED_ACTIVATIONS, (m, k), start=at)
@@ -189,7 +192,7 @@ def workload_inputs(synth, name, m, row_scale, linears):
     for lin, wtype, k, n in linears:
         wf = synth.normal(synth.SEED_WEIGHTS, (n, k), std=0.02, start=wt)
         wt += n * k + (n * k) % 2
-        ws[lin] = synth.pack_q5_K(wf) if wtype == "Q5_K" else wf
+        ws[lin] = synth.pack_q5_K(wf) if wtype == "Q5_K" else synth.pack_q6_K(wf) if wtype == "Q6_K" else wf
     return xs, ws
 
 
@@ -737,7 +740,7 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
-    from pixelina_amd import Q5_K, Q8_0, Session, _lib, synth
+    from pixelina_amd import Q5_K, Q6_K, Q8_0, Session, _lib, synth
 
     x, wb, ch = gemm_workload(synth)
     ops = 2.0 * GEMM_M * GEMM_N * GEMM_K
@@ -769,7 +772,7 @@ def main():
         if pcie:
             log(f"host operands (PCIe-inclusive): {pcie['us']:.0f} us per step")
             pcie = {"headline": pcie, **bench_pcie_ops(sess, synth, _lib)}
-        types = {"Q5_K": Q5_K, "Q8_0": Q8_0}
+        types = {"Q5_K": Q5_K, "Q6_K": Q6_K, "Q8_0": Q8_0}
         workloads, keep = ({}, {}) if args.no_blocks else bench_workloads(sess, synth, _lib, types, args.steps)
         gguf_bytes, resident_bytes = sess.residency()
 
@@ -785,10 +788,11 @@ def main():
             wdev.free()
             qdev.free()
             wq5 = synth.pack_q5_K(wv)
+            wq6 = synth.pack_q6_K(wv)
             del wv
             xvb = sess.to_device(xv)
             yvb = sess.alloc(MV_N * 4)
-            for name, wtype, wbytes in (("q5_K", Q5_K, wq5), ("q8_0", Q8_0, wq8)):
+            for name, wtype, wbytes in (("q5_K", Q5_K, wq5), ("q8_0", Q8_0, wq8), ("q6_K", Q6_K, wq6)):
                 copies = int(np.ceil(MALL_DEFEAT_BYTES / wbytes.nbytes))
                 handles = [sess.weight(f"bench:mv:{name}:{i}", wbytes, wtype, MV_K, MV_N) for i in range(copies)]
                 sess.bench_matmul(handles, xvb.ptr, 1, yvb.ptr, both, copies)
