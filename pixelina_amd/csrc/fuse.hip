@@ -228,7 +228,12 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs
     if constexpr (CACHE > 0) {
         // all of this wave's chunks at once (past `mine` they are zeros)
 #pragma unroll
-        for (int j = 0; j < CACHE; j++) v[j] = load4(src,K,j < mine? (size_t)(part + WPR * j) * 256 + 4 * lane : K);
+        for (int j = 0; j < CACHE; j++) {
+            const size_t k0 = j < mine? (size_t)(part + WPR * j) * 256 + 4 * lane : K - 4;
+            // Q8_K rows are whole chunks and slots past `mine` are never read
+            if constexpr (KIND == 1) v[j] = *reinterpret_cast<const float4*>(src + k0);
+            else v[j] = load4(src,K,j < mine? k0 : K);
+        }
     }
     if (staged) {
         // The workgroup's copy of the vectors, every thread (also of a dead
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs
 #pragma unroll
     for (int j = 0; j < J; j++) {
         const size_t k0 = (size_t)(part + WPR * j) * 256 + 4 * lane;
-        if (j < mine && k0 < K) {
+        if (j < mine && (KIND == 1 || k0 < K)) {
             const float4 t = chunk(j);
             const double e0 = (double)t.x - mean, e1 = (double)t.y - mean, e2 = (double)t.z - mean, e3 = (double)t.w - mean;
             sq += (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs
         const int c = part + WPR * j;
         const size_t k0 = (size_t)c * 256 + 4 * lane;
         float4 y = make_float4(0.f,0.f,0.f,0.f);
-        if (k0 < K) {
+        if (KIND == 1 || k0 < K) {
             const float4 t = chunk(j);
             // weight and 1 + modulation: 1.0 where absent (multiplying by
             // 1.0 is exact, as the reference's empty weight is)
@@ -332,7 +337,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_quantize_kernel(FuseArgs
                 if (j < mine) {  // wave-uniform
                     yv[q] = norm_y(j);
                     const size_t k0 = (size_t)(part + WPR * j) * 256 + 4 * lane;
-                    if (a.y && k0 < K) *reinterpret_cast<float4*>(a.y + row * K + k0) = yv[q];
+                    if (a.y) *reinterpret_cast<float4*>(a.y + row * K + k0) = yv[q];
                 }
             }
             float4 t[4];
