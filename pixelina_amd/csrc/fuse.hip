@@ -428,7 +428,7 @@ __device__ __forceinline__ float silu_ref(float v)
 }
 
 // One wave per 256-value chunk of one row: y = silu(gate) * up.
-template <int KIND>
+template <int KIND, bool FULL>
 __global__ __launch_bounds__(64 * kGateWaves) void silu_gate_quantize_kernel(FuseArgs a)
 {
     // Workgroup = (group of kGateRows rows, chunk), chunk fastest; wave w takes
@@ -445,8 +445,13 @@ __global__ __launch_bounds__(64 * kGateWaves) void silu_gate_quantize_kernel(Fus
     // all loads first, from clamped rows and columns (zeros past K)
     for (int i = 0; i < kPer; i++) {
         const size_t row = first + (size_t)kGateWaves * i, r = row < a.rows? row : a.rows - 1;
-        g[i] = load4(a.x + r * a.K,a.K,k0);
-        u[i] = load4(a.u + r * a.K,a.K,k0);
+        if constexpr (FULL) {  // whole 256-value chunks: no bounds on the loads
+            g[i] = *reinterpret_cast<const float4*>(a.x + r * a.K + k0);
+            u[i] = *reinterpret_cast<const float4*>(a.u + r * a.K + k0);
+        } else {
+            g[i] = load4(a.x + r * a.K,a.K,k0);
+            u[i] = load4(a.u + r * a.K,a.K,k0);
+        }
     }
     for (int i = 0; i < kPer; i++) {
         const size_t row = first + (size_t)kGateWaves * i;
@@ -533,9 +538,13 @@ hipError_t launch_silu_gate_quantize(const float* gate, const float* up, size_t 
     const size_t grid = (rows + kGateRows - 1) / kGateRows * nch;
     if (grid >= ((size_t)1 << 32)) return hipErrorInvalidValue;
     const dim3 g((unsigned)grid), b(64 * kGateWaves);
-    if (kind == 1) silu_gate_quantize_kernel<1><<<g,b,0,s>>>(a);
-    else if (kind == 2) silu_gate_quantize_kernel<2><<<g,b,0,s>>>(a);
-    else silu_gate_quantize_kernel<0><<<g,b,0,s>>>(a);
+    // whole chunks (and, for Q8_0, no planar padding chunk past K)
+    const bool full = K % 256 == 0 && (kind != 2 || a.kpad == K);
+    if (kind == 1) silu_gate_quantize_kernel<1,true><<<g,b,0,s>>>(a);
+    else if (kind == 2 && full) silu_gate_quantize_kernel<2,true><<<g,b,0,s>>>(a);
+    else if (kind == 2) silu_gate_quantize_kernel<2,false><<<g,b,0,s>>>(a);
+    else if (full) silu_gate_quantize_kernel<0,true><<<g,b,0,s>>>(a);
+    else silu_gate_quantize_kernel<0,false><<<g,b,0,s>>>(a);
     return hipGetLastError();
 }
 
